@@ -1,0 +1,90 @@
+// Shared helpers of libhsd: error state, launch checks, bf16/f16 conversion, the
+// XCD-aware workgroup remap. gfx950 (MI355X) only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/hsd.h"
+
+namespace hsd {
+
+// ---------------------------------------------------------------- error state
+// One message per host thread; entry points return a negative code and leave the
+// message here (hsd_last_error).
+int set_error(int code, const char* fmt, ...);
+
+// Checks the launch that was just issued on this thread.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- bf16 / f16
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
+  return __uint_as_float(bits << 16);
+}
+
+// Round to nearest even; every NaN becomes the canonical quiet NaN 0x7FC0.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element loads/stores by dtype tag (HSD_DT_*).
+template <int DT> struct Elem;
+template <> struct Elem<HSD_DT_BF16> {
+  using T = uint16_t;
+  __device__ __forceinline__ static float load(const T* p, size_t i) { return bf16_bits_to_f32(p[i]); }
+  __device__ __forceinline__ static void store(T* p, size_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+};
+template <> struct Elem<HSD_DT_F16> {
+  using T = uint16_t;
+  __device__ __forceinline__ static float load(const T* p, size_t i) { return f16_bits_to_f32(p[i]); }
+  __device__ __forceinline__ static void store(T* p, size_t i, float v) { p[i] = f32_to_f16_bits(v); }
+};
+template <> struct Elem<HSD_DT_F32> {
+  using T = float;
+  __device__ __forceinline__ static float load(const T* p, size_t i) { return p[i]; }
+  __device__ __forceinline__ static void store(T* p, size_t i, float v) { p[i] = v; }
+};
+
+// ---------------------------------------------------------------- XCD remap
+// MI355X dispatches workgroup i of a launch to XCD i % 8 (round robin). This maps a
+// hardware workgroup id to a logical one so that logically consecutive workgroups run
+// on the same XCD and share its L2 (neighbouring 64-byte pieces of one weight row,
+// one tile's column blocks). Bijective for any n.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int q = n / kXcds, r = n % kXcds;
+  const int x = bid % kXcds, i = bid / kXcds;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+// softplus(x) = log(1 + e^x); above 20 it equals x in fp32.
+__device__ __forceinline__ float softplus_f32(float x) {
+  return x > 20.0f ? x : log1pf(expf(x));
+}
+
+// Deterministic butterfly sum over the 64 lanes of a wavefront (same tree on every
+// call, so equal inputs give equal bits).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace hsd

@@ -1,0 +1,67 @@
+"""The C ABI: libhsd.so loads, exports exactly what include/hsd.h declares, and its
+host-side argument checks return the documented error codes (no kernel is launched, so
+these run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from hsd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hsd.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(hsd_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    declared = header_functions()
+    assert len(declared) >= 17
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/hsd.h but not exported"
+    assert set(declared) == set(N.EXPORTS), "the ctypes signature table must cover the header exactly"
+    assert lib.hsd_abi_version() == 1
+
+
+def test_argument_errors_are_reported():
+    lib = N.lib()
+    assert lib.hsd_permute_nibbles(None, None, 1, 8, 1, None) == -1
+    assert b"null" in lib.hsd_last_error()
+    dummy = ctypes.c_void_p(16)
+    assert lib.hsd_permute_nibbles(dummy, dummy, 1, 12, 1, None) == -2          # rows % 8
+    assert b"multiple of 8" in lib.hsd_last_error()
+    args = [dummy, 0, dummy, dummy] + [dummy] * 6 + [dummy, 0]
+    # D not a multiple of 128
+    assert lib.hsd_sparse_down_decode(*args, 1, 200, 1856, 3712, 6, 128, 0, None, None, dummy, 1 << 30, None) == -2
+    # h dtype tag unknown -> checked after shapes and workspace
+    ws = N.lib().hsd_sparse_down_workspace_bytes(1, 2688, 1856, 3712, 6)
+    assert lib.hsd_sparse_down_decode(*args, 1, 2688, 1856, 3712, 6, 128, 0, None, None, dummy, ws - 1, None) == -5
+    assert lib.hsd_mamba_verify(*([dummy, 10304] * 3), *([dummy] * 9), 4, dummy, 0,
+                                3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, dummy, 1 << 20, None) == -2  # N != 128
+    assert lib.hsd_mamba_select_row(dummy, None, 4, 4, None) == -1                 # n_keep >= nslab
+    assert lib.hsd_prefill_gemm(*([dummy] * 13), 0, 512, 2688, 1856, 3712, 6, 128, 48, 240, 3712,
+                                dummy, 1 << 30, None) == -2                          # tt = 48
+
+
+def test_workspace_sizes():
+    lib = N.lib()
+    # 16 parts per token row x D fp32 partials
+    assert lib.hsd_sparse_down_workspace_bytes(1, 2688, 1856, 3712, 6) == 16 * 2688 * 4
+    assert lib.hsd_sparse_down_workspace_bytes(3, 2688, 1856, 3712, 6) == 3 * 16 * 2688 * 4
+    assert lib.hsd_prefill_num_tiles(512, 6, 128, 32) == 240
+    assert lib.hsd_prefill_num_tiles(512, 6, 128, 64) == 184
+    assert lib.hsd_prefill_num_tiles(2048, 6, 128, 32) == 576
+    assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 6) == 512 * 7 * 2688 * 4
+    assert lib.hsd_mamba_workspace_bytes(3, 64, 64) == 3 * 4096 * 4
+
+
+def test_python_layer_refuses_cpu_tensors():
+    import torch
+    with pytest.raises(N.HSDError):
+        N.ptr(torch.zeros(4))

@@ -1,0 +1,121 @@
+"""GPU parity of the sparse decode down projection (hsd/decode.py:37-186) at the
+BASELINE shape (D=2688, F=1856, FS=3712, top-6 of 128 + shared, affine 4-bit g64).
+
+Bars:
+* integer work bit-exact: the canonical live masks equal the oracle's;
+* fp32 output within max|y - ref| <= 1e-5 * max|ref| of the float64 oracle;
+* bf16 output within the north-star bound |y - ref| <= 2e-2 + 1e-2 * |ref|;
+* bit-exact: dense-h control == sparse (skipping exact zeros is exact), and every row
+  of a B-row call == the same row alone (verify rows == single rows).
+"""
+import numpy as np
+import pytest
+import torch
+
+from hsd import decode, layout, synth as S
+from oracle import hsd_oracle as O
+
+pytestmark = pytest.mark.gpu
+D, F, FS, TOPK = 2688, 1856, 3712, 6
+KW = dict(F=F, FS=FS, D=D, topk=TOPK)
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    lay = S.moe_layer_np(7)
+    dv = {k: S.to_device(v, dev) for k, v in lay.items()}
+    pw, ps, pb = layout.to_neuron_major(dv["w"], dv["s"], dv["b"])
+    spw, sps, spb = layout.to_neuron_major(dv["sw"], dv["ss"], dv["sb"])
+    nm_np = O.to_neuron_major(lay["w"], lay["s"], lay["b"]) + O.to_neuron_major(lay["sw"], lay["ss"], lay["sb"])
+    return dict(np=lay, dev=dv, nm=(pw, ps, pb, spw, sps, spb), nm_np=nm_np)
+
+
+def run_case(layer, dev, seed, B, zero_frac, out_dtype=torch.float32, h_dtype=torch.bfloat16, **kw):
+    h, sel, gains = S.decode_inputs_np(seed, B=B, zero_frac=zero_frac)
+    hd = S.to_device(h, dev).to(h_dtype)
+    y = decode.sparse_down(hd, S.to_device(sel, dev), S.to_device(gains, dev), *layer["nm"], out_dtype=out_dtype,
+                           **KW, **kw)
+    return h, sel, gains, hd, y
+
+
+@pytest.mark.parametrize("zero_frac", [0.0, 0.7, 0.9, 0.97, 1.0])
+def test_sparse_down_matches_oracle(layer, dev, zero_frac):
+    h, sel, gains, hd, y = run_case(layer, dev, 11, 1, zero_frac)
+    ref = O.sparse_down(O.bf16_to_f32(h), sel, gains, *layer["nm_np"], **KW)
+    yh = y.cpu().numpy()
+    scale = max(np.abs(ref).max(), 1e-30)
+    print(f"zero_frac {zero_frac}: max|ref| {scale:.3f}  max rel err {np.abs(yh - ref).max() / scale:.2e}")
+    if zero_frac == 1.0:
+        assert np.all(yh == 0.0)
+    else:
+        assert np.abs(yh - ref).max() <= 1e-5 * scale
+
+
+def test_bf16_output_and_textbook_reference(layer, dev):
+    h, sel, gains, hd, y = run_case(layer, dev, 12, 1, 0.9, out_dtype=torch.bfloat16)
+    lay = layer["np"]
+    ref = O.dense_reference(O.bf16_to_f32(h), sel, gains, lay["w"], lay["s"], lay["b"], lay["sw"], lay["ss"],
+                            lay["sb"], **KW)
+    yh = y.float().cpu().numpy()
+    assert np.all(np.abs(yh - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+
+
+def test_live_masks_bit_exact(layer, dev):
+    h, sel, gains = S.decode_inputs_np(13, B=3, zero_frac=0.9)
+    h[0, :64] = 0                                   # an all-dead group
+    h[1, 5] = 0x8000                                # -0.0 is dead
+    h[2, TOPK * F - 1] = S.bf16_bits(2.0)           # last neuron of the last routed slot
+    masks = torch.zeros(3 * (TOPK * F // 64 + FS // 64), dtype=torch.int64, device=dev)
+    decode.sparse_down(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev), *layer["nm"],
+                       live_masks=masks, **KW)
+    want = O.live_masks(O.bf16_to_f32(h), F, FS, TOPK).reshape(-1)
+    assert np.array_equal(masks.cpu().numpy().view(np.uint64), want)
+
+
+@pytest.mark.parametrize("zero_frac", [0.5, 0.9])
+def test_dense_h_control_is_bit_identical(layer, dev, zero_frac):
+    h, sel, gains, hd, y = run_case(layer, dev, 14, 2, zero_frac)
+    yd = decode.sparse_down(hd, S.to_device(sel, dev), S.to_device(gains, dev), *layer["nm"],
+                            out_dtype=torch.float32, dense=True, **KW)
+    assert torch.equal(y, yd)
+
+
+def test_rows_independent_of_batch(layer, dev):
+    h, sel, gains, hd, y3 = run_case(layer, dev, 15, 3, 0.9)
+    for b in range(3):
+        y1 = decode.sparse_down(hd[b:b + 1], S.to_device(sel[b:b + 1], dev), S.to_device(gains[b:b + 1], dev),
+                                *layer["nm"], out_dtype=torch.float32, **KW)
+        assert torch.equal(y1[0], y3[b])
+
+
+@pytest.mark.parametrize("h_dtype", [torch.float32, torch.float16])
+def test_other_activation_dtypes(layer, dev, h_dtype):
+    h, sel, gains, hd, y = run_case(layer, dev, 16, 1, 0.9, h_dtype=h_dtype)
+    hv = hd.float().cpu().numpy()
+    ref = O.sparse_down(hv, sel, gains, *layer["nm_np"], **KW)
+    assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_bad_expert_id_is_flagged_and_skipped(layer, dev):
+    h, sel, gains = S.decode_inputs_np(17, B=1, zero_frac=0.9)
+    bad = sel.copy()
+    bad[0, 2] = 999
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    y = decode.sparse_down(S.to_device(h, dev), S.to_device(bad, dev), S.to_device(gains, dev), *layer["nm"],
+                           out_dtype=torch.float32, status=status, **KW)
+    assert int(status.item()) == 1
+    g0 = gains.copy()
+    g0[0, 2] = 0.0
+    ref = O.sparse_down(O.bf16_to_f32(h), sel, g0, *layer["nm_np"], **KW)
+    assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_dense_stock_comparator(layer, dev):
+    h, sel, gains = S.decode_inputs_np(18, B=2, zero_frac=0.9)
+    dv = layer["dev"]
+    y = decode.dense_down(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev), dv["w"], dv["s"],
+                          dv["b"], dv["sw"], dv["ss"], dv["sb"], out_dtype=torch.float32, **KW)
+    lay = layer["np"]
+    ref = O.dense_reference(O.bf16_to_f32(h), sel, gains, lay["w"], lay["s"], lay["b"], lay["sw"], lay["ss"],
+                            lay["sb"], **KW)
+    assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()

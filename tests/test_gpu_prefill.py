@@ -1,0 +1,67 @@
+"""GPU parity of the prefill path (hsd/prefill.py:48-321): tile order and union lists
+bit-exact against the oracle; the MFMA grouped GEMM against the float64 oracle within
+the north-star bound (bf16 operands, fp32 accumulation): |y - ref| <= 2e-2 + 1e-2*|ref|
+elementwise and max|y - ref| <= 1e-2 * max|ref|."""
+import numpy as np
+import pytest
+import torch
+
+from hsd import layout, prefill, synth as S
+from oracle import hsd_oracle as O
+
+pytestmark = pytest.mark.gpu
+D, F, FS, TOPK, E = 2688, 1856, 3712, 6, 128
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    lay = S.moe_layer_np(21)
+    dv = {k: S.to_device(v, dev) for k, v in lay.items()}
+    nm = layout.to_neuron_major(dv["w"], dv["s"], dv["b"]) + layout.to_neuron_major(dv["sw"], dv["ss"], dv["sb"])
+    nm_np = O.to_neuron_major(lay["w"], lay["s"], lay["b"]) + O.to_neuron_major(lay["sw"], lay["ss"], lay["sb"])
+    return dict(nm=nm, nm_np=nm_np)
+
+
+@pytest.mark.parametrize("T,tt,zipf", [(512, 32, 1.1), (512, 64, 1.1), (37, 32, 1.1), (2048, 32, 1.1), (256, 32, 0)])
+def test_tiles_bit_exact(dev, T, tt, zipf):
+    rng = np.random.default_rng(T + tt)
+    sel = S.zipf_sel_np(rng, T, E, TOPK, zipf) if zipf else \
+        np.stack([rng.permutation(E)[:TOPK] for _ in range(T)]).astype(np.int32)
+    te, ts = prefill.build_tiles(S.to_device(sel, dev), E, tt)
+    we, ws = O.build_tiles(sel, E, tt)
+    assert np.array_equal(te.cpu().numpy(), we) and np.array_equal(ts.cpu().numpy(), ws)
+
+
+def test_tiles_flag_bad_expert(dev):
+    sel = np.array([[0, 1], [2, 700]], np.int32)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    te, ts = prefill.build_tiles(S.to_device(sel, dev), 4, 32, status=status)
+    assert int(status.item()) == 1
+    assert 3 not in ts.cpu().numpy()[: (4 * 2 // 32 + 4) * 32].tolist()
+
+
+@pytest.mark.parametrize("T,tt,zf", [(512, 32, 0.9), (512, 64, 0.9), (96, 32, 0.99)])
+def test_union_bit_exact(dev, T, tt, zf):
+    h, sel, gains = S.prefill_inputs_np(31 + T, T=T, zero_frac=zf)
+    hd = S.to_device(h, dev)
+    te, ts = prefill.build_tiles(S.to_device(sel, dev), E, tt)
+    ul, uc = prefill.build_union(hd, te, ts, F=F, FS=FS, topk=TOPK, E=E, tt=tt)
+    we, ws = O.build_tiles(sel, E, tt)
+    wl, wc = O.build_union(O.bf16_to_f32(h), we, ws, F=F, FS=FS, topk=TOPK, E=E, tt=tt)
+    assert np.array_equal(uc.cpu().numpy(), wc)
+    assert np.array_equal(ul.cpu().numpy(), wl)
+
+
+@pytest.mark.parametrize("T,tt,zf", [(128, 32, 0.9), (512, 32, 0.9), (256, 64, 0.9), (64, 32, 0.995)])
+def test_prefill_gemm_matches_oracle(layer, dev, T, tt, zf):
+    h, sel, gains = S.prefill_inputs_np(41 + T + tt, T=T, zero_frac=zf)
+    y = prefill.sparse_down_prefill(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev),
+                                    *layer["nm"], F=F, FS=FS, D=D, topk=TOPK, E=E, tt=tt, out_dtype=torch.float32)
+    ref, _ = O.sparse_down_prefill(O.bf16_to_f32(h), sel, gains, *layer["nm_np"], F=F, FS=FS, D=D, topk=TOPK,
+                                   E=E, tt=tt)
+    yh = y.cpu().numpy()
+    scale = np.abs(ref).max()
+    err = np.abs(yh - ref)
+    print(f"T={T} tt={tt}: max|ref| {scale:.2f} max abs err {err.max():.3e} rel {err.max() / scale:.2e}")
+    assert err.max() <= 1e-2 * scale
+    assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref))
