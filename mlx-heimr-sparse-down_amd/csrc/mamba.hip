@@ -43,6 +43,7 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   const int hh = blockIdx.x / npb, pblk = blockIdx.x - (blockIdx.x / npb) * npb;
   const int tid = threadIdx.x;
   const int cur = *cur_ptr;
+  if ((unsigned)cur >= (unsigned)nslab) return;  // a corrupt ring index: touch nothing
   const int DI = H * P, GN = G * kN, CD = DI + 2 * GN;
   const int hpg = H / G;
   const int g = hh / hpg;
@@ -163,7 +164,8 @@ __global__ void k_select_row(int32_t* cur, const int32_t* n_keep_dev, int n_keep
                              int nslab) {
   if (threadIdx.x == 0) {
     const int nk = n_keep_dev ? *n_keep_dev : n_keep_host;
-    if (nk >= 0 && nk < nslab) *cur = (*cur + nk) % nslab;
+    const int c = *cur;
+    if (nk >= 0 && nk < nslab && c >= 0 && c < nslab) *cur = (c + nk) % nslab;
   }
 }
 
@@ -217,7 +219,7 @@ __global__ void k_accept(const int32_t* __restrict__ draft, const int32_t* __res
   for (int i = 0; i <= k; ++i) tokens[i] = i < a ? draft[i] : (i == a ? tgt[a] : -1);
   if (n_accept) *n_accept = a;
   if (n_keep) *n_keep = a + 1;
-  if (cur) *cur = (*cur + a + 1) % nslab;
+  if (cur && *cur >= 0 && *cur < nslab) *cur = (*cur + a + 1) % nslab;
 }
 
 }  // namespace
