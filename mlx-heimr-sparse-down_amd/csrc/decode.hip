@@ -2,33 +2,36 @@
 // neuron-major layout (hsd/decode.py), plus the dense 4-bit comparator on the stock
 // layout.
 //
-// Work split of the sparse kernel (one token row b, BASELINE shape D=2688, F=1856,
-// FS=3712, top-6 + shared):
-//   * D is cut into chunks of 128 outputs = 16 weight words = 64 bytes of every row.
-//   * A slot's 64-neuron groups are cut into "parts" of up to 16 groups (routed: 16+13,
-//     shared: 16+16+16+10), 16 parts per token.
-//   * One workgroup = (part, D chunk): 256 threads = 16 lane-groups of 16 lanes; lane-
-//     group j owns group g0+j, lane l owns weight word 16c+l (8 outputs). 336
-//     workgroups per token row.
-// Compaction: each lane loads 4 of its group's 64 activations; 4 wave ballots give every
-// lane-group the 64-bit live mask of its group (bit n = neuron 64g+n live). A lane then
-// walks the set bits in ascending order, 8 rows in flight, loading only the live rows'
-// 4-byte words and, if the group has a live row, the group's 16-byte scale and bias
-// vectors. Per group: acc[t] = sum h_i q_{i,t}, hsum = sum h_i (fp32), and
-// term = s*acc + b*hsum (the factorisation of decode.py:125-128). The 16 group terms
-// are summed in ascending group order through LDS, times the slot's gain, into one fp32
-// partial per (part, chunk); a second kernel sums the 16 parts in part order.
-// Every row of a batch is computed by the same code independently of B.
+// Split over (D chunk x groups) so that every CU gets an even share of the bytes and of
+// the arithmetic, then a fixed-order sum (the reference's partial + reduce structure,
+// decode.py:37-144). At the BASELINE shape (D=2688, F=1856, FS=3712, top-6 of 128 +
+// shared) a token row has 232 64-neuron groups:
+//   * k_sparse_down_part: one workgroup = (128-output chunk c, part p of <=16 groups of
+//     one slot): 21 x 16 = 336 workgroups per row. 512 threads = 32 teams of 16 lanes;
+//     team (j, phase) owns the live rows n of group g0+j with n % 2 == phase; lane l owns
+//     weight word 16c+l (8 outputs, a 64-byte piece of every row per team).
+//       1. one round trip: the slot's expert id and gain, and the group's 64 activations
+//          (4 per lane); 4 wave ballots give the live mask and an ascending live-row
+//          list in LDS (+-0 dead, NaN live);
+//       2. one round trip: the live rows' words (4 B per lane) and, once per group, its
+//          16-byte scale and bias vectors;
+//       3. acc[t] = sum h_i q_{i,t}, hsum = sum h_i (fp32); term = s*acc + b*hsum (the
+//          group factorisation of decode.py:125-128);
+//       4. terms summed in (group, phase) order, times the slot's gain -> part[b, p, chunk].
+//   * k_sum_parts: y[b, o] = sum over the 16 parts in part order.
+// No atomics, no inter-workgroup signalling: results are bit-reproducible, and a row
+// of a B-row call is computed exactly as that row alone.
 #include "hsd_common.h"
 
 namespace hsd {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kDC = 128;                 // outputs per D chunk
-constexpr int kWPC = kDC / 8;            // weight words per chunk (one lane each)
-constexpr int kGPW = kThreads / kWPC;    // groups per workgroup (one per lane-group)
-constexpr int kRB = 8;                   // live rows in flight per lane
+constexpr int kRS = 2;                   // row phases per group
+constexpr int kThreads = 256 * kRS;
+constexpr int kWPC = 16;                 // weight words per D chunk (one lane each)
+constexpr int kDC = kWPC * 8;            // outputs per D chunk
+constexpr int kGPW = 16;                 // groups per workgroup
+constexpr int kRB = (16 + kRS - 1) / kRS;  // rows per lane per batch (16 live rows a group)
 
 struct Geom {
   int D, F, FS, topk, E, NR, NW;
@@ -36,7 +39,6 @@ struct Geom {
   int gpr;     // groups per routed expert (F/64)
   int gsh;     // groups of the shared expert (FS/64)
   int ppr;     // parts per routed slot
-  int psh;     // parts of the shared slot
   int nparts;  // parts per token row
   int nwg;     // workgroups per token row
   int ngt;     // groups per token row (live mask entries)
@@ -51,8 +53,7 @@ Geom make_geom(int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E) {
   g.gpr = (int)(F / 64);
   g.gsh = (int)(FS / 64);
   g.ppr = (g.gpr + kGPW - 1) / kGPW;
-  g.psh = (g.gsh + kGPW - 1) / kGPW;
-  g.nparts = g.topk * g.ppr + g.psh;
+  g.nparts = g.topk * g.ppr + (g.gsh + kGPW - 1) / kGPW;
   g.nwg = g.nparts * g.nchunk;
   g.ngt = g.topk * g.gpr + g.gsh;
   return g;
@@ -60,6 +61,12 @@ Geom make_geom(int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E) {
 
 __device__ __forceinline__ float lo_bf16(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
+// nonzero test on the element's bits: +-0 dead, NaN live
+template <int HDT> __device__ __forceinline__ bool live_bits(typename Elem<HDT>::T v);
+template <> __device__ __forceinline__ bool live_bits<HSD_DT_BF16>(uint16_t v) { return (v & 0x7FFFu) != 0; }
+template <> __device__ __forceinline__ bool live_bits<HSD_DT_F16>(uint16_t v) { return (v & 0x7FFFu) != 0; }
+template <> __device__ __forceinline__ bool live_bits<HSD_DT_F32>(float v) { return !(v == 0.0f); }
 
 template <int HDT>
 __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
@@ -69,146 +76,191 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
     const uint32_t* __restrict__ spw, const uint16_t* __restrict__ sps,
     const uint16_t* __restrict__ spb, float* __restrict__ part, uint64_t* __restrict__ live_out,
     int32_t* __restrict__ status, Geom g, int B, int dense) {
-  __shared__ float hsh[kGPW][64];
-  __shared__ float red[kGPW * 8 * kWPC];  // [j][t][l]
+  using HT = typename Elem<HDT>::T;
+  __shared__ HT hs[kGPW * kRS][64];                 // per team: the group's activations
+  __shared__ uint8_t lst[kGPW * kRS][64];           // per team: the group's live rows, ascending
+  __shared__ float red[kGPW * kRS][8][kWPC];        // per team: group terms
+  __shared__ float sum2[kDC][kRS * 2 + 1];
 
   const int logical = xcd_remap((int)blockIdx.x, B * g.nwg);
   const int b = logical / g.nwg;
   const int rem = logical - b * g.nwg;
   const int p = rem / g.nchunk, c = rem - p * g.nchunk;
-  const int tid = threadIdx.x, j = tid >> 4, l = tid & 15;
-
-  int k, g0, ng, gbase;
-  if (p < g.topk * g.ppr) {
-    k = p / g.ppr;
-    g0 = (p - k * g.ppr) * kGPW;
-    ng = min(kGPW, g.gpr - g0);
-    gbase = k * g.gpr;
-  } else {
-    k = g.topk;
-    g0 = (p - g.topk * g.ppr) * kGPW;
-    ng = min(kGPW, g.gsh - g0);
-    gbase = g.topk * g.gpr;
-  }
-
-  const uint32_t* wb;
-  const uint16_t* sb;
-  const uint16_t* bb;
-  int hoff;
-  bool ok = true;
-  if (k < g.topk) {
-    const int e = sel[b * g.topk + k];
-    ok = (unsigned)e < (unsigned)g.E;
-    const size_t es = ok ? (size_t)e : 0;
-    wb = pw + es * (size_t)g.F * g.NW;
-    sb = ps + es * (size_t)g.gpr * g.D;
-    bb = pb + es * (size_t)g.gpr * g.D;
-    hoff = k * g.F;
-  } else {
-    wb = spw;
-    sb = sps;
-    bb = spb;
-    hoff = g.topk * g.F;
-  }
-  if (!ok && tid == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
-  const float gain = gains[b * (g.topk + 1) + k];
-
-  // ---- compaction: the group's 64-bit live mask from four wave ballots
+  const int tid = threadIdx.x, team = tid >> 4, l = tid & 15;
+  const int j = team % kGPW, phase = team / kGPW;   // group slot, row phase
+  const bool routed = p < g.topk * g.ppr;
+  const int k = routed ? p / g.ppr : g.topk;
+  const int g0 = (routed ? p - k * g.ppr : p - g.topk * g.ppr) * kGPW;
+  const int ng = min(kGPW, (routed ? g.gpr : g.gsh) - g0);
   const int grp = g0 + j;
-  const bool gvalid = ok && j < ng;
-  const typename Elem<HDT>::T* hrow = h + (size_t)b * g.NR + hoff + (size_t)grp * 64;
+  const bool jv = j < ng;
+
+  // ---- round trip 1: expert id, gain and activations, issued together. The id/gain are
+  // fetched as vector loads (an opaque zero lane offset) so that the activation loads do
+  // not wait on them through the scalar-load counter.
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  const int e = routed ? sel[b * g.topk + k + z] : 0;
+  const float gain = gains[b * (g.topk + 1) + k + z];
+  const uint32_t hoff = (uint32_t)b * (uint32_t)g.NR + (uint32_t)(routed ? k * g.F : g.topk * g.F) +
+                        (uint32_t)grp * 64u;
+  HT hv[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) hv[v] = jv ? h[hoff + 16 * v + l] : (HT)0;
+  __builtin_amdgcn_sched_barrier(0);
+  const bool ok = !routed || (unsigned)e < (unsigned)g.E;
+  if (!ok && tid == 0 && c == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+
+  // ---- live mask (4 ballots over the wave's 4 teams) and the compacted row list
+  const int sh = 16 * (team & 3);
+  int cnt = 0;
   uint64_t live = 0;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const float x = gvalid ? Elem<HDT>::load(hrow, 16 * v + l) : 0.0f;
-    const uint64_t bal = __ballot(gvalid && !(x == 0.0f));  // +-0 dead, NaN live
-    live |= ((bal >> (16 * (j & 3))) & 0xFFFFull) << (16 * v);
-    hsh[j][16 * v + l] = x;
+    const bool nz = ok && jv && live_bits<HDT>(hv[v]);
+    // a team walks the rows n = 16v + l with n % kRS == phase: the phase of a row depends
+    // on the row alone, so the dense control sums in the same grouping and order
+    const bool use = jv && (dense ? ok : nz) && (l % kRS) == phase;
+    const uint32_t mnz = (uint32_t)(__ballot(nz) >> sh) & 0xFFFFu;
+    const uint32_t muse = (uint32_t)(__ballot(use) >> sh) & 0xFFFFu;
+    live |= (uint64_t)mnz << (16 * v);
+    if (use) lst[team][cnt + __popc(muse & ((1u << l) - 1u))] = (uint8_t)(16 * v + l);
+    cnt += __popc(muse);
+    hs[team][16 * v + l] = hv[v];
   }
-  const uint64_t rows = dense ? (gvalid ? ~0ull : 0ull) : live;
-  if (live_out && c == 0 && l == 0 && j < ng) live_out[(size_t)b * g.ngt + gbase + grp] = live;
+  if (live_out && c == 0 && phase == 0 && l == 0 && jv)
+    live_out[(size_t)b * g.ngt + (routed ? k * g.gpr : g.topk * g.gpr) + grp] = live;
+  // the team's LDS rows were written by lanes of this wave: a wave-level hand-off
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- the group's scales and biases, only if it has a row to read
+  // ---- round trip 2: live rows of this phase, and the group's scales/biases
   const int w = c * kWPC + l;
-  uint4 sv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
-  if (rows) {
-    sv = *reinterpret_cast<const uint4*>(sb + (size_t)grp * g.D + 8 * w);
-    bv = *reinterpret_cast<const uint4*>(bb + (size_t)grp * g.D + 8 * w);
-  }
-  __syncthreads();
-
-  // ---- live rows, ascending, kRB in flight
-  const uint32_t* wrow = wb + (size_t)grp * 64 * g.NW + w;
+  const size_t es = ok ? (size_t)e : 0;
+  const uint16_t* sb = routed ? ps + es * (size_t)g.gpr * g.D : sps;
+  const uint16_t* bb = routed ? pb + es * (size_t)g.gpr * g.D : spb;
+  const uint32_t* wb = routed ? pw + es * (size_t)g.F * g.NW : spw;
+  const uint32_t row0 = (uint32_t)grp * 64u * (uint32_t)g.NW + (uint32_t)w;
   float acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
   float hsum = 0.0f;
-  uint64_t m = rows;
-  while (m) {
+  uint4 sv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
+  const int nmine = cnt;                              // this team's rows
+  int nmax = nmine;                                   // most rows of any team of the wave
+  nmax = max(nmax, __shfl_xor(nmax, 16, 64));
+  nmax = max(nmax, __shfl_xor(nmax, 32, 64));
+  nmax = __builtin_amdgcn_readfirstlane(nmax);
+  for (int r0 = 0; r0 < nmax; r0 += kRB) {            // one batch unless > 16 live rows
+    int idx[kRB];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r) idx[r] = r0 + r < nmine ? (int)lst[team][r0 + r] : -1;
     uint32_t q[kRB];
-    float hv[kRB];
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
-      if (m) {
-        const int n = __builtin_ctzll(m);
-        m &= m - 1;
-        q[r] = wrow[(size_t)n * g.NW];
-        hv[r] = hsh[j][n];
-      } else {
-        q[r] = 0u;
-        hv[r] = 0.0f;
-      }
+      q[r] = 0u;
+      if (idx[r] >= 0)
+        q[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(wb) +
+                                                  (size_t)(row0 + (uint32_t)idx[r] * (uint32_t)g.NW) * 4u);
     }
+    if (r0 == 0 && cnt > 0) {
+      const size_t off = ((size_t)grp * g.D + 8u * (uint32_t)w) * 2u;
+      sv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(sb) + off);
+      bv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(bb) + off);
+    }
+    HT hr[kRB];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r) hr[r] = hs[team][idx[r] < 0 ? 0 : idx[r]];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
-      hsum += hv[r];
-      const uint32_t lo = q[r] & 0x0F0F0F0Fu, hi = (q[r] >> 4) & 0x0F0F0F0Fu;
+      if (r0 + r < nmax) {                            // wave-uniform bound
+        const float x = idx[r] >= 0 ? Elem<HDT>::load(&hr[r], 0) : 0.0f;
+        hsum += x;
+        const uint32_t lo = q[r] & 0x0F0F0F0Fu, hi = (q[r] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] = fmaf(hv[r], (float)((lo >> (8 * i)) & 0xFFu), acc[2 * i]);
-        acc[2 * i + 1] = fmaf(hv[r], (float)((hi >> (8 * i)) & 0xFFu), acc[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = fmaf(x, (float)((lo >> (8 * i)) & 0xFFu), acc[2 * i]);
+          acc[2 * i + 1] = fmaf(x, (float)((hi >> (8 * i)) & 0xFFu), acc[2 * i + 1]);
+        }
       }
     }
   }
 
-  // ---- group term s*acc + b*hsum, then the ordered sum over the workgroup's groups
+  // ---- group terms, then the ordered sum over (group, phase), two levels
   const uint32_t s32[4] = {sv.x, sv.y, sv.z, sv.w};
   const uint32_t b32[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    red[(j * 8 + 2 * i) * kWPC + l] = fmaf(lo_bf16(s32[i]), acc[2 * i], lo_bf16(b32[i]) * hsum);
-    red[(j * 8 + 2 * i + 1) * kWPC + l] =
-        fmaf(hi_bf16(s32[i]), acc[2 * i + 1], hi_bf16(b32[i]) * hsum);
+    red[team][2 * i][l] = fmaf(lo_bf16(s32[i]), acc[2 * i], lo_bf16(b32[i]) * hsum);
+    red[team][2 * i + 1][l] = fmaf(hi_bf16(s32[i]), acc[2 * i + 1], hi_bf16(b32[i]) * hsum);
+  }
+  __syncthreads();
+  // level 1: kThreads/kDC threads per output, each over a contiguous run of groups
+  constexpr int kL1 = kThreads / kDC;                 // 4 sub-sums per output
+  constexpr int kGPS = kGPW / kL1;                    // groups per sub-sum
+  {
+    const int o = tid % kDC, s = tid / kDC;
+    const int lw = o >> 3, t = o & 7;
+    float acc2 = 0.0f;
+    bool first = true;
+#pragma unroll
+    for (int i = 0; i < kGPS; ++i) {
+      const int jj = s * kGPS + i;
+      if (jj < ng) {
+#pragma unroll
+        for (int ph = 0; ph < kRS; ++ph) {
+          const float v = red[ph * kGPW + jj][t][lw];
+          acc2 = first ? v : acc2 + v;
+          first = false;
+        }
+      }
+    }
+    sum2[o][s] = acc2;
   }
   __syncthreads();
   if (tid < kDC) {
-    const int lw = tid >> 3, t = tid & 7;  // output 8*lw + t of the chunk
-    float s = red[t * kWPC + lw];
-    for (int jj = 1; jj < ng; ++jj) s += red[(jj * 8 + t) * kWPC + lw];
-    part[((size_t)b * g.nparts + p) * g.D + (size_t)c * kDC + tid] = gain * s;
+    float v = sum2[tid][0];
+#pragma unroll
+    for (int s = 1; s < kL1; ++s) v += sum2[tid][s];
+    part[((size_t)b * g.nparts + p) * g.D + (size_t)c * kDC + tid] = gain * v;
   }
 }
 
-template <int YDT>
+template <int YDT, int NP>
 __global__ __launch_bounds__(256) void k_sum_parts(const float* __restrict__ part,
                                                    typename Elem<YDT>::T* __restrict__ y, int D,
-                                                   int nparts) {
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  const int b = blockIdx.y;
-  if (o >= D) return;
+                                                   int nparts, int n) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n) return;
+  const int b = idx / D, o = idx - b * D;
   const float* pp = part + (size_t)b * nparts * D + o;
-  float s = pp[0];
-  for (int q = 1; q < nparts; ++q) s += pp[(size_t)q * D];
-  Elem<YDT>::store(y, (size_t)b * D + o, s);
+  if (NP > 0) {
+    float v[NP > 0 ? NP : 1];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) v[q] = pp[(size_t)q * D];
+    float s = v[0];
+#pragma unroll
+    for (int q = 1; q < NP; ++q) s += v[q];
+    Elem<YDT>::store(y, idx, s);
+  } else {
+    float s = pp[0];
+    for (int q = 1; q < nparts; ++q) s += pp[(size_t)q * D];
+    Elem<YDT>::store(y, idx, s);
+  }
 }
 
 // ----------------------------------------------------------------- dense comparator
-// One wavefront per kOPW outputs, all topk+1 slots: lane u reads the 16-byte word
-// group (32 neurons) u of each output row, with that half-group's scale and bias; the
-// token's h is staged once per workgroup in LDS (fp32). Per lane and slot:
-// gain * (s*acc + b*hsum) over its 32 neurons; a butterfly sum over the wave gives y.
+// The stock layout w [E, D, F/8]: output row o of a slot is F/8 contiguous words. One
+// wavefront computes kOPW outputs over all topk+1 slots: the slots' rows, seen as one
+// run of 16-byte pieces (32 neurons each; piece u covers h[32u .. 32u+31] because the
+// slots are contiguous in h), are split over the 64 lanes (piece u -> lane u % 64). Every
+// lane issues all its weight/scale/bias loads for the kOPW outputs before using any;
+// h comes from LDS. Per piece: gain * (s*acc + b*hsum); a butterfly sum gives y.
 constexpr int kOPW = 2;
 constexpr int kDenseWaves = 4;
+constexpr int kMaxPieces = 8;            // pieces per lane: (topk*F + FS)/32 <= 512
 
 template <int HDT, int YDT>
 __global__ __launch_bounds__(64 * kDenseWaves) void k_dense_down(
@@ -218,61 +270,90 @@ __global__ __launch_bounds__(64 * kDenseWaves) void k_dense_down(
     const uint32_t* __restrict__ sw, const uint16_t* __restrict__ ss,
     const uint16_t* __restrict__ sbias, typename Elem<YDT>::T* __restrict__ y,
     int32_t* __restrict__ status, int D, int F, int FS, int topk, int E) {
-  extern __shared__ float hsh[];
+  using HT = typename Elem<HDT>::T;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+  HT* hsh = reinterpret_cast<HT*>(dsm);
   const int NR = topk * F + FS;
   const int b = blockIdx.y;
-  for (int i = threadIdx.x; i < NR; i += blockDim.x) hsh[i] = Elem<HDT>::load(h, (size_t)b * NR + i);
-  __syncthreads();
+  for (int i = threadIdx.x; i < NR; i += blockDim.x) hsh[i] = h[(size_t)b * NR + i];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int o0 = (blockIdx.x * kDenseWaves + wave) * kOPW;
-  float tot[kOPW];
+  const int ur = F / 32, nu = NR / 32;
+  // this lane's pieces: slot, piece within the slot's row, gain, row base
+  const uint32_t* rowp[kMaxPieces];
+  const uint16_t* scp[kMaxPieces];
+  const uint16_t* bip[kMaxPieces];
+  int rowstride[kMaxPieces], gstride[kMaxPieces];
+  float gn[kMaxPieces];
+  bool pv[kMaxPieces];
 #pragma unroll
-  for (int i = 0; i < kOPW; ++i) tot[i] = 0.0f;
-  for (int k = 0; k <= topk; ++k) {
-    const uint32_t* wk;
-    const uint16_t *sk, *bk;
-    int width, hoff;
+  for (int i = 0; i < kMaxPieces; ++i) {
+    const int u = lane + 64 * i;
+    pv[i] = u < nu;
+    rowp[i] = sw; scp[i] = ss; bip[i] = sbias; rowstride[i] = 0; gstride[i] = 0; gn[i] = 0.0f;
+    if (!pv[i]) continue;
+    int k, uu;
+    if (u < topk * ur) { k = u / ur; uu = u - k * ur; } else { k = topk; uu = u - topk * ur; }
+    gn[i] = gains[b * (topk + 1) + k];
     if (k < topk) {
-      int e = sel[b * topk + k];
+      const int e = sel[b * topk + k];
       if ((unsigned)e >= (unsigned)E) {
-        if (lane == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+        if (status && uu == 0) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+        pv[i] = false;
         continue;
       }
-      width = F;
-      hoff = k * F;
-      wk = w + (size_t)e * D * (F / 8);
-      sk = s + (size_t)e * D * (F / 64);
-      bk = bias + (size_t)e * D * (F / 64);
+      rowstride[i] = F / 8; gstride[i] = F / 64;
+      rowp[i] = w + (size_t)e * D * (F / 8) + 4 * uu;
+      scp[i] = s + (size_t)e * D * (F / 64) + uu / 2;
+      bip[i] = bias + (size_t)e * D * (F / 64) + uu / 2;
     } else {
-      width = FS;
-      hoff = topk * F;
-      wk = sw;
-      sk = ss;
-      bk = sbias;
+      rowstride[i] = FS / 8; gstride[i] = FS / 64;
+      rowp[i] = sw + 4 * uu;
+      scp[i] = ss + uu / 2;
+      bip[i] = sbias + uu / 2;
     }
-    const float gain = gains[b * (topk + 1) + k];
-    const int nu = width / 32, ngr = width / 64, nwd = width / 8;
-    for (int u = lane; u < nu; u += 64) {
-      const float* hv = hsh + hoff + 32 * u;
-      float hs = 0.0f;
+  }
+  uint4 q[kOPW][kMaxPieces];
+  float sc[kOPW][kMaxPieces], bi[kOPW][kMaxPieces];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) hs += hv[i];
+  for (int oi = 0; oi < kOPW; ++oi) {
+    const int o = min(o0 + oi, D - 1);
 #pragma unroll
-      for (int oi = 0; oi < kOPW; ++oi) {
-        const int o = o0 + oi;
-        if (o >= D) break;
-        const uint4 q4 = *reinterpret_cast<const uint4*>(wk + (size_t)o * nwd + 4 * u);
-        const float sc = bf16_bits_to_f32(sk[(size_t)o * ngr + u / 2]);
-        const float bi = bf16_bits_to_f32(bk[(size_t)o * ngr + u / 2]);
-        const uint32_t qw[4] = {q4.x, q4.y, q4.z, q4.w};
-        float acc = 0.0f;
-#pragma unroll
-        for (int wi = 0; wi < 4; ++wi)
-#pragma unroll
-          for (int n = 0; n < 8; ++n)
-            acc = fmaf(hv[8 * wi + n], (float)((qw[wi] >> (4 * n)) & 0xFu), acc);
-        tot[oi] = fmaf(gain, fmaf(sc, acc, bi * hs), tot[oi]);
+    for (int i = 0; i < kMaxPieces; ++i) {
+      q[oi][i] = make_uint4(0, 0, 0, 0);
+      sc[oi][i] = 0.0f;
+      bi[oi][i] = 0.0f;
+      if (pv[i]) {
+        q[oi][i] = *reinterpret_cast<const uint4*>(rowp[i] + (size_t)o * rowstride[i]);
+        sc[oi][i] = bf16_bits_to_f32(scp[i][(size_t)o * gstride[i]]);
+        bi[oi][i] = bf16_bits_to_f32(bip[i][(size_t)o * gstride[i]]);
       }
+    }
+  }
+  __syncthreads();
+  float tot[kOPW];
+#pragma unroll
+  for (int oi = 0; oi < kOPW; ++oi) tot[oi] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMaxPieces; ++i) {
+    if (!pv[i]) continue;
+    const int u = lane + 64 * i;
+    float hv[32];
+    float hs = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 32; ++n) {
+      hv[n] = Elem<HDT>::load(hsh, 32 * u + n);
+      hs += hv[n];
+    }
+#pragma unroll
+    for (int oi = 0; oi < kOPW; ++oi) {
+      const uint32_t qw[4] = {q[oi][i].x, q[oi][i].y, q[oi][i].z, q[oi][i].w};
+      float acc = 0.0f;
+#pragma unroll
+      for (int wi = 0; wi < 4; ++wi)
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc = fmaf(hv[8 * wi + n], (float)((qw[wi] >> (4 * n)) & 0xFu), acc);
+      tot[oi] = fmaf(gn[i], fmaf(sc[oi][i], acc, bi[oi][i] * hs), tot[oi]);
     }
   }
 #pragma unroll
@@ -310,9 +391,11 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
     return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (B < 0 || topk <= 0 || E <= 0) return set_error(HSD_ERR_SHAPE, "%s: bad B/topk/E", fn);
   if (D <= 0 || D % kDC || F <= 0 || F % 64 || FS <= 0 || FS % 64)
-    return set_error(HSD_ERR_SHAPE, "%s: need D %% 128 == 0, F %% 64 == 0, FS %% 64 == 0 (D=%lld F=%lld FS=%lld)",
-                     fn, (long long)D, (long long)F, (long long)FS);
-  if (topk * F + FS > (int64_t)1 << 30 || D > 65536 || B > 65535)
+    return set_error(HSD_ERR_SHAPE, "%s: need D %% %d == 0, F %% 64 == 0, FS %% 64 == 0 (D=%lld F=%lld FS=%lld)",
+                     fn, kDC, (long long)D, (long long)F, (long long)FS);
+  if (topk * F + FS > (int64_t)1 << 30 || D > 65536 || B > 65535 ||
+      B * (topk * F + FS) >= ((int64_t)1 << 32) || F * (D / 8) >= ((int64_t)1 << 32) ||
+      FS * (D / 8) >= ((int64_t)1 << 32))
     return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
   if (!aligned16(ps) || !aligned16(pb) || !aligned16(sps) || !aligned16(spb))
     return set_error(HSD_ERR_ALIGN, "%s: scales/biases must be 16-byte aligned", fn);
@@ -325,9 +408,9 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
   hipStream_t st = as_stream(stream);
   const int64_t nblk = B * (int64_t)g.nwg;
   if (nblk > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too many workgroups", fn);
-#define HSD_PART(DT)                                                                        \
-  hipLaunchKernelGGL(k_sparse_down_part<DT>, dim3((unsigned)nblk), dim3(kThreads), 0, st,  \
-                     reinterpret_cast<const typename Elem<DT>::T*>(h), sel, gains, pw, ps, pb, \
+#define HSD_PART(DT)                                                                          \
+  hipLaunchKernelGGL(k_sparse_down_part<DT>, dim3((unsigned)nblk), dim3(kThreads), 0, st,    \
+                     reinterpret_cast<const typename Elem<DT>::T*>(h), sel, gains, pw, ps, pb,  \
                      spw, sps, spb, part, live_masks, dev_status, g, (int)B, dense)
   switch (h_dtype) {
     case HSD_DT_BF16: HSD_PART(HSD_DT_BF16); break;
@@ -338,10 +421,15 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
 #undef HSD_PART
   int rc = check_launch(fn);
   if (rc) return rc;
-  dim3 rgrid((unsigned)((D + 255) / 256), (unsigned)B);
-#define HSD_SUM(DT)                                                                   \
-  hipLaunchKernelGGL(k_sum_parts<DT>, rgrid, dim3(256), 0, st, part,                 \
-                     reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts)
+  const int n = (int)(B * D);
+  const dim3 rgrid((unsigned)((n + 255) / 256));
+#define HSD_SUM(DT)                                                                                  \
+  if (g.nparts == 16)                                                                                \
+    hipLaunchKernelGGL((k_sum_parts<DT, 16>), rgrid, dim3(256), 0, st, part,                         \
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n);            \
+  else                                                                                               \
+    hipLaunchKernelGGL((k_sum_parts<DT, 0>), rgrid, dim3(256), 0, st, part,                          \
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n);
   switch (y_dtype) {
     case HSD_DT_BF16: HSD_SUM(HSD_DT_BF16); break;
     case HSD_DT_F16: HSD_SUM(HSD_DT_F16); break;
@@ -365,13 +453,14 @@ extern "C" int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* 
     return set_error(HSD_ERR_SHAPE, "%s: need F %% 64 == 0 and FS %% 64 == 0", fn);
   if (!aligned16(w) || !aligned16(sw)) return set_error(HSD_ERR_ALIGN, "%s: weights must be 16-byte aligned", fn);
   const int64_t NR = topk * F + FS;
-  if (NR * 4 > 65536) return set_error(HSD_ERR_SHAPE, "%s: h row of %lld floats exceeds LDS", fn, (long long)NR);
+  if (NR > 64 * 32 * kMaxPieces || (h_dtype == HSD_DT_F32 && NR * 4 > 65536))
+    return set_error(HSD_ERR_SHAPE, "%s: h row of %lld elements too long", fn, (long long)NR);
   if (B == 0) return HSD_OK;
   if (B > 65535 || D > (1 << 24)) return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
   const int per_wg = kOPW * kDenseWaves;
   dim3 grid((unsigned)((D + per_wg - 1) / per_wg), (unsigned)B);
   hipStream_t st = as_stream(stream);
-  const size_t lds = (size_t)NR * sizeof(float);
+  const size_t lds = (size_t)NR * (h_dtype == HSD_DT_F32 ? 4 : 2);
 #define HSD_DENSE(HD, YD)                                                                        \
   hipLaunchKernelGGL((k_dense_down<HD, YD>), grid, dim3(64 * kDenseWaves), lds, st,              \
                      reinterpret_cast<const typename Elem<HD>::T*>(h), sel, gains, w, s, b, sw, ss, \

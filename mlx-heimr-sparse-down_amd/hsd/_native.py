@@ -12,7 +12,8 @@ import os
 import torch
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_ROOT, "libhsd.so")
+# HSD_LIB: path of another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("HSD_LIB") or os.path.join(_PKG_ROOT, "libhsd.so")
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 STATUS_BAD_EXPERT = 1
@@ -34,7 +35,7 @@ _SIGS = {
     "hsd_prefill_num_tiles": (_c_i64, [_c_i64] * 4),
     "hsd_prefill_tiles_workspace_bytes": (_c_size, [_c_i64] * 3),
     "hsd_prefill_tiles": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_size, _vp]),
-    "hsd_prefill_union": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp] + [_c_i64] * 9 + [_vp]),
+    "hsd_prefill_union": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp] + [_c_i64] * 8 + [_vp]),
     "hsd_prefill_gemm_workspace_bytes": (_c_size, [_c_i64] * 3),
     "hsd_prefill_gemm": (_c_int, [_vp] * 13 + [_c_int] + [_c_i64] * 9 + [_vp, _c_size, _vp]),
     "hsd_mamba_workspace_bytes": (_c_size, [_c_i64] * 3),

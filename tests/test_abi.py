@@ -29,6 +29,22 @@ def test_library_exports_every_declared_symbol():
     assert lib.hsd_abi_version() == 1
 
 
+def header_arities():
+    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(hsd_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", src):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_header_arity():
+    ar = header_arities()
+    assert set(ar) == set(N.EXPORTS)
+    for name, (_, argtypes) in N._SIGS.items():
+        assert len(argtypes) == ar[name], f"{name}: ctypes has {len(argtypes)} args, header {ar[name]}"
+
+
 def test_argument_errors_are_reported():
     lib = N.lib()
     assert lib.hsd_permute_nibbles(None, None, 1, 8, 1, None) == -1
@@ -39,9 +55,10 @@ def test_argument_errors_are_reported():
     args = [dummy, 0, dummy, dummy] + [dummy] * 6 + [dummy, 0]
     # D not a multiple of 128
     assert lib.hsd_sparse_down_decode(*args, 1, 200, 1856, 3712, 6, 128, 0, None, None, dummy, 1 << 30, None) == -2
-    # h dtype tag unknown -> checked after shapes and workspace
-    ws = N.lib().hsd_sparse_down_workspace_bytes(1, 2688, 1856, 3712, 6)
-    assert lib.hsd_sparse_down_decode(*args, 1, 2688, 1856, 3712, 6, 128, 0, None, None, dummy, ws - 1, None) == -5
+    # misaligned scales
+    odd = ctypes.c_void_p(18)
+    args2 = [dummy, 0, dummy, dummy, dummy, odd] + [dummy] * 4 + [dummy, 0]
+    assert lib.hsd_sparse_down_decode(*args2, 1, 2688, 1856, 3712, 6, 128, 0, None, None, None, 0, None) == -4
     assert lib.hsd_mamba_verify(*([dummy, 10304] * 3), *([dummy] * 9), 4, dummy, 0,
                                 3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, dummy, 1 << 20, None) == -2  # N != 128
     assert lib.hsd_mamba_select_row(dummy, None, 4, 4, None) == -1                 # n_keep >= nslab
