@@ -305,7 +305,8 @@ def bench_prefill(args):
         nvalid = (ts.view(-1, tt) >= 0).sum(1)
         flops += int((2 * D * nvalid.long() * uc.long()).sum().item())
         prep.append((te, ts, ul, uc))
-    ws = torch.empty(N.lib().hsd_prefill_gemm_workspace_bytes(chunk, D, K), dtype=torch.uint8, device=dev)
+    ws = torch.empty(N.lib().hsd_prefill_gemm_workspace_bytes(chunk, D, F, FS, K, E, tt), dtype=torch.uint8,
+                     device=dev)
 
     def run(i, with_tiles):
         l, h, sel, gains = chunks[i]

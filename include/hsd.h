@@ -105,28 +105,32 @@ int hsd_prefill_tiles(const int32_t* sel, int64_t T, int64_t topk, int64_t E, in
 
 /* Replaces hsd/prefill.py:281-291 `build_union` (kernel prefill.py:48-93): per tile the
  * ascending columns live in any of its valid slots, -1 padded to umax; ucount = size.
- * h [T, topk*F + FS] (h_dtype); ulist [NT, umax] int32; ucount [NT] int32.
- * umax >= FS. */
+ * h [T, topk*F + FS] (h_dtype, 16-byte aligned); ulist [NT, umax] int32;
+ * ucount [NT] int32. umax >= FS; F, FS multiples of 8. */
 int hsd_prefill_union(const void* h, int h_dtype, const int32_t* tile_e,
                       const int32_t* tile_slot, int32_t* ulist, int32_t* ucount, int64_t T,
                       int64_t F, int64_t FS, int64_t topk, int64_t E, int64_t tt, int64_t NT,
                       int64_t umax, void* stream);
 
-/* Replaces hsd/prefill.py:294-321 `sparse_down_prefill` (GEMM kernel prefill.py:119-222
- * and the partial sum prefill.py:320): per tile a bf16 MFMA GEMM over the tile's union
- * rows, B tiles dequantised from the neuron-major layout in LDS, fp32 accumulation,
- * gain epilogue, then y[t] = sum over the topk+1 partials in slot order.
- * h [T, topk*F+FS] bf16; gains [T, topk+1] f32; y [T, D] (y_dtype).
- * Requirements: tt in {32, 64}, D % 128 == 0, F % 64 == 0, FS % 64 == 0.
- * workspace: hsd_prefill_gemm_workspace_bytes() bytes. */
-size_t hsd_prefill_gemm_workspace_bytes(int64_t T, int64_t D, int64_t topk);
-int hsd_prefill_gemm(const uint16_t* h, const float* gains, const int32_t* tile_e,
-                     const int32_t* tile_slot, const int32_t* ulist, const int32_t* ucount,
-                     const uint32_t* pw, const uint16_t* ps, const uint16_t* pb,
-                     const uint32_t* spw, const uint16_t* sps, const uint16_t* spb, void* y,
-                     int y_dtype, int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk,
-                     int64_t E, int64_t tt, int64_t NT, int64_t umax, void* workspace,
-                     size_t workspace_bytes, void* stream);
+/* Replaces hsd/prefill.py:294-321 `sparse_down_prefill` (gather kernel prefill.py:95-117,
+ * GEMM kernel prefill.py:119-222, partial sum prefill.py:320): per tile a bf16 MFMA GEMM
+ * over the tile's union rows (the union list given here decides which rows are read),
+ * the affine dequantisation factored per 64-row group (exact bf16 128+q operands, fp32
+ * accumulation, per-group scale and bias applied in fp32), the gain epilogue, then
+ * y[t] = sum over the topk+1 partials in slot order. Routed slots whose sel entry is out
+ * of range contribute nothing (their tiles never held them).
+ * h [T, topk*F+FS] bf16 (16-byte aligned); sel [T, topk] int32; gains [T, topk+1] f32;
+ * y [T, D] (y_dtype). Requirements: tt in {32, 64}, D % 128 == 0, F and FS multiples of
+ * 64 and at most 4032. workspace: hsd_prefill_gemm_workspace_bytes() bytes. */
+size_t hsd_prefill_gemm_workspace_bytes(int64_t T, int64_t D, int64_t F, int64_t FS,
+                                        int64_t topk, int64_t E, int64_t tt);
+int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const float* gains,
+                     const int32_t* tile_e, const int32_t* tile_slot, const int32_t* ulist,
+                     const int32_t* ucount, const uint32_t* pw, const uint16_t* ps,
+                     const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
+                     const uint16_t* spb, void* y, int y_dtype, int64_t T, int64_t D, int64_t F,
+                     int64_t FS, int64_t topk, int64_t E, int64_t tt, int64_t NT, int64_t umax,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ Mamba-2
  * Replaces the state update of hsd/mamba.py:19-44 `mamba_verify` (depthwise conv,

@@ -49,6 +49,19 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   const int g = hh / hpg;
   const bool owner_bc = (hh % hpg == 0) && pblk == 0;  // writes the B/C conv checkpoints
 
+  // ---- the state rows this workgroup streams: issued first, they do not depend on the
+  // conv, so their latency overlaps it
+  const int lane = tid & 63, wave = tid >> 6;
+  constexpr int kRPW = kPB / (kMT / 64);
+  float2 S[kRPW];
+  const size_t slab_sz = (size_t)H * P * kN;
+#pragma unroll
+  for (int i = 0; i < kRPW; ++i) {
+    const int p = pblk * kPB + wave * kRPW + i;
+    S[i] = *reinterpret_cast<const float2*>(ssm + (size_t)cur * slab_sz +
+                                            ((size_t)hh * P + p) * kN + 2 * lane);
+  }
+
   // ---- depthwise causal conv + silu of the channels this workgroup needs
   const uint16_t* cs0 = convs + (size_t)cur * (kK - 1) * CD;
   for (int t = tid; t < kPB + 2 * kN; t += kMT) {
@@ -100,16 +113,6 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   __syncthreads();
 
   // ---- the state rows: 4 per wave, 2 state elements per lane
-  const int lane = tid & 63, wave = tid >> 6;
-  constexpr int kRPW = kPB / (kMT / 64);
-  float2 S[kRPW];
-  const size_t slab_sz = (size_t)H * P * kN;
-#pragma unroll
-  for (int i = 0; i < kRPW; ++i) {
-    const int p = pblk * kPB + wave * kRPW + i;
-    S[i] = *reinterpret_cast<const float2*>(ssm + (size_t)cur * slab_sz +
-                                            ((size_t)hh * P + p) * kN + 2 * lane);
-  }
   for (int r = 0; r < L; ++r) {
     const float B0 = Bs[r][2 * lane], B1 = Bs[r][2 * lane + 1];
     const float C0 = Cs[r][2 * lane], C1 = Cs[r][2 * lane + 1];

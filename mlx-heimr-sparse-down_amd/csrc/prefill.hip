@@ -4,16 +4,10 @@
 //   k_tiles      one workgroup: stable expert sort of the T*topk slots (wave ballots
 //                give each slot its rank among equal experts), tile bases by a scan,
 //                fixed NT = T*topk/tt + E + ceil(T/tt) with -1 padding, no host readback.
-//   k_union      one workgroup per tile: OR of h != 0 over the tile's slots, ballot +
-//                prefix compaction into an ascending union list (ulist, ucount).
-//   k_gemm       one workgroup per (tile, 128-column block of D): K = the tile's union
-//                rows in chunks of 64. Per chunk the B tile (64 rows x 128 columns) is
-//                dequantised from the 4-bit rows and their groups' bf16 scale/bias as
-//                bf16(s*q + b) into LDS (n-major), the A tile (tt slots x 64 union
-//                columns of h, bf16) is gathered into LDS, and 4 waves run
-//                v_mfma_f32_32x32x16_bf16 with fp32 accumulators (wave w: columns
-//                32w..32w+31, all tt rows). Epilogue: gain * acc into part[token*(topk+1)+k].
-//   k_sum_slots  y[t] = sum over the topk+1 partials in slot order.
+//   k_union      one workgroup per tile, 8 columns per thread: OR over the tile's slots
+//                of h != 0 (16-byte loads), prefix compaction into the ascending union
+//                list (ulist, ucount).
+//   k_stage, k_gemm, k_sum_slots: the grouped GEMM, described above k_stage.
 #include "hsd_common.h"
 
 namespace hsd {
@@ -110,7 +104,33 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
 }
 
 // ------------------------------------------------------------------ union
-constexpr int kUT = 256;
+constexpr int kUT = 512;  // threads of the union kernel; each owns 8 consecutive columns
+
+// Bit j set when element j of the 8 activations in v is nonzero (+-0 are dead, NaN is live).
+template <int HDT> struct Live8;
+template <> struct Live8<HSD_DT_BF16> {
+  __device__ __forceinline__ static uint32_t get(const void* p) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      m |= (((w[i] & 0x7FFFu) != 0u) ? 1u : 0u) << (2 * i) |
+           (((w[i] & 0x7FFF0000u) != 0u) ? 1u : 0u) << (2 * i + 1);
+    return m;
+  }
+};
+template <> struct Live8<HSD_DT_F16> : Live8<HSD_DT_BF16> {};
+template <> struct Live8<HSD_DT_F32> {
+  __device__ __forceinline__ static uint32_t get(const void* p) {
+    const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m |= (((w[i] & 0x7FFFFFFFu) != 0u) ? 1u : 0u) << i;
+    return m;
+  }
+};
 
 template <int HDT>
 __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __restrict__ h,
@@ -120,7 +140,7 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
                                                int32_t* __restrict__ ucount, int F, int FS,
                                                int topk, int E, int tt, int umax) {
   __shared__ int hoff[64];
-  __shared__ int wtot[kUT / 64];
+  __shared__ int wsum[kUT / 64];
   const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS;
   int32_t* out = ulist + (size_t)tile * umax;
@@ -138,24 +158,43 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
   }
   __syncthreads();
   int base = 0;
-  for (int c0 = 0; c0 < FF; c0 += kUT) {
-    const int c = c0 + tid;
-    bool live = false;
-    if (c < FF)
-      for (int m = 0; m < tt; ++m) {
-        const int o = hoff[m];
-        if (o >= 0) {
-          const float v = Elem<HDT>::load(h, (size_t)o + c);
-          live = live || !(v == 0.0f);
+  for (int c0 = 0; c0 < FF; c0 += 8 * kUT) {
+    const int c = c0 + 8 * tid;
+    uint32_t live = 0;  // bit j: column c + j is live in some slot of the tile
+    if (c < FF) {
+      // 8 slots' loads in flight at a time, then their OR
+      for (int m0 = 0; m0 < tt; m0 += 8) {
+        uint32_t lm[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int o = m0 + i < tt ? hoff[m0 + i] : -1;
+          lm[i] = o >= 0 ? Live8<HDT>::get(h + (size_t)o + c) : 0u;
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) live |= lm[i];
       }
-    const uint64_t bal = __ballot(live);
-    if (lane == 0) wtot[wave] = __popcll(bal);
+    }
+    // exclusive prefix of the live counts over the workgroup, in column order
+    const int n = __popc(live);
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    int before = base;
-    for (int w = 0; w < wave; ++w) before += wtot[w];
-    if (live) out[before + __popcll(bal & ((1ull << lane) - 1ull))] = c;
-    for (int w = 0; w < kUT / 64; ++w) base += wtot[w];
+    int before = base, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kUT / 64; ++w) {
+      before += w < wave ? wsum[w] : 0;
+      tot += wsum[w];
+    }
+    int pos = before + incl - n;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if ((live >> j) & 1u) out[pos++] = c + j;
+    base += tot;
     __syncthreads();
   }
   for (int i = base + tid; i < umax; i += kUT) out[i] = -1;
@@ -163,153 +202,411 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 }
 
 // ------------------------------------------------------------------ GEMM
-constexpr int kGT = 256;  // 4 waves
-constexpr int kNB = 128;  // output columns per workgroup
-constexpr int kKC = 64;   // union rows per chunk
-constexpr int kKP = kKC + 8;  // LDS row pitch (bf16) of the A and B tiles
+// The grouped GEMM factors the affine dequantisation by 64-row group g:
+//   y[m, n] = sum_g s[g, n] * sum_{k in g} h[m, k] * q[k, n]  +  sum_g hs[m, g] * b[g, n],
+//   hs[m, g] = sum_{k in g} h[m, k].
+// The MFMA B operand is the exact bf16 value 128 + q, made from a packed nibble word by
+// a mask and an OR with 0x4300 (bf16 128.0); the extra 128 * hs[m, g] per group is
+// removed in the correction term below. The K dimension is the tile's union rows, laid
+// out group by group, each group padded to whole 16-row k-blocks, so one k-block never
+// mixes two groups' scales.
+//
+//   k_stage   one workgroup per tile: group starts in the union list, the padded row
+//             list (row byte offsets, kPadRow for padding), the A fragments of every
+//             k-block in MFMA lane order (h at the padded rows, bf16), hs[m, g] summed in
+//             union order, and the correction A fragments.
+//   k_gemm    one wavefront per (tile, column block): 128 columns for 32-slot tiles, 64
+//             for 64-slot tiles. Per k-block each lane loads 8 packed words (its 8 rows,
+//             one word column) with buffer loads, kPD k-blocks ahead of their use, turns
+//             them into bf16 B fragments with v_perm_b32 + shift/and_or, and runs
+//             v_mfma_f32_32x32x16_bf16. acc accumulates over all groups; at the end of
+//             group g, y += (s_g - s_next) * acc, which sums to sum_g s_g * acc_g (Abel
+//             summation, so acc is never cleared). Before the loop, y starts as the
+//             correction sum_g [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo] x [b, b, s, s]:
+//             4 MFMA k-blocks per 16 groups, their B side staged in an LDS ring.
+//             Epilogue: gain * y into part[token*(topk+1) + k], float4 per lane.
+//   k_sum_slots  y[t] = sum over the topk+1 partials in slot order; routed slots whose
+//             expert id is out of range contribute nothing.
+constexpr int kGMax = 63;          // groups per expert (F/64, FS/64), one per lane
+constexpr int kST = 256;           // threads of the staging kernel
+constexpr int kPadRow = 0x7FFF0000;  // padding row offset: past every expert's weights
+constexpr int kPD = 3;             // k-blocks of weight words in flight per wavefront
+constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 
-template <int MS>  // MS = tt / 32 row blocks
-__global__ __launch_bounds__(kGT) void k_gemm(
-    const uint16_t* __restrict__ h, const float* __restrict__ gains,
-    const int32_t* __restrict__ tile_e, const int32_t* __restrict__ tile_slot,
-    const int32_t* __restrict__ ulist, const int32_t* __restrict__ ucount,
-    const uint32_t* __restrict__ pw, const uint16_t* __restrict__ ps,
-    const uint16_t* __restrict__ pb, const uint32_t* __restrict__ spw,
-    const uint16_t* __restrict__ sps, const uint16_t* __restrict__ spb, float* __restrict__ part,
-    int D, int F, int FS, int topk, int E, int NT, int umax) {
+// k-blocks per tile: at most 4 per group, plus the padding to a multiple of kPD
+__host__ __device__ constexpr int kb_max(int gmx) { return 4 * gmx + kPD; }
+__host__ __device__ constexpr int nch_max(int gmx) { return (gmx + 15) / 16; }
+
+template <int MS>
+__global__ __launch_bounds__(kST) void k_stage(
+    const uint16_t* __restrict__ h, const int32_t* __restrict__ tile_e,
+    const int32_t* __restrict__ tile_slot, const int32_t* __restrict__ ulist,
+    const int32_t* __restrict__ ucount, int32_t* __restrict__ kbg, int32_t* __restrict__ krow,
+    uint4* __restrict__ hc, uint4* __restrict__ hcor, int D, int F, int FS, int topk, int E,
+    int umax, int GMX) {
   constexpr int TT = 32 * MS;
-  __shared__ __attribute__((aligned(16))) uint16_t As[TT * kKP];    // [m][k]
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kNB * kKP];   // [n][k]
   __shared__ int hoff[TT];
-  __shared__ int rows[kKC];
-  const int nblk = D / kNB;
-  const int logical = xcd_remap((int)blockIdx.x, NT * nblk);
-  const int tile = logical / nblk, nb = logical - (logical / nblk) * nblk;
+  __shared__ int gs[kGMax + 1];   // first union position of each group
+  __shared__ int kbs[kGMax + 1];  // first k-block of each group
+  __shared__ int prow[16 * kb_max(kGMax)];
+  __shared__ float hsl[TT][kGMax];
+  const int tile = blockIdx.x, tid = threadIdx.x;
+  const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
+  int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
   const int e = tile_e[tile];
-  if (e < 0) return;
-  const int U = ucount[tile];
-  if (U == 0) return;  // all-dead tile: its slots' partials were zeroed by the caller
+  if (e < 0) {
+    for (int g = tid; g <= GMX; g += kST) kbgT[g] = 0;
+    return;
+  }
   const bool shared = e >= E;
+  const int FF = shared ? FS : F, G = FF / 64;
   const int NR = topk * F + FS;
-  const int NW = D / 8;
-  const int n0 = nb * kNB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t* wb = shared ? spw : pw + (size_t)e * F * NW;
-  const uint16_t* sb = shared ? sps : ps + (size_t)e * (F / 64) * D;
-  const uint16_t* bb = shared ? spb : pb + (size_t)e * (F / 64) * D;
+  const int U = min(max(ucount[tile], 0), umax);
   const int32_t* ul = ulist + (size_t)tile * umax;
   if (tid < TT) {
     const int s = tile_slot[tile * TT + tid];
     hoff[tid] = s < 0 ? -1 : (shared ? s * NR + topk * F : (s / topk) * NR + (s % topk) * F);
   }
-  f32x16 acc[MS];
+  for (int g = tid; g <= G; g += kST) {  // lower bound of 64 g in the ascending list
+    int lo = 0, hi = U;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ul[mid] < 64 * g) lo = mid + 1; else hi = mid;
+    }
+    gs[g] = lo;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int g = 0; g < G; ++g) {  // a group holds at most 64 rows (clamped: any list stays in bounds)
+      kbs[g] = run;
+      run += (min(max(gs[g + 1] - gs[g], 0), 64) + 15) >> 4;
+    }
+    kbs[G] = run;
+    // zero k-blocks (pad rows, A = 0) extend the last group to a multiple of kPD, so the
+    // GEMM loop runs whole rounds of its prefetch ring
+    const int padded = (run + kPD - 1) / kPD * kPD;
+    for (int g = G; g >= 0 && kbs[g] == run; --g) kbs[g] = padded;
+  }
+  __syncthreads();
+  const int nkb = kbs[G];
+  for (int g = tid; g <= GMX; g += kST) kbgT[g] = kbs[g < G ? g : G];
+  for (int p = tid; p < 16 * nkb; p += kST) {
+    int lo = 0, hi = G - 1;  // the last group whose first k-block is at or before p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (16 * kbs[mid] <= p) lo = mid; else hi = mid - 1;
+    }
+    const int j = p - 16 * kbs[lo];
+    int r = -1;
+    if (j < min(max(gs[lo + 1] - gs[lo], 0), 64)) {
+      r = ul[gs[lo] + j];
+      if ((unsigned)r >= (unsigned)FF) r = -1;
+    }
+    prow[p] = r;
+    krow[(size_t)tile * KMX + p] = r >= 0 ? r * (D / 2) : kPadRow;
+  }
+  __syncthreads();
+  // A fragments: lane l of k-block kb, row block ms holds h[slot 32 ms + l%32] at the
+  // padded positions 16 kb + 8 (l/32) + 0..7; hs[m, g] in union order
+  for (int it = tid; it < TT * G; it += kST) {
+    const int m = it / G, g = it - m * G;
+    const int o = hoff[m];
+    float hs = 0.0f;
+    for (int kb = kbs[g]; kb < kbs[g + 1]; ++kb) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = prow[16 * kb + 8 * half + i];
+          v[i] = (o >= 0 && r >= 0) ? (uint32_t)h[(size_t)o + r] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hs += bf16_bits_to_f32(v[i]);
+        hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] =
+            make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                       v[6] | (v[7] << 16));
+      }
+    }
+    hsl[m][g] = hs;
+  }
+  __syncthreads();
+  // correction A fragments, 16 groups per chunk: sections [hs_hi, hs_lo, -128 hs_hi,
+  // -128 hs_lo]; hs = hs_hi + hs_lo to about 16 bits, -128 x is exact in bf16
+  const int NCH = (G + 15) >> 4;
+  for (int it = tid; it < NCH * 4 * MS * 64; it += kST) {
+    const int lane = it & 63, ms = (it >> 6) % MS, sec = (it / (64 * MS)) & 3,
+              ch = it / (256 * MS);
+    const int m = 32 * ms + (lane & 31), khalf = lane >> 5;
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int g = 16 * ch + 8 * khalf + i;
+      const float s = g < G ? hsl[m][g] : 0.0f;
+      const uint16_t hi = f32_to_bf16_bits(s);
+      uint16_t b = (sec & 1) ? f32_to_bf16_bits(s - bf16_bits_to_f32(hi)) : hi;
+      if (sec >= 2) b = f32_to_bf16_bits(-128.0f * bf16_bits_to_f32(b));
+      v[i] = b;
+    }
+    hcor[((((size_t)tile * NCHMX + ch) * 4 + sec) * MS + ms) * 64 + lane] =
+        make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                   v[6] | (v[7] << 16));
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(bf16x8, make_uint4(a, b, c, d));
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+template <int MS>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(
+    const int32_t* __restrict__ tile_e, const int32_t* __restrict__ tile_slot,
+    const float* __restrict__ gains, const int32_t* __restrict__ kbg,
+    const int32_t* __restrict__ krow, const uint4* __restrict__ hc,
+    const uint4* __restrict__ hcor, const uint32_t* __restrict__ pw,
+    const uint16_t* __restrict__ ps, const uint16_t* __restrict__ pb,
+    const uint32_t* __restrict__ spw, const uint16_t* __restrict__ sps,
+    const uint16_t* __restrict__ spb, float* __restrict__ part, int D, int F, int FS, int topk,
+    int E, int NT, int GMX) {
+  constexpr int TT = 32 * MS, NWC = 16 / MS, NMF = 4 / MS, NCOL = 8 * NWC;
+  constexpr int RP = 40;  // ring pitch per column (bf16): b of 16 groups, s of 16 groups, pad
+  // LDS: first the correction ring [NCOL][RP], then the scale table [G][NCOL] of this block
+  constexpr int kLds = NCOL * RP > kGMax * NCOL ? NCOL * RP : kGMax * NCOL;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[kLds];
+  const int nblk = D / NCOL;
+  const int logical = xcd_remap((int)blockIdx.x, NT * nblk);
+  const int tile = logical / nblk, nb = logical - (logical / nblk) * nblk;
+  const int e = tile_e[tile];
+  if (e < 0) return;
+  const bool shared = e >= E;
+  const int FF = shared ? FS : F, G = FF / 64;
+  const int l = threadIdx.x, khalf = l >> 5, c = (l & 31) % NWC, jq = (l & 31) / NWC;
+  const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
+  const int n0 = nb * NCOL;
+  const int lcol = 8 * c + NMF * jq;  // first of this lane's NMF columns within the block
+  const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
+  const int kv = l <= G ? kbgT[l] : 0;
+  const int kn = l < G ? kbgT[l + 1] : 0;
+  const uint64_t nonempty = __ballot(l < G && kn > kv);
+  // k-blocks of this tile: a multiple of kPD and at most kb_max(G) by construction; the
+  // clamp keeps a corrupted workspace from driving the loop out of its buffers
+  const int nkb = min(max(__builtin_amdgcn_readlane(kv, G), 0), kb_max(G)) / kPD * kPD;
+
+  f32x16 y[MS][NMF];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[ms][v] = 0.0f;
+    for (int i = 0; i < NMF; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) y[ms][i][v] = 0.0f;
 
-  // B staging task of this thread: rows 4*kq .. 4*kq+3 of the chunk, columns 8*wv .. +7
-  const int kq = tid >> 4, wv = tid & 15;
-  for (int u0 = 0; u0 < U; u0 += kKC) {
-    if (tid < kKC) rows[tid] = (u0 + tid < U) ? ul[u0 + tid] : -1;
+  if (nkb > 0) {
+    f32x16 acc[MS][NMF];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int i = 0; i < NMF; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[ms][i][v] = 0.0f;
+    const uint32_t* wb = shared ? spw : pw + (size_t)e * F * (D / 8);
+    const uint16_t* sb = (shared ? sps : ps + (size_t)e * (F / 64) * D) + n0 + lcol;
+    const uint16_t* bb = (shared ? spb : pb + (size_t)e * (F / 64) * D) + n0 + lcol;
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, FF * (D / 2), 0x00020000);
+    const uint32_t colbyte = (uint32_t)(n0 / 8 + c) * 4u;
+    // the nibble mask as an opaque register, so (x & mask) | magic is one v_and_or_b32
+    // (two literal operands would not fit the instruction)
+    uint32_t nmask;
+    asm volatile("v_mov_b32 %0, 0xf000f" : "=v"(nmask));
+    const uint32_t bsel = MS == 1 ? 2u * jq : (uint32_t)jq;
+    const uint32_t psel = MS == 1 ? (bsel | (bsel + 1) << 8 | (bsel + 4) << 16 | (bsel + 5) << 24)
+                                  : (bsel | 0x0C00u | (bsel + 4) << 16 | 0x0C000000u);
+    const int32_t* kr = krow + (size_t)tile * KMX + 8 * khalf;
+    const uint4* ha = hc + (size_t)tile * KBMX * MS * 64 + l;
+    const uint4* hq = hcor + (size_t)tile * NCHMX * 4 * MS * 64 + l;
+
+    // The correction sum_g [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo] x [b, b, s, s], 16 groups
+    // at a time: the groups' b and s rows of this column block go through the LDS ring
+    // [column][b of 16 groups | s of 16 groups | pad], then 4 MFMA k-blocks start y.
+    const int NCH = (G + 15) >> 4;
+    for (int ch = 0; ch < NCH; ++ch) {
+      uint4 a[4][MS];
+#pragma unroll
+      for (int sec = 0; sec < 4; ++sec)
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) a[sec][ms] = hq[(((size_t)ch * 4 + sec) * MS + ms) * 64];
+      constexpr int V8 = NCOL / 8;           // uint4 pieces per row segment
+      constexpr int NIT = 32 * V8 / 64;      // 32 row segments (b, s of 16 groups)
+      uint4 v[NIT];
+#pragma unroll
+      for (int t = 0; t < NIT; ++t) {
+        const int item = l + 64 * t, r = item / V8, c8 = item % V8;
+        const int gg = 16 * ch + (r & 15);
+        const uint16_t* src = (r < 16 ? bb : sb) - lcol + (size_t)gg * D + 8 * c8;
+        v[t] = gg < G ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < NIT; ++t) {
+        const int item = l + 64 * t, r = item / V8, c8 = item % V8;
+        const uint32_t w[4] = {v[t].x, v[t].y, v[t].z, v[t].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          ring[(8 * c8 + j) * RP + 16 * (r >> 4) + (r & 15)] =
+              (uint16_t)((j & 1) ? w[j >> 1] >> 16 : w[j >> 1]);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int sec = 0; sec < 4; ++sec)
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          const uint4 bv = *reinterpret_cast<const uint4*>(&ring[(lcol + i) * RP + (sec >> 1) * 16 + 8 * khalf]);
+#pragma unroll
+          for (int ms = 0; ms < MS; ++ms)
+            y[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[sec][ms]), as_bf16x8(bv), y[ms][i], 0, 0, 0);
+        }
+    }
+
+    // the scale table s[g][n0 .. n0 + NCOL) of all groups, so that the k-block loop issues
+    // no global load inside its group-end branch
     __syncthreads();
-    // ---- B: dequantise 4 rows x 8 columns -> Bs[n][k]
     {
-      uint32_t q[4];
-      uint4 s4[4], b4[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rows[4 * kq + i];
-        q[i] = 0u;
-        s4[i] = make_uint4(0, 0, 0, 0);
-        b4[i] = make_uint4(0, 0, 0, 0);
-        if (r >= 0) {
-          q[i] = wb[(size_t)r * NW + (n0 >> 3) + wv];
-          s4[i] = *reinterpret_cast<const uint4*>(sb + (size_t)(r >> 6) * D + n0 + 8 * wv);
-          b4[i] = *reinterpret_cast<const uint4*>(bb + (size_t)(r >> 6) * D + n0 + 8 * wv);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {  // column n0 + 8*wv + c
-        uint16_t v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t sw = (&s4[i].x)[c >> 1], bw = (&b4[i].x)[c >> 1];
-          const float sc = (c & 1) ? __uint_as_float(sw & 0xFFFF0000u) : __uint_as_float(sw << 16);
-          const float bi = (c & 1) ? __uint_as_float(bw & 0xFFFF0000u) : __uint_as_float(bw << 16);
-          const float qv = (float)((q[i] >> (4 * c)) & 0xFu);
-          v[i] = f32_to_bf16_bits(fmaf(sc, qv, bi));
-        }
-        uint2 pk;
-        pk.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
-        pk.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
-        *reinterpret_cast<uint2*>(&Bs[(8 * wv + c) * kKP + 4 * kq]) = pk;
-      }
-    }
-    // ---- A: gather h[slot m, rows k] -> As[m][k]
-#pragma unroll
-    for (int it = 0; it < (TT * kKC / 8) / kGT; ++it) {
-      const int task = tid + it * kGT;
-      const int m = task >> 3, ko = (task & 7) * 8;
-      const int o = hoff[m];
-      uint32_t pk[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r0 = rows[ko + 2 * i], r1 = rows[ko + 2 * i + 1];
-        const uint32_t v0 = (o >= 0 && r0 >= 0) ? h[(size_t)o + r0] : 0u;
-        const uint32_t v1 = (o >= 0 && r1 >= 0) ? h[(size_t)o + r1] : 0u;
-        pk[i] = v0 | (v1 << 16);
-      }
-      *reinterpret_cast<uint4*>(&As[m * kKP + ko]) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    }
-    __syncthreads();
-    // ---- MFMA: wave owns columns 32*wave .. +31
-#pragma unroll
-    for (int ks = 0; ks < kKC / 16; ++ks) {
-      const int kk = ks * 16 + 8 * (lane >> 5);
-      const bf16x8 bfrag =
-          *reinterpret_cast<const bf16x8*>(&Bs[(32 * wave + (lane & 31)) * kKP + kk]);
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms) {
-        const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(&As[(32 * ms + (lane & 31)) * kKP + kk]);
-        acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag, bfrag, acc[ms], 0, 0, 0);
+      constexpr int V8 = NCOL / 8;
+      for (int idx = l; idx < G * V8; idx += 64) {
+        const int gg = idx / V8, c8 = idx % V8;
+        *reinterpret_cast<uint4*>(&ring[gg * NCOL + 8 * c8]) =
+            *reinterpret_cast<const uint4*>(sb - lcol + (size_t)gg * D + 8 * c8);
       }
     }
     __syncthreads();
+    auto scales = [&](int g, float (&s)[NMF]) {  // this lane's NMF scales of group g
+      uint32_t w[NMF / 2];
+      if constexpr (NMF == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(&ring[g * NCOL + lcol]);
+        w[0] = v.x; w[1] = v.y;
+      } else {
+        w[0] = *reinterpret_cast<const uint32_t*>(&ring[g * NCOL + lcol]);
+      }
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) s[i] = bf16_bits_to_f32((i & 1) ? w[i >> 1] >> 16 : w[i >> 1] & 0xFFFFu);
+    };
+    // group state: current group g, its end k-block, its scales
+    int g = __builtin_ctzll(nonempty);
+    int gend = __builtin_amdgcn_readlane(kn, g);
+    float scur[NMF];
+    scales(g, scur);
+
+    int4 rq[kPD][2];
+    uint32_t wq[kPD][8];
+    uint4 aq[kPD][MS];
+    auto load_rows = [&](int kb, int4 (&r)[2]) {
+      r[0] = *reinterpret_cast<const int4*>(kr + 16 * kb);
+      r[1] = *reinterpret_cast<const int4*>(kr + 16 * kb + 4);
+    };
+    auto load_words = [&](int kb, const int4 (&r)[2], uint32_t (&w)[8], uint4 (&a)[MS]) {
+      const int ro[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        w[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, (uint32_t)ro[i] + colbyte, 0, 0);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) a[ms] = ha[((size_t)kb * MS + ms) * 64];
+    };
+    // Prefetches past the last k-block re-read the last one (in bounds, never used), so
+    // every path issues the same loads and the waits stay partial.
+    const int klast = nkb - 1;
+#pragma unroll
+    for (int d = 0; d < kPD; ++d) load_rows(min(d, klast), rq[d]);
+    // issue order = consumption order (slot 0 first), so the loop's waits stay partial
+#pragma unroll
+    for (int d = 0; d < kPD; ++d) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_words(min(d, klast), rq[d], wq[d], aq[d]);
+      load_rows(min(d + kPD, klast), rq[d]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int kb0 = 0; kb0 < nkb; kb0 += kPD) {
+#pragma unroll
+      for (int d = 0; d < kPD; ++d) {  // nkb is a multiple of kPD
+        const int kb = kb0 + d;
+        // B fragments: P_i holds column lcol + i of rows (2p, 2p+1) as bf16 128 + q
+        uint32_t bf[NMF][4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t x = __builtin_amdgcn_perm(wq[d][2 * p + 1], wq[d][2 * p], psel);
+#pragma unroll
+          for (int i = 0; i < NMF; ++i) bf[i][p] = ((x >> (4 * i)) & nmask) | kMagic;
+        }
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          const bf16x8 bv = as_bf16x8(bf[i][0], bf[i][1], bf[i][2], bf[i][3]);
+#pragma unroll
+          for (int ms = 0; ms < MS; ++ms)
+            acc[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(aq[d][ms]), bv, acc[ms][i], 0, 0, 0);
+        }
+        load_words(min(kb + kPD, klast), rq[d], wq[d], aq[d]);
+        load_rows(min(kb + 2 * kPD, klast), rq[d]);
+        if (kb + 1 == gend) {  // end of group g: y += (s_g - s_next) * acc
+          const uint64_t rest = nonempty & ~((2ull << g) - 1ull);
+          const int gp = rest ? __builtin_ctzll(rest) : -1;
+          float sn[NMF], ds[NMF];
+          scales(gp >= 0 ? gp : g, sn);
+#pragma unroll
+          for (int i = 0; i < NMF; ++i) {
+            if (gp < 0) sn[i] = 0.0f;
+            ds[i] = scur[i] - sn[i];
+            scur[i] = sn[i];
+          }
+#pragma unroll
+          for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+            for (int i = 0; i < NMF; ++i)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) y[ms][i][v] = fmaf(ds[i], acc[ms][i][v], y[ms][i][v]);
+          if (gp >= 0) {
+            g = gp;
+            gend = __builtin_amdgcn_readlane(kn, g);
+          }
+        }
+      }
+    }
   }
-  // ---- epilogue: C[i][j], j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4
-  const int j = n0 + 32 * wave + (lane & 31);
+
+  // epilogue: C[i][j], j = lane%32 -> column lcol + i, row 32 ms + 8 (v/4) + 4 (lane/32) + v%4
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int i = 32 * ms + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      const int s = tile_slot[tile * TT + i];
-      if (s >= 0) {
-        const int gi = shared ? s * (topk + 1) + topk : (s / topk) * (topk + 1) + (s % topk);
-        part[(size_t)gi * D + j] = gains[gi] * acc[ms][v];
-      }
+      const int m = 32 * ms + 8 * (v >> 2) + 4 * khalf + (v & 3);
+      const int s = tile_slot[tile * TT + m];
+      if (s < 0) continue;
+      const int gi = shared ? s * (topk + 1) + topk : (s / topk) * (topk + 1) + (s % topk);
+      const float gn = gains[gi];
+      float* dst = part + (size_t)gi * D + n0 + lcol;
+      if constexpr (NMF == 4)
+        *reinterpret_cast<float4*>(dst) =
+            make_float4(gn * y[ms][0][v], gn * y[ms][1][v], gn * y[ms][2][v], gn * y[ms][3][v]);
+      else
+        *reinterpret_cast<float2*>(dst) = make_float2(gn * y[ms][0][v], gn * y[ms][1][v]);
     }
-}
-
-// Partials of slots that no GEMM workgroup writes (an empty union, a bad expert id)
-// must read as 0: cleared by a fill kernel (graph-capture safe, no memset node).
-__global__ void k_zero_f32(float* __restrict__ p, size_t n) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) p[i] = 0.0f;
 }
 
 template <int YDT>
 __global__ __launch_bounds__(256) void k_sum_slots(const float* __restrict__ part,
+                                                   const int32_t* __restrict__ sel,
                                                    typename Elem<YDT>::T* __restrict__ y, int T,
-                                                   int D, int nk) {
+                                                   int D, int topk, int E) {
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (size_t)T * D) return;
   const size_t t = idx / D, o = idx - t * D;
-  const float* p = part + t * nk * D + o;
-  float s = p[0];
-  for (int k = 1; k < nk; ++k) s += p[(size_t)k * D];
+  const float* p = part + t * (topk + 1) * D + o;
+  const int32_t* st = sel + t * topk;
+  float s = (unsigned)st[0] < (unsigned)E ? p[0] : 0.0f;
+  for (int k = 1; k < topk; ++k)
+    if ((unsigned)st[k] < (unsigned)E) s += p[(size_t)k * D];
+  s += p[(size_t)topk * D];
   Elem<YDT>::store(y, idx, s);
 }
 
@@ -357,8 +654,11 @@ extern "C" int hsd_prefill_union(const void* h, int h_dtype, const int32_t* tile
   if (!h || !tile_e || !tile_slot || !ulist || !ucount) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (T <= 0 || F <= 0 || FS <= 0 || topk <= 0 || E <= 0 || tt <= 0 || tt > 64 || NT <= 0)
     return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  if (F % 8 || FS % 8) return set_error(HSD_ERR_SHAPE, "%s: F and FS must be multiples of 8", fn);
   if (umax < FS || umax < F) return set_error(HSD_ERR_SHAPE, "%s: umax must be >= FS and F", fn);
   if (NT != hsd_prefill_num_tiles(T, topk, E, tt)) return set_error(HSD_ERR_SHAPE, "%s: NT mismatch", fn);
+  if ((topk * F + FS) * T > ((int64_t)1 << 31)) return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  if ((uintptr_t)h & 15u) return set_error(HSD_ERR_ALIGN, "%s: h must be 16-byte aligned", fn);
   hipStream_t st = as_stream(stream);
   switch (h_dtype) {
 #define HSD_UNION(DT)                                                                             \
@@ -376,58 +676,98 @@ extern "C" int hsd_prefill_union(const void* h, int h_dtype, const int32_t* tile
   return check_launch(fn);
 }
 
-extern "C" size_t hsd_prefill_gemm_workspace_bytes(int64_t T, int64_t D, int64_t topk) {
-  if (T <= 0 || D <= 0 || topk <= 0) return 0;
-  return ((size_t)T * (topk + 1) * D * sizeof(float) + 255) & ~(size_t)255;
+namespace {
+// Workspace of hsd_prefill_gemm, in this order, each piece 256-byte aligned:
+//   part [T*(topk+1), D] f32 | kbg [NT, GMX+1] i32 | krow [NT, 16 KB] i32 |
+//   hc [NT, KB, MS, 64] uint4 | hcor [NT, ceil(GMX/16), 4, MS, 64] uint4, KB = kb_max(GMX)
+struct GemmWs {
+  size_t part, kbg, krow, hc, hcor, total;
+};
+inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E, int64_t tt) {
+  GemmWs w{};
+  const int64_t NT = hsd_prefill_num_tiles(T, topk, E, tt);
+  const int64_t GMX = (F > FS ? F : FS) / 64, MS = tt / 32;
+  w.part = 0;
+  w.kbg = al256((size_t)T * (topk + 1) * D * sizeof(float));
+  w.krow = w.kbg + al256((size_t)NT * (GMX + 1) * sizeof(int32_t));
+  w.hc = w.krow + al256((size_t)NT * 16 * kb_max((int)GMX) * sizeof(int32_t));
+  w.hcor = w.hc + al256((size_t)NT * kb_max((int)GMX) * MS * 64 * sizeof(uint4));
+  w.total = w.hcor + al256((size_t)NT * nch_max((int)GMX) * 4 * MS * 64 * sizeof(uint4));
+  return w;
+}
+}  // namespace
+
+extern "C" size_t hsd_prefill_gemm_workspace_bytes(int64_t T, int64_t D, int64_t F, int64_t FS,
+                                                   int64_t topk, int64_t E, int64_t tt) {
+  if (T <= 0 || D <= 0 || F <= 0 || FS <= 0 || topk <= 0 || E <= 0 || (tt != 32 && tt != 64))
+    return 0;
+  return gemm_ws(T, D, F, FS, topk, E, tt).total;
 }
 
-extern "C" int hsd_prefill_gemm(const uint16_t* h, const float* gains, const int32_t* tile_e,
-                                const int32_t* tile_slot, const int32_t* ulist,
-                                const int32_t* ucount, const uint32_t* pw, const uint16_t* ps,
-                                const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
-                                const uint16_t* spb, void* y, int y_dtype, int64_t T, int64_t D,
-                                int64_t F, int64_t FS, int64_t topk, int64_t E, int64_t tt,
-                                int64_t NT, int64_t umax, void* workspace,
+extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const float* gains,
+                                const int32_t* tile_e, const int32_t* tile_slot,
+                                const int32_t* ulist, const int32_t* ucount, const uint32_t* pw,
+                                const uint16_t* ps, const uint16_t* pb, const uint32_t* spw,
+                                const uint16_t* sps, const uint16_t* spb, void* y, int y_dtype,
+                                int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk,
+                                int64_t E, int64_t tt, int64_t NT, int64_t umax, void* workspace,
                                 size_t workspace_bytes, void* stream) {
   const char* fn = "hsd_prefill_gemm";
-  if (!h || !gains || !tile_e || !tile_slot || !ulist || !ucount || !pw || !ps || !pb || !spw ||
-      !sps || !spb || !y)
+  if (!h || !sel || !gains || !tile_e || !tile_slot || !ulist || !ucount || !pw || !ps || !pb ||
+      !spw || !sps || !spb || !y)
     return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (tt != 32 && tt != 64) return set_error(HSD_ERR_SHAPE, "%s: tt must be 32 or 64", fn);
-  if (T <= 0 || D <= 0 || D % kNB || F <= 0 || F % 64 || FS <= 0 || FS % 64 || topk <= 0 || E <= 0)
+  if (T <= 0 || D <= 0 || D % 128 || F <= 0 || F % 64 || FS <= 0 || FS % 64 || topk <= 0 || E <= 0)
     return set_error(HSD_ERR_SHAPE, "%s: need D %% 128 == 0, F %% 64 == 0, FS %% 64 == 0", fn);
+  if (F / 64 > kGMax || FS / 64 > kGMax)
+    return set_error(HSD_ERR_SHAPE, "%s: F and FS must be <= %d", fn, 64 * kGMax);
   if (NT != hsd_prefill_num_tiles(T, topk, E, tt)) return set_error(HSD_ERR_SHAPE, "%s: NT mismatch", fn);
   if (umax < FS || umax < F) return set_error(HSD_ERR_SHAPE, "%s: umax must be >= FS", fn);
-  if (NT * (D / kNB) > 0x7FFFFFFF || (topk * F + FS) * T > ((int64_t)1 << 31))
+  if (NT * (D / 64) > 0x7FFFFFFF || (topk * F + FS) * T > ((int64_t)1 << 31) ||
+      (int64_t)(F > FS ? F : FS) * (D / 2) >= (int64_t)kPadRow)
     return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
   const uintptr_t al = (uintptr_t)ps | (uintptr_t)pb | (uintptr_t)sps | (uintptr_t)spb;
   if (al & 15u) return set_error(HSD_ERR_ALIGN, "%s: scales/biases must be 16-byte aligned", fn);
-  const size_t need = hsd_prefill_gemm_workspace_bytes(T, D, topk);
-  if (!workspace || workspace_bytes < need)
-    return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
+  const GemmWs w = gemm_ws(T, D, F, FS, topk, E, tt);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, w.total);
   hipStream_t st = as_stream(stream);
-  float* part = reinterpret_cast<float*>(workspace);
-  const size_t npart = (size_t)T * (topk + 1) * D;
-  hipLaunchKernelGGL(k_zero_f32, dim3(1024), dim3(256), 0, st, part, npart);
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* part = reinterpret_cast<float*>(ws + w.part);
+  int32_t* kbg = reinterpret_cast<int32_t*>(ws + w.kbg);
+  int32_t* krow = reinterpret_cast<int32_t*>(ws + w.krow);
+  uint4* hc = reinterpret_cast<uint4*>(ws + w.hc);
+  uint4* hcor = reinterpret_cast<uint4*>(ws + w.hcor);
+  const int GMX = (int)((F > FS ? F : FS) / 64);
+  if (tt == 32) {
+    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)NT), dim3(kST), 0, st, h, tile_e, tile_slot,
+                       ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
+                       (int)E, (int)umax, GMX);
+    int rc = check_launch(fn);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * (D / 128))), dim3(64), 0, st, tile_e,
+                       tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
+                       (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
+  } else {
+    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)NT), dim3(kST), 0, st, h, tile_e, tile_slot,
+                       ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
+                       (int)E, (int)umax, GMX);
+    int rc = check_launch(fn);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * (D / 64))), dim3(64), 0, st, tile_e,
+                       tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
+                       (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
+  }
   int rc = check_launch(fn);
-  if (rc) return rc;
-  const unsigned grid = (unsigned)(NT * (D / kNB));
-  if (tt == 32)
-    hipLaunchKernelGGL(k_gemm<1>, dim3(grid), dim3(kGT), 0, st, h, gains, tile_e, tile_slot,
-                       ulist, ucount, pw, ps, pb, spw, sps, spb, part, (int)D, (int)F, (int)FS,
-                       (int)topk, (int)E, (int)NT, (int)umax);
-  else
-    hipLaunchKernelGGL(k_gemm<2>, dim3(grid), dim3(kGT), 0, st, h, gains, tile_e, tile_slot,
-                       ulist, ucount, pw, ps, pb, spw, sps, spb, part, (int)D, (int)F, (int)FS,
-                       (int)topk, (int)E, (int)NT, (int)umax);
-  rc = check_launch(fn);
   if (rc) return rc;
   const unsigned sg = (unsigned)((T * D + 255) / 256);
   switch (y_dtype) {
-#define HSD_SUMS(DT)                                                                        \
-  case DT:                                                                                  \
-    hipLaunchKernelGGL(k_sum_slots<DT>, dim3(sg), dim3(256), 0, st, part,                  \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)T, (int)D, (int)(topk + 1)); \
+#define HSD_SUMS(DT)                                                                          \
+  case DT:                                                                                    \
+    hipLaunchKernelGGL(k_sum_slots<DT>, dim3(sg), dim3(256), 0, st, part, sel,               \
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)T, (int)D, (int)topk, \
+                       (int)E);                                                               \
     break;
     HSD_SUMS(HSD_DT_BF16)
     HSD_SUMS(HSD_DT_F16)

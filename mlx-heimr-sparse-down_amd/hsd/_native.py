@@ -36,8 +36,8 @@ _SIGS = {
     "hsd_prefill_tiles_workspace_bytes": (_c_size, [_c_i64] * 3),
     "hsd_prefill_tiles": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "hsd_prefill_union": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp] + [_c_i64] * 8 + [_vp]),
-    "hsd_prefill_gemm_workspace_bytes": (_c_size, [_c_i64] * 3),
-    "hsd_prefill_gemm": (_c_int, [_vp] * 13 + [_c_int] + [_c_i64] * 9 + [_vp, _c_size, _vp]),
+    "hsd_prefill_gemm_workspace_bytes": (_c_size, [_c_i64] * 7),
+    "hsd_prefill_gemm": (_c_int, [_vp] * 14 + [_c_int] + [_c_i64] * 9 + [_vp, _c_size, _vp]),
     "hsd_mamba_workspace_bytes": (_c_size, [_c_i64] * 3),
     "hsd_mamba_verify": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64] + [_vp] * 9 + [_c_i64, _vp, _c_int]
                          + [_c_i64] * 6 + [_c_float] * 3 + [_vp, _c_size, _vp]),

@@ -57,7 +57,7 @@ def sparse_down_prefill(h, sel, gains, pw, ps, pb, spw, sps, spb, *, F, FS, D, t
     """hsd/prefill.py:294-321. h [T, topk*F + FS] bf16, sel [T, topk] int32,
     gains [T, topk+1] f32 -> y [T, D] (out_dtype, default h.dtype). tt in {32, 64}:
     slots per tile. nb / kc / nsg are Metal tile knobs, accepted and ignored (the HIP
-    GEMM uses 128-column blocks, 64-row K chunks and 4 waves)."""
+    GEMM uses one wavefront per 128-column block (64 for tt=64) and 16-row k-blocks)."""
     del nb, nsg
     if h.dtype != torch.bfloat16:
         raise N.HSDError("sparse_down_prefill takes bf16 activations (the MFMA operand type)")
@@ -70,8 +70,10 @@ def sparse_down_prefill(h, sel, gains, pw, ps, pb, spw, sps, spb, *, F, FS, D, t
     gains = N.contig(gains.to(torch.float32))
     od = out_dtype or h.dtype
     y = torch.empty((T, D), dtype=od, device=h.device)
-    ws = _workspace(N.lib().hsd_prefill_gemm_workspace_bytes(T, D, topk), h.device, workspace)
-    N.call("hsd_prefill_gemm", N.ptr(h), N.ptr(gains), N.ptr(N.contig(tile_e)), N.ptr(N.contig(tile_slot)),
+    ws = _workspace(N.lib().hsd_prefill_gemm_workspace_bytes(T, D, F, FS, topk, E, tt), h.device,
+                    workspace)
+    sel = N.contig(sel.to(torch.int32))
+    N.call("hsd_prefill_gemm", N.ptr(h), N.ptr(sel), N.ptr(gains), N.ptr(N.contig(tile_e)), N.ptr(N.contig(tile_slot)),
            N.ptr(N.contig(ulist)), N.ptr(N.contig(ucount)), N.ptr(N.as_words(N.contig(pw))),
            N.ptr(N.contig(ps)), N.ptr(N.contig(pb)), N.ptr(N.as_words(N.contig(spw))),
            N.ptr(N.contig(sps)), N.ptr(N.contig(spb)), N.ptr(y), N.dtype_tag(od), T, D, F, FS, topk,

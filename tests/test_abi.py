@@ -62,8 +62,10 @@ def test_argument_errors_are_reported():
     assert lib.hsd_mamba_verify(*([dummy, 10304] * 3), *([dummy] * 9), 4, dummy, 0,
                                 3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, dummy, 1 << 20, None) == -2  # N != 128
     assert lib.hsd_mamba_select_row(dummy, None, 4, 4, None) == -1                 # n_keep >= nslab
-    assert lib.hsd_prefill_gemm(*([dummy] * 13), 0, 512, 2688, 1856, 3712, 6, 128, 48, 240, 3712,
+    assert lib.hsd_prefill_gemm(*([dummy] * 14), 0, 512, 2688, 1856, 3712, 6, 128, 48, 240, 3712,
                                 dummy, 1 << 30, None) == -2                          # tt = 48
+    assert lib.hsd_prefill_gemm(*([dummy] * 14), 0, 512, 2688, 1856, 4096, 6, 128, 32, 240, 4096,
+                                dummy, 1 << 30, None) == -2                          # FS > 4032
 
 
 def test_workspace_sizes():
@@ -74,7 +76,15 @@ def test_workspace_sizes():
     assert lib.hsd_prefill_num_tiles(512, 6, 128, 32) == 240
     assert lib.hsd_prefill_num_tiles(512, 6, 128, 64) == 184
     assert lib.hsd_prefill_num_tiles(2048, 6, 128, 32) == 576
-    assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 6) == 512 * 7 * 2688 * 4
+    # partials [T*7, D] f32, then per tile: group starts (59), padded rows (16 per k-block,
+    # 4*58+3 k-blocks), A fragments (1 KiB per k-block), correction fragments (4 x 4 KiB)
+    def al(x):
+        return (x + 255) // 256 * 256
+    kb = 4 * 58 + 3
+    want = (al(512 * 7 * 2688 * 4) + al(240 * 59 * 4) + al(240 * 16 * kb * 4) + al(240 * kb * 1024)
+            + al(240 * 4 * 4 * 1024))
+    assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 32) == want
+    assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 48) == 0
     assert lib.hsd_mamba_workspace_bytes(3, 64, 64) == 3 * 4096 * 4
 
 

@@ -65,3 +65,45 @@ def test_prefill_gemm_matches_oracle(layer, dev, T, tt, zf):
     print(f"T={T} tt={tt}: max|ref| {scale:.2f} max abs err {err.max():.3e} rel {err.max() / scale:.2e}")
     assert err.max() <= 1e-2 * scale
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref))
+    # exact 4-bit operands and fp32 group sums leave far less than the bound: a dropped
+    # bias or offset-correction term would show here
+    assert err.max() <= 1e-4 * scale
+
+
+@pytest.mark.parametrize("tt", [32, 64])
+def test_prefill_gemm_small_shapes(dev, tt):
+    """D=256, F=128, FS=192, 8 experts, top-2: two and three 64-row groups, two column
+    blocks; dense, sparse and all-zero activations."""
+    d, f, fs, e, k, T = 256, 128, 192, 8, 2, 70
+    lay = S.moe_layer_np(5, n_experts=e, d=d, f=f, fs=fs)
+    dv = {n: S.to_device(v, dev) for n, v in lay.items()}
+    nm = layout.to_neuron_major(dv["w"], dv["s"], dv["b"]) + layout.to_neuron_major(dv["sw"], dv["ss"], dv["sb"])
+    nm_np = O.to_neuron_major(lay["w"], lay["s"], lay["b"]) + O.to_neuron_major(lay["sw"], lay["ss"], lay["sb"])
+    for zf in (0.0, 0.7, 0.98, 1.0):
+        h, sel, gains = S.prefill_inputs_np(7, T=T, zero_frac=zf, n_experts=e, f=f, fs=fs, topk=k)
+        y = prefill.sparse_down_prefill(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev), *nm,
+                                        F=f, FS=fs, D=d, topk=k, E=e, tt=tt, out_dtype=torch.float32).cpu().numpy()
+        ref, _ = O.sparse_down_prefill(O.bf16_to_f32(h), sel, gains, *nm_np, F=f, FS=fs, D=d, topk=k, E=e, tt=tt)
+        if zf == 1.0:
+            assert np.array_equal(y, np.zeros_like(y))
+            continue
+        err = np.abs(y - ref)
+        assert err.max() <= 1e-4 * np.abs(ref).max(), (zf, err.max())
+
+
+def test_prefill_gemm_skips_bad_expert(layer, dev):
+    """A routed slot with an out-of-range expert id is in no tile and adds nothing; the
+    other slots of its token are unchanged."""
+    T = 64
+    h, sel, gains = S.prefill_inputs_np(77, T=T, zero_frac=0.9)
+    bad = sel.copy()
+    bad[5, 2] = 1000
+    run = lambda s: prefill.sparse_down_prefill(  # noqa: E731
+        S.to_device(h, dev), S.to_device(s, dev), S.to_device(gains, dev), *layer["nm"], F=F, FS=FS, D=D,
+        topk=TOPK, E=E, tt=32, out_dtype=torch.float32).cpu().numpy()
+    y = run(bad)
+    g2 = gains.copy()
+    g2[5, 2] = 0.0
+    ref, _ = O.sparse_down_prefill(O.bf16_to_f32(h), sel, g2, *layer["nm_np"], F=F, FS=FS, D=D, topk=TOPK,
+                                   E=E, tt=32)
+    assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
