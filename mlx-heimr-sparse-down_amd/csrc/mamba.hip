@@ -144,10 +144,11 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   const int ngrp = DI / NG;
   const int r = blockIdx.x / ngrp, gi = blockIdx.x - (blockIdx.x / ngrp) * ngrp;
   const int per = NG / kMT;
-  float z[8];
+  float z[8], nw[8];
   float ss = 0.0f;
-  for (int i = 0; i < per; ++i) {
+  for (int i = 0; i < per; ++i) {  // every load (activations, gate, weight) before the reduction
     const int c = gi * NG + i * kMT + threadIdx.x;
+    nw[i] = bf16_bits_to_f32(norm_w[c]);
     z[i] = y_pre[(size_t)r * DI + c] * silu_f32(bf16_bits_to_f32(gate[(size_t)r * gate_ld + c]));
     ss = fmaf(z[i], z[i], ss);
   }
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   const float inv = 1.0f / sqrtf(tot / (float)NG + eps);
   for (int i = 0; i < per; ++i) {
     const int c = gi * NG + i * kMT + threadIdx.x;
-    Elem<YDT>::store(y, (size_t)r * DI + c, (z[i] * inv) * bf16_bits_to_f32(norm_w[c]));
+    Elem<YDT>::store(y, (size_t)r * DI + c, (z[i] * inv) * nw[i]);
   }
 }
 

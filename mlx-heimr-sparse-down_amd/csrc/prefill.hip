@@ -211,10 +211,12 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 // out group by group, each group padded to whole 16-row k-blocks, so one k-block never
 // mixes two groups' scales.
 //
-//   k_stage   one workgroup per tile: group starts in the union list, the padded row
+//   k_stage   kSplit workgroups per tile, each for every kSplit-th slot: the union list
+//             copied to LDS, group starts in it, the padded row
 //             list (row byte offsets, kPadRow for padding), the A fragments of every
-//             k-block in MFMA lane order (h at the padded rows, bf16), hs[m, g] summed in
-//             union order, and the correction A fragments.
+//             k-block in MFMA lane order (h at the padded rows, bf16), hs[m, g] summed
+//             over each group's fragments in a fixed order, and the correction A
+//             fragments.
 //   k_gemm    one wavefront per (tile, column block): 128 columns for 32-slot tiles, 64
 //             for 64-slot tiles. Per k-block each lane loads 8 packed words (its 8 rows,
 //             one word column) with buffer loads, kPD k-blocks ahead of their use, turns
@@ -229,6 +231,7 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 //             expert id is out of range contribute nothing.
 constexpr int kGMax = 63;          // groups per expert (F/64, FS/64), one per lane
 constexpr int kST = 256;           // threads of the staging kernel
+constexpr int kSplit = 16;         // staging workgroups per tile (slot m goes to m % kSplit)
 constexpr int kPadRow = 0x7FFF0000;  // padding row offset: past every expert's weights
 constexpr int kPD = 3;             // k-blocks of weight words in flight per wavefront
 constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
@@ -244,112 +247,141 @@ __global__ __launch_bounds__(kST) void k_stage(
     const int32_t* __restrict__ ucount, int32_t* __restrict__ kbg, int32_t* __restrict__ krow,
     uint4* __restrict__ hc, uint4* __restrict__ hcor, int D, int F, int FS, int topk, int E,
     int umax, int GMX) {
-  constexpr int TT = 32 * MS;
-  __shared__ int hoff[TT];
-  __shared__ int gs[kGMax + 1];   // first union position of each group
-  __shared__ int kbs[kGMax + 1];  // first k-block of each group
+  constexpr int TT = 32 * MS, SPM = TT / kSplit;  // slots staged by this workgroup
+  __shared__ int uls[kGMax * 64];  // the tile's union list
+  __shared__ int gs[kGMax + 1];    // first union position of each group
+  __shared__ int kbs[kGMax + 1];   // first k-block of each group
   __shared__ int prow[16 * kb_max(kGMax)];
-  __shared__ float hsl[TT][kGMax];
-  const int tile = blockIdx.x, tid = threadIdx.x;
+  __shared__ int hoff[SPM];
+  __shared__ float hsl[SPM][kGMax];
+  __shared__ int kreal;            // k-blocks before the padding to a multiple of kPD
+  const int tile = blockIdx.x / kSplit, sp = blockIdx.x % kSplit, tid = threadIdx.x;
   const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
   int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
   const int e = tile_e[tile];
   if (e < 0) {
-    for (int g = tid; g <= GMX; g += kST) kbgT[g] = 0;
+    if (sp == 0)
+      for (int g = tid; g <= GMX; g += kST) kbgT[g] = 0;
     return;
   }
   const bool shared = e >= E;
   const int FF = shared ? FS : F, G = FF / 64;
   const int NR = topk * F + FS;
-  const int U = min(max(ucount[tile], 0), umax);
+  const int U = min(max(ucount[tile], 0), min(umax, FF));
   const int32_t* ul = ulist + (size_t)tile * umax;
-  if (tid < TT) {
-    const int s = tile_slot[tile * TT + tid];
+  for (int i = tid; i < U; i += kST) uls[i] = ul[i];
+  if (tid < SPM) {
+    const int s = tile_slot[tile * TT + sp + kSplit * tid];
     hoff[tid] = s < 0 ? -1 : (shared ? s * NR + topk * F : (s / topk) * NR + (s % topk) * F);
   }
+  __syncthreads();
   for (int g = tid; g <= G; g += kST) {  // lower bound of 64 g in the ascending list
     int lo = 0, hi = U;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (ul[mid] < 64 * g) lo = mid + 1; else hi = mid;
+      if (uls[mid] < 64 * g) lo = mid + 1; else hi = mid;
     }
     gs[g] = lo;
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int g = 0; g < G; ++g) {  // a group holds at most 64 rows (clamped: any list stays in bounds)
-      kbs[g] = run;
-      run += (min(max(gs[g + 1] - gs[g], 0), 64) + 15) >> 4;
+  if (tid < 64) {  // k-blocks per group, exclusive scan over the groups (one wavefront)
+    const int n = tid < G ? (min(max(gs[tid + 1] - gs[tid], 0), 64) + 15) >> 4 : 0;  // <= 4
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += t;
     }
-    kbs[G] = run;
+    const int run = __shfl(incl, 63, 64);
     // zero k-blocks (pad rows, A = 0) extend the last group to a multiple of kPD, so the
     // GEMM loop runs whole rounds of its prefetch ring
     const int padded = (run + kPD - 1) / kPD * kPD;
-    for (int g = G; g >= 0 && kbs[g] == run; --g) kbs[g] = padded;
+    if (tid <= G) kbs[tid] = incl - n == run ? padded : incl - n;
+    if (tid == 0) kreal = run;
   }
   __syncthreads();
-  const int nkb = kbs[G];
-  for (int g = tid; g <= GMX; g += kST) kbgT[g] = kbs[g < G ? g : G];
-  for (int p = tid; p < 16 * nkb; p += kST) {
-    int lo = 0, hi = G - 1;  // the last group whose first k-block is at or before p
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (16 * kbs[mid] <= p) lo = mid; else hi = mid - 1;
-    }
-    const int j = p - 16 * kbs[lo];
+  const int nkb = kbs[G], nreal = kreal;
+  if (sp == 0)
+    for (int g = tid; g <= GMX; g += kST) kbgT[g] = kbs[g < G ? g : G];
+  // padded row list: position 16 kbs[g] + j holds union row gs[g] + j of group g; the
+  // rest of the group's k-blocks and the trailing zero k-blocks are padding
+  for (int it = tid; it < 64 * G; it += kST) {
+    const int g = it >> 6, j = it & 63;
+    const int nb_g = min(kbs[g + 1], nreal) - kbs[g];  // real k-blocks of group g
+    if (j >= 16 * nb_g) continue;
+    const int p = 16 * kbs[g] + j;
     int r = -1;
-    if (j < min(max(gs[lo + 1] - gs[lo], 0), 64)) {
-      r = ul[gs[lo] + j];
+    if (j < min(max(gs[g + 1] - gs[g], 0), 64)) {
+      r = uls[gs[g] + j];
       if ((unsigned)r >= (unsigned)FF) r = -1;
     }
     prow[p] = r;
-    krow[(size_t)tile * KMX + p] = r >= 0 ? r * (D / 2) : kPadRow;
+    if (sp == 0) krow[(size_t)tile * KMX + p] = r >= 0 ? r * (D / 2) : kPadRow;
+  }
+  for (int p = 16 * nreal + tid; p < 16 * nkb; p += kST) {
+    prow[p] = -1;
+    if (sp == 0) krow[(size_t)tile * KMX + p] = kPadRow;
   }
   __syncthreads();
-  // A fragments: lane l of k-block kb, row block ms holds h[slot 32 ms + l%32] at the
-  // padded positions 16 kb + 8 (l/32) + 0..7; hs[m, g] in union order
-  for (int it = tid; it < TT * G; it += kST) {
-    const int m = it / G, g = it - m * G;
-    const int o = hoff[m];
-    float hs = 0.0f;
-    for (int kb = kbs[g]; kb < kbs[g + 1]; ++kb) {
+  // A fragments. Eight lanes per (slot, group) pair, one per (k-block, half) of the group:
+  // lane sub = kb offset * 2 + half gathers h[slot] at the 8 padded positions
+  // 16 kb + 8 half + 0..7, stores the fragment of MFMA lane (m % 32) + 32 half, and the
+  // pair's 8 lanes sum hs[m, g] in a fixed butterfly order.
+  const int npair = SPM * G;
+  const int nround = (npair + kST / 8 - 1) / (kST / 8);
+  for (int rd = 0; rd < nround; ++rd) {
+    const int q = rd * (kST / 8) + (tid >> 3), sub = tid & 7;
+    const int jj = q / G, g = q - (q / G) * G;
+    const int kb = q < npair ? kbs[g] + (sub >> 1) : 0;  // a group has at most 4 real k-blocks
+    const bool live = q < npair && kb < min(kbs[g + 1], nreal);
+    const int o = live ? hoff[jj] : -1;
+    const int half = sub & 1;
+    uint32_t v[8];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        uint32_t v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int r = prow[16 * kb + 8 * half + i];
-          v[i] = (o >= 0 && r >= 0) ? (uint32_t)h[(size_t)o + r] : 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hs += bf16_bits_to_f32(v[i]);
-        hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] =
-            make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
-                       v[6] | (v[7] << 16));
-      }
+    for (int i = 0; i < 8; ++i) {
+      const int r = live ? prow[16 * kb + 8 * half + i] : -1;
+      v[i] = (o >= 0 && r >= 0) ? (uint32_t)h[(size_t)o + r] : 0u;
     }
-    hsl[m][g] = hs;
+    float s8 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s8 += bf16_bits_to_f32(v[i]);
+    if (live) {
+      const int m = sp + kSplit * jj;
+      hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] =
+          make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                     v[6] | (v[7] << 16));
+    }
+    s8 += __shfl_xor(s8, 1, 64);
+    s8 += __shfl_xor(s8, 2, 64);
+    s8 += __shfl_xor(s8, 4, 64);
+    if (sub == 0 && q < npair) hsl[jj][g] = s8;
+  }
+  // the padding k-blocks (at most kPD - 1) hold zero fragments
+  for (int it = tid; it < (nkb - nreal) * SPM * 2; it += kST) {
+    const int kb = nreal + it / (2 * SPM), jj = (it >> 1) % SPM, half = it & 1;
+    const int m = sp + kSplit * jj;
+    hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] = make_uint4(0, 0, 0, 0);
   }
   __syncthreads();
-  // correction A fragments, 16 groups per chunk: sections [hs_hi, hs_lo, -128 hs_hi,
-  // -128 hs_lo]; hs = hs_hi + hs_lo to about 16 bits, -128 x is exact in bf16
+  // correction A fragments of this workgroup's slots, 16 groups per chunk: sections
+  // [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo]; hs = hs_hi + hs_lo to about 16 bits, -128 x
+  // is exact in bf16
   const int NCH = (G + 15) >> 4;
-  for (int it = tid; it < NCH * 4 * MS * 64; it += kST) {
-    const int lane = it & 63, ms = (it >> 6) % MS, sec = (it / (64 * MS)) & 3,
-              ch = it / (256 * MS);
-    const int m = 32 * ms + (lane & 31), khalf = lane >> 5;
+  for (int it = tid; it < NCH * 4 * SPM * 2; it += kST) {
+    const int khalf = it & 1, jj = (it >> 1) % SPM, sec = (it / (2 * SPM)) & 3,
+              ch = it / (8 * SPM);
+    const int m = sp + kSplit * jj;
     uint32_t v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int g = 16 * ch + 8 * khalf + i;
-      const float s = g < G ? hsl[m][g] : 0.0f;
+      const float s = g < G ? hsl[jj][g] : 0.0f;
       const uint16_t hi = f32_to_bf16_bits(s);
       uint16_t b = (sec & 1) ? f32_to_bf16_bits(s - bf16_bits_to_f32(hi)) : hi;
       if (sec >= 2) b = f32_to_bf16_bits(-128.0f * bf16_bits_to_f32(b));
       v[i] = b;
     }
-    hcor[((((size_t)tile * NCHMX + ch) * 4 + sec) * MS + ms) * 64 + lane] =
+    hcor[((((size_t)tile * NCHMX + ch) * 4 + sec) * MS + (m >> 5)) * 64 + (m & 31) + 32 * khalf] =
         make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
                    v[6] | (v[7] << 16));
   }
@@ -741,7 +773,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   uint4* hcor = reinterpret_cast<uint4*>(ws + w.hcor);
   const int GMX = (int)((F > FS ? F : FS) / 64);
   if (tt == 32) {
-    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)NT), dim3(kST), 0, st, h, tile_e, tile_slot,
+    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
                        ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
                        (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
@@ -750,7 +782,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
                        (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   } else {
-    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)NT), dim3(kST), 0, st, h, tile_e, tile_slot,
+    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
                        ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
                        (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
