@@ -217,10 +217,14 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 //             k-block in MFMA lane order (h at the padded rows, bf16), hs[m, g] summed
 //             over each group's fragments in a fixed order, and the correction A
 //             fragments.
+//   k_sched   one workgroup: the GEMM's block schedule, column stripes of each expert
+//             dealt over the XCDs, longest tiles first (see the kernel).
 //   k_gemm    one wavefront per (tile, column block): 128 columns for 32-slot tiles, 64
-//             for 64-slot tiles. Per k-block each lane loads 8 packed words (its 8 rows,
-//             one word column) with buffer loads, kPD k-blocks ahead of their use, turns
-//             them into bf16 B fragments with v_perm_b32 + shift/and_or, and runs
+//             for 64-slot tiles. Per k-block each lane loads 16 bytes of one row's
+//             segment with a buffer load, kPD k-blocks ahead of their use; the words
+//             pass through a double-buffered LDS transpose to the lanes that hold their
+//             word column, which turn them into bf16 B fragments with v_perm_b32 +
+//             shift/and_or, and run
 //             v_mfma_f32_32x32x16_bf16. acc accumulates over all groups; at the end of
 //             group g, y += (s_g - s_next) * acc, which sums to sum_g s_g * acc_g (Abel
 //             summation, so acc is never cleared). Before the loop, y starts as the
@@ -233,11 +237,12 @@ constexpr int kGMax = 63;          // groups per expert (F/64, FS/64), one per l
 constexpr int kST = 256;           // threads of the staging kernel
 constexpr int kSplit = 16;         // staging workgroups per tile (slot m goes to m % kSplit)
 constexpr int kPadRow = 0x7FFF0000;  // padding row offset: past every expert's weights
-constexpr int kPD = 3;             // k-blocks of weight words in flight per wavefront
+constexpr int kPD = 8;             // k-blocks in flight per wavefront (32-slot tiles); tiles pad to it
 constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 
 // k-blocks per tile: at most 4 per group, plus the padding to a multiple of kPD
 __host__ __device__ constexpr int kb_max(int gmx) { return 4 * gmx + kPD; }
+__host__ __device__ constexpr int nkb_cap(int g) { return kb_max(g) / kPD * kPD; }
 __host__ __device__ constexpr int nch_max(int gmx) { return (gmx + 15) / 16; }
 
 template <int MS>
@@ -387,6 +392,133 @@ __global__ __launch_bounds__(kST) void k_stage(
   }
 }
 
+// The GEMM's block schedule. GEMM workgroup b runs on XCD b % 8 (the hardware deals
+// workgroups to the XCDs in turn) and takes entry xcd_remap(b, n) of blk, so XCD x owns
+// the contiguous range [start_x, start_x + q_x) of blk, q_x = n / 8 or n / 8 + 1. An
+// entry is a block, tile * nblk + nb (column block nb of the tile), or -1 (no work).
+// Work is dealt by column stripe: span consecutive column blocks of one expert, 128
+// bytes of each weight row (whole cache lines). The tiles of an expert read the same
+// weight bytes in a stripe, so a stripe stays on one XCD with its tiles side by side in
+// the dispatch order, where they share those bytes in the XCD's L2. An expert deals its
+// stripes to the XCDs in turn, starting as many XCDs further on than the expert before
+// it as it has stripes (so the remainders rotate), which gives every XCD nearly the same
+// share of every expert. Within an XCD the experts come in descending order of their
+// largest tile and then by id: the longest blocks start first and the launch ends on
+// short ones. When the blocks do not fit the XCD ranges (too few empty tiles to spare),
+// blk is the identity. Only the schedule depends on blk; every block writes its own
+// outputs.
+constexpr int kOT = 1024;
+constexpr int kOrderMaxE = kOT - 1;  // experts the schedule supports (E + 1 runs <= kOT)
+__global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_e,
+                                               const int32_t* __restrict__ kbg,
+                                               int32_t* __restrict__ blk, int NT, int nblk,
+                                               int span, int F, int FS, int E, int GMX) {
+  __shared__ __attribute__((aligned(16))) int rkey[kOT];
+  __shared__ int rlen[kOT], rmax[kOT], rrank[kOT], byrank[kOT], rcnt[kOT];
+  __shared__ int base[kXcds][kOT];  // per XCD: blocks of the higher-ranked experts
+  __shared__ int wsum[kOT / 64][kXcds], wbase[kOT / 64][kXcds];
+  __shared__ int tot[kXcds], st[kXcds + 1];
+  const int tid = threadIdx.x, R = E + 1, n = NT * nblk;  // run r = expert r (r = E: shared)
+  const int q = n / kXcds, rr = n % kXcds;
+  rlen[tid] = 0;
+  rmax[tid] = 0;
+  rcnt[tid] = 0;
+  byrank[tid] = -1;
+  if (tid <= kXcds) st[tid] = tid < rr ? tid * (q + 1) : rr * (q + 1) + (tid - rr) * q;
+  __syncthreads();
+  for (int t = tid; t < NT; t += kOT) {
+    // both candidate k-block totals are loaded with the expert id (one round trip)
+    const int32_t* kg = kbg + (size_t)t * (GMX + 1);
+    const int e = tile_e[t], kr = kg[F / 64], ks = kg[FS / 64];
+    if (e < 0 || e > E) continue;
+    atomicAdd(&rlen[e], 1);
+    atomicMax(&rmax[e], min(max(e >= E ? ks : kr, 0), nkb_cap(GMX)));
+  }
+  __syncthreads();
+  // unique keys, larger first: the largest tile, then the lower id; -1 for no tiles
+  rkey[tid] = tid < R && rlen[tid] > 0 ? (rmax[tid] << 10 | (kOT - 1 - tid)) : -1;
+  __syncthreads();
+  if (rkey[tid] >= 0) {
+    const int k = rkey[tid];
+    const int4* k4 = reinterpret_cast<const int4*>(rkey);
+    int rk = 0;
+#pragma unroll 4
+    for (int r = 0; r < (R + 3) / 4; ++r) {
+      const int4 u = k4[r];
+      rk += (u.x > k) + (u.y > k) + (u.z > k) + (u.w > k);
+    }
+    rrank[tid] = rk;
+    byrank[rk] = tid;
+  }
+  __syncthreads();
+  // blocks the expert of rank tid puts on each XCD, and their exclusive prefix over ranks.
+  // Stripe u (column blocks u*span ..) goes to XCD (u + off) % 8; the last may be short.
+  const int U = (nblk + span - 1) / span, last = nblk - (U - 1) * span;
+  int v[kXcds], inc[kXcds];
+  const int off = (tid * U) & (kXcds - 1), me = byrank[tid];
+#pragma unroll
+  for (int x = 0; x < kXcds; ++x) {
+    const int x0 = (x - off) & (kXcds - 1);
+    const int nu = x0 < U ? (U - 1 - x0) / kXcds + 1 : 0;
+    const int nbx = nu * span - ((U - 1) % kXcds == x0 ? span - last : 0);
+    v[x] = me >= 0 ? rlen[me] * nbx : 0;
+    inc[x] = v[x];
+  }
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) {
+      const int u = __shfl_up(inc[x], s, 64);
+      if (lane >= s) inc[x] += u;
+    }
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) wsum[wv][x] = inc[x];
+  }
+  __syncthreads();
+  if (tid < kXcds) {
+    int s = 0;
+    for (int w = 0; w < kOT / 64; ++w) {
+      wbase[w][tid] = s;
+      s += wsum[w][tid];
+    }
+    tot[tid] = s;
+  }
+  __syncthreads();
+  bool fits = true;
+#pragma unroll
+  for (int x = 0; x < kXcds; ++x) {
+    base[x][tid] = wbase[wv][x] + inc[x] - v[x];
+    fits = fits && tot[x] <= st[x + 1] - st[x];
+  }
+  __syncthreads();
+  if (!fits) {  // identity: entry l is block l where its tile has an expert
+    for (int l = tid; l < n; l += kOT) {
+      const int e = tile_e[l / nblk];
+      blk[l] = e >= 0 && e <= E ? l : -1;
+    }
+    return;
+  }
+  for (int l = tid; l < n; l += kOT) {  // the unused tail of each XCD's range
+    int x = 0;
+#pragma unroll
+    for (int y = 1; y < kXcds; ++y) x += l >= st[y];
+    if (l - st[x] >= tot[x]) blk[l] = -1;
+  }
+  for (int t = tid; t < NT; t += kOT) {
+    const int e = tile_e[t];
+    if (e < 0 || e > E) continue;
+    const int k = atomicAdd(&rcnt[e], 1), i = rrank[e], L = rlen[e];
+    const int o = (i * U) & (kXcds - 1);
+    for (int nb = 0; nb < nblk; ++nb) {
+      const int u = nb / span, j = nb - u * span, x = (u + o) & (kXcds - 1);
+      blk[st[x] + base[x][i] + ((u / kXcds) * span + j) * L + k] = t * nblk + nb;
+    }
+  }
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(bf16x8, make_uint4(a, b, c, d));
 }
@@ -400,16 +532,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const uint4* __restrict__ hcor, const uint32_t* __restrict__ pw,
     const uint16_t* __restrict__ ps, const uint16_t* __restrict__ pb,
     const uint32_t* __restrict__ spw, const uint16_t* __restrict__ sps,
-    const uint16_t* __restrict__ spb, float* __restrict__ part, int D, int F, int FS, int topk,
-    int E, int NT, int GMX) {
+    const uint16_t* __restrict__ spb, float* __restrict__ part, const int32_t* __restrict__ blk,
+    int D, int F, int FS, int topk, int E, int NT, int GMX) {
   constexpr int TT = 32 * MS, NWC = 16 / MS, NMF = 4 / MS, NCOL = 8 * NWC;
   constexpr int RP = 40;  // ring pitch per column (bf16): b of 16 groups, s of 16 groups, pad
   // LDS: first the correction ring [NCOL][RP], then the scale table [G][NCOL] of this block
   constexpr int kLds = NCOL * RP > kGMax * NCOL ? NCOL * RP : kGMax * NCOL;
   __shared__ __attribute__((aligned(16))) uint16_t ring[kLds];
+  // k-block words in transit: [word column][row], pitch 20 (conflict-free 4-byte writes)
+  constexpr int TP = 20;
+  __shared__ __attribute__((aligned(16))) uint32_t tbuf[2][NWC * TP];  // double buffered
+  constexpr int PD = MS == 1 ? kPD : kPD / 2;  // register ring depth (a divisor of kPD)
+  constexpr int LPR = NWC / 4;                 // lanes loading one row segment, 16 B each
   const int nblk = D / NCOL;
-  const int logical = xcd_remap((int)blockIdx.x, NT * nblk);
-  const int tile = logical / nblk, nb = logical - (logical / nblk) * nblk;
+  const int bv = blk[xcd_remap((int)blockIdx.x, NT * nblk)];
+  if (bv < 0) return;
+  const int tile = bv / nblk, nb = bv - (bv / nblk) * nblk;
   const int e = tile_e[tile];
   if (e < 0) return;
   const bool shared = e >= E;
@@ -418,6 +556,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
   const int n0 = nb * NCOL;
   const int lcol = 8 * c + NMF * jq;  // first of this lane's NMF columns within the block
+  // the partial row and gain of slot l of the tile (lanes past TT repeat a slot), loaded
+  // here and passed to the epilogue through LDS
+  __shared__ int2 sinfo[TT];
+  const int sl = tile_slot[(size_t)tile * TT + (l & (TT - 1))];
+  const int gi = sl < 0 ? -1 : shared ? sl * (topk + 1) + topk : (sl / topk) * (topk + 1) + (sl % topk);
+  const float gn = gains[max(gi, 0)];
   const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
   const int kv = l <= G ? kbgT[l] : 0;
   const int kn = l < G ? kbgT[l + 1] : 0;
@@ -447,7 +591,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const uint16_t* bb = (shared ? spb : pb + (size_t)e * (F / 64) * D) + n0 + lcol;
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, FF * (D / 2), 0x00020000);
-    const uint32_t colbyte = (uint32_t)(n0 / 8 + c) * 4u;
+    const int lr = (l / LPR) & 15, la = l % LPR;     // this lane's row and 16-byte piece
+    const uint32_t colbyte = (uint32_t)(n0 / 8) * 4u + 16u * (uint32_t)la;
     // the nibble mask as an opaque register, so (x & mask) | magic is one v_and_or_b32
     // (two literal operands would not fit the instruction)
     uint32_t nmask;
@@ -455,35 +600,39 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const uint32_t bsel = MS == 1 ? 2u * jq : (uint32_t)jq;
     const uint32_t psel = MS == 1 ? (bsel | (bsel + 1) << 8 | (bsel + 4) << 16 | (bsel + 5) << 24)
                                   : (bsel | 0x0C00u | (bsel + 4) << 16 | 0x0C000000u);
-    const int32_t* kr = krow + (size_t)tile * KMX + 8 * khalf;
+    const int32_t* kr = krow + (size_t)tile * KMX + lr;
     const uint4* ha = hc + (size_t)tile * KBMX * MS * 64 + l;
     const uint4* hq = hcor + (size_t)tile * NCHMX * 4 * MS * 64 + l;
 
     // The correction sum_g [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo] x [b, b, s, s], 16 groups
     // at a time: the groups' b and s rows of this column block go through the LDS ring
-    // [column][b of 16 groups | s of 16 groups | pad], then 4 MFMA k-blocks start y.
+    // [column][b of 16 groups | s of 16 groups | pad], then 4 MFMA k-blocks start y. The
+    // next chunk's loads are in flight while a chunk is processed. Loads are never
+    // conditional (a branch around a load makes the compiler wait for every load at the
+    // merge): rows past G re-read row G - 1 and are zeroed, chunks past the last re-read it.
     const int NCH = (G + 15) >> 4;
-    for (int ch = 0; ch < NCH; ++ch) {
-      uint4 a[4][MS];
+    constexpr int V8 = NCOL / 8;       // uint4 pieces per row segment
+    constexpr int NIT = 32 * V8 / 64;  // 32 row segments (b, s of 16 groups)
+    auto load_chunk = [&](int ch, uint4 (&a)[4][MS], uint4 (&v)[NIT]) {
 #pragma unroll
       for (int sec = 0; sec < 4; ++sec)
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) a[sec][ms] = hq[(((size_t)ch * 4 + sec) * MS + ms) * 64];
-      constexpr int V8 = NCOL / 8;           // uint4 pieces per row segment
-      constexpr int NIT = 32 * V8 / 64;      // 32 row segments (b, s of 16 groups)
-      uint4 v[NIT];
 #pragma unroll
       for (int t = 0; t < NIT; ++t) {
         const int item = l + 64 * t, r = item / V8, c8 = item % V8;
-        const int gg = 16 * ch + (r & 15);
-        const uint16_t* src = (r < 16 ? bb : sb) - lcol + (size_t)gg * D + 8 * c8;
-        v[t] = gg < G ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+        const int gg = min(16 * ch + (r & 15), G - 1);
+        v[t] = *reinterpret_cast<const uint4*>((r < 16 ? bb : sb) - lcol + (size_t)gg * D + 8 * c8);
       }
+    };
+    auto process = [&](int ch, const uint4 (&a)[4][MS], const uint4 (&v)[NIT]) {
       __syncthreads();
 #pragma unroll
       for (int t = 0; t < NIT; ++t) {
         const int item = l + 64 * t, r = item / V8, c8 = item % V8;
-        const uint32_t w[4] = {v[t].x, v[t].y, v[t].z, v[t].w};
+        const bool live = 16 * ch + (r & 15) < G;
+        const uint32_t w[4] = {live ? v[t].x : 0u, live ? v[t].y : 0u, live ? v[t].z : 0u,
+                               live ? v[t].w : 0u};
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           ring[(8 * c8 + j) * RP + 16 * (r >> 4) + (r & 15)] =
@@ -499,18 +648,40 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           for (int ms = 0; ms < MS; ++ms)
             y[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[sec][ms]), as_bf16x8(bv), y[ms][i], 0, 0, 0);
         }
+    };
+    // Chunks go in pairs; a chunk past the last one (odd NCH) has all rows zeroed and adds
+    // exact zeros. Nothing is conditional, so no load sinks into a branch, and the
+    // scheduling barriers keep each chunk's loads ahead of the work before them.
+    {
+      uint4 a0[4][MS], v0[NIT], a1[4][MS], v1[NIT];
+      load_chunk(0, a0, v0);
+      for (int ch = 0; ch < NCH; ch += 2) {
+        load_chunk(min(ch + 1, NCH - 1), a1, v1);
+        __builtin_amdgcn_sched_barrier(0);
+        process(ch, a0, v0);
+        load_chunk(min(ch + 2, NCH - 1), a0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        process(ch + 1, a1, v1);
+      }
     }
 
     // the scale table s[g][n0 .. n0 + NCOL) of all groups, so that the k-block loop issues
-    // no global load inside its group-end branch
-    __syncthreads();
+    // no global load inside its group-end branch: every load first, then the stores.
+    // Pieces past the table repeat its last piece (same source, same place).
     {
-      constexpr int V8 = NCOL / 8;
-      for (int idx = l; idx < G * V8; idx += 64) {
-        const int gg = idx / V8, c8 = idx % V8;
-        *reinterpret_cast<uint4*>(&ring[gg * NCOL + 8 * c8]) =
-            *reinterpret_cast<const uint4*>(sb - lcol + (size_t)gg * D + 8 * c8);
+      constexpr int NST = (kGMax * V8 + 63) / 64;
+      uint32_t sv[NST][4];
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < NST; ++t) {
+        const int idx = min(l + 64 * t, G * V8 - 1), gg = idx / V8, c8 = idx % V8;
+        const uint4 u = *reinterpret_cast<const uint4*>(sb - lcol + (size_t)gg * D + 8 * c8);
+        sv[t][0] = u.x; sv[t][1] = u.y; sv[t][2] = u.z; sv[t][3] = u.w;
       }
+#pragma unroll
+      for (int t = 0; t < NST; ++t)  // piece idx = (g, c8) goes to ring[g * NCOL + 8 * c8]
+        *reinterpret_cast<uint4*>(&ring[8 * min(l + 64 * t, G * V8 - 1)]) =
+            make_uint4(sv[t][0], sv[t][1], sv[t][2], sv[t][3]);
     }
     __syncthreads();
     auto scales = [&](int g, float (&s)[NMF]) {  // this lane's NMF scales of group g
@@ -530,44 +701,63 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     float scur[NMF];
     scales(g, scur);
 
-    int4 rq[kPD][2];
-    uint32_t wq[kPD][8];
-    uint4 aq[kPD][MS];
-    auto load_rows = [&](int kb, int4 (&r)[2]) {
-      r[0] = *reinterpret_cast<const int4*>(kr + 16 * kb);
-      r[1] = *reinterpret_cast<const int4*>(kr + 16 * kb + 4);
-    };
-    auto load_words = [&](int kb, const int4 (&r)[2], uint32_t (&w)[8], uint4 (&a)[MS]) {
-      const int ro[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        w[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, (uint32_t)ro[i] + colbyte, 0, 0);
+    // Register ring of PD k-blocks: per lane one row offset, one 16-byte piece of a row
+    // segment (4 lanes per 64-byte segment) and the A fragment(s). A k-block's words
+    // reach their lanes through tbuf one step before use.
+    int rq[PD];
+    uint4 wq[PD];
+    uint4 aq[PD][MS];
+    uint32_t w8[8];  // this lane's 8 words (rows 8 khalf + 0..7, word column c)
+    auto load_row = [&](int kb, int& r) { r = kr[16 * kb]; };
+    auto load_kb = [&](int kb, int r, uint4& w, uint4 (&a)[MS]) {
+      // 16-byte aligned: row offsets are multiples of D/2 = 16 * D/32, colbyte of 16
+      w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)r + colbyte, 0, 0));
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) a[ms] = ha[((size_t)kb * MS + ms) * 64];
+    };
+    // A k-block's words reach their lanes through tbuf[kb & 1]: written two steps and read
+    // one step before use, so the LDS round trip hides behind a step's work. One
+    // wavefront per workgroup executes its LDS operations in order.
+    auto put = [&](int buf, const uint4& w) {  // row lr, words 4 la .. 4 la + 3
+      tbuf[buf][(4 * la + 0) * TP + lr] = w.x;
+      tbuf[buf][(4 * la + 1) * TP + lr] = w.y;
+      tbuf[buf][(4 * la + 2) * TP + lr] = w.z;
+      tbuf[buf][(4 * la + 3) * TP + lr] = w.w;
+    };
+    auto get = [&](int buf) {  // this lane's rows 8 khalf + 0..7 of word column c
+      const uint4 u0 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + 8 * khalf]);
+      const uint4 u1 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + 8 * khalf + 4]);
+      w8[0] = u0.x; w8[1] = u0.y; w8[2] = u0.z; w8[3] = u0.w;
+      w8[4] = u1.x; w8[5] = u1.y; w8[6] = u1.z; w8[7] = u1.w;
     };
     // Prefetches past the last k-block re-read the last one (in bounds, never used), so
     // every path issues the same loads and the waits stay partial.
     const int klast = nkb - 1;
 #pragma unroll
-    for (int d = 0; d < kPD; ++d) load_rows(min(d, klast), rq[d]);
+    for (int d = 0; d < PD; ++d) load_row(min(d, klast), rq[d]);
     // issue order = consumption order (slot 0 first), so the loop's waits stay partial
 #pragma unroll
-    for (int d = 0; d < kPD; ++d) {
+    for (int d = 0; d < PD; ++d) {
       __builtin_amdgcn_sched_barrier(0);
-      load_words(min(d, klast), rq[d], wq[d], aq[d]);
-      load_rows(min(d + kPD, klast), rq[d]);
+      load_kb(min(d, klast), rq[d], wq[d], aq[d]);
+      load_row(min(d + PD, klast), rq[d]);
     }
     __builtin_amdgcn_sched_barrier(0);
+    put(0, wq[0]);
+    put(1, wq[1]);
+    __builtin_amdgcn_wave_barrier();
+    get(0);
+    __builtin_amdgcn_wave_barrier();
 
-    for (int kb0 = 0; kb0 < nkb; kb0 += kPD) {
+    for (int kb0 = 0; kb0 < nkb; kb0 += PD) {
 #pragma unroll
-      for (int d = 0; d < kPD; ++d) {  // nkb is a multiple of kPD
+      for (int d = 0; d < PD; ++d) {  // nkb is a multiple of PD
         const int kb = kb0 + d;
         // B fragments: P_i holds column lcol + i of rows (2p, 2p+1) as bf16 128 + q
         uint32_t bf[NMF][4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-          const uint32_t x = __builtin_amdgcn_perm(wq[d][2 * p + 1], wq[d][2 * p], psel);
+          const uint32_t x = __builtin_amdgcn_perm(w8[2 * p + 1], w8[2 * p], psel);
 #pragma unroll
           for (int i = 0; i < NMF; ++i) bf[i][p] = ((x >> (4 * i)) & nmask) | kMagic;
         }
@@ -578,8 +768,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           for (int ms = 0; ms < MS; ++ms)
             acc[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(aq[d][ms]), bv, acc[ms][i], 0, 0, 0);
         }
-        load_words(min(kb + kPD, klast), rq[d], wq[d], aq[d]);
-        load_rows(min(kb + 2 * kPD, klast), rq[d]);
+        load_kb(min(kb + PD, klast), rq[d], wq[d], aq[d]);
+        load_row(min(kb + 2 * PD, klast), rq[d]);
+        // The wave barriers order the lanes' LDS accesses for the compiler and document
+        // the wavefront-synchronous exchange (no instruction is emitted).
+        put(d & 1, wq[(d + 2) % PD]);  // k-block kb + 2 (loaded PD - 2 steps ago)
+        __builtin_amdgcn_wave_barrier();
+        get((d + 1) & 1);              // k-block kb + 1 (written one step ago)
+        __builtin_amdgcn_wave_barrier();
         if (kb + 1 == gend) {  // end of group g: y += (s_g - s_next) * acc
           const uint64_t rest = nonempty & ~((2ull << g) - 1ull);
           const int gp = rest ? __builtin_ctzll(rest) : -1;
@@ -607,16 +803,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
 
   // epilogue: C[i][j], j = lane%32 -> column lcol + i, row 32 ms + 8 (v/4) + 4 (lane/32) + v%4
+  if (l < TT) sinfo[l] = make_int2(gi, __float_as_int(gn));
+  __syncthreads();
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int m = 32 * ms + 8 * (v >> 2) + 4 * khalf + (v & 3);
-      const int s = tile_slot[tile * TT + m];
-      if (s < 0) continue;
-      const int gi = shared ? s * (topk + 1) + topk : (s / topk) * (topk + 1) + (s % topk);
-      const float gn = gains[gi];
-      float* dst = part + (size_t)gi * D + n0 + lcol;
+      const int2 si = sinfo[32 * ms + 8 * (v >> 2) + 4 * khalf + (v & 3)];
+      if (si.x < 0) continue;
+      const float gn = __int_as_float(si.y);
+      float* dst = part + (size_t)si.x * D + n0 + lcol;
       if constexpr (NMF == 4)
         *reinterpret_cast<float4*>(dst) =
             make_float4(gn * y[ms][0][v], gn * y[ms][1][v], gn * y[ms][2][v], gn * y[ms][3][v]);
@@ -711,9 +907,10 @@ extern "C" int hsd_prefill_union(const void* h, int h_dtype, const int32_t* tile
 namespace {
 // Workspace of hsd_prefill_gemm, in this order, each piece 256-byte aligned:
 //   part [T*(topk+1), D] f32 | kbg [NT, GMX+1] i32 | krow [NT, 16 KB] i32 |
-//   hc [NT, KB, MS, 64] uint4 | hcor [NT, ceil(GMX/16), 4, MS, 64] uint4, KB = kb_max(GMX)
+//   hc [NT, KB, MS, 64] uint4 | hcor [NT, ceil(GMX/16), 4, MS, 64] uint4 |
+//   blk [NT * D * MS / 128] i32 (the GEMM's block schedule), KB = kb_max(GMX)
 struct GemmWs {
-  size_t part, kbg, krow, hc, hcor, total;
+  size_t part, kbg, krow, hc, hcor, blk, total;
 };
 inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E, int64_t tt) {
@@ -725,7 +922,8 @@ GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_
   w.krow = w.kbg + al256((size_t)NT * (GMX + 1) * sizeof(int32_t));
   w.hc = w.krow + al256((size_t)NT * 16 * kb_max((int)GMX) * sizeof(int32_t));
   w.hcor = w.hc + al256((size_t)NT * kb_max((int)GMX) * MS * 64 * sizeof(uint4));
-  w.total = w.hcor + al256((size_t)NT * nch_max((int)GMX) * 4 * MS * 64 * sizeof(uint4));
+  w.blk = w.hcor + al256((size_t)NT * nch_max((int)GMX) * 4 * MS * 64 * sizeof(uint4));
+  w.total = w.blk + al256((size_t)NT * (D * MS / 128) * sizeof(int32_t));
   return w;
 }
 }  // namespace
@@ -756,6 +954,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
     return set_error(HSD_ERR_SHAPE, "%s: F and FS must be <= %d", fn, 64 * kGMax);
   if (NT != hsd_prefill_num_tiles(T, topk, E, tt)) return set_error(HSD_ERR_SHAPE, "%s: NT mismatch", fn);
   if (umax < FS || umax < F) return set_error(HSD_ERR_SHAPE, "%s: umax must be >= FS", fn);
+  if (E > kOrderMaxE) return set_error(HSD_ERR_SHAPE, "%s: at most %d experts", fn, kOrderMaxE);
   if (NT * (D / 64) > 0x7FFFFFFF || (topk * F + FS) * T > ((int64_t)1 << 31) ||
       (int64_t)(F > FS ? F : FS) * (D / 2) >= (int64_t)kPadRow)
     return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
@@ -771,6 +970,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   int32_t* krow = reinterpret_cast<int32_t*>(ws + w.krow);
   uint4* hc = reinterpret_cast<uint4*>(ws + w.hc);
   uint4* hcor = reinterpret_cast<uint4*>(ws + w.hcor);
+  int32_t* blk = reinterpret_cast<int32_t*>(ws + w.blk);
   const int GMX = (int)((F > FS ? F : FS) / 64);
   if (tt == 32) {
     hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
@@ -778,18 +978,26 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
                        (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
     if (rc) return rc;
+    hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
+                       (int)(D / 128), 2, (int)F, (int)FS, (int)E, GMX);
+    rc = check_launch(fn);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * (D / 128))), dim3(64), 0, st, tile_e,
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
-                       (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
+                       blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   } else {
     hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
                        ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
                        (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
     if (rc) return rc;
+    hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
+                       (int)(D / 64), 4, (int)F, (int)FS, (int)E, GMX);
+    rc = check_launch(fn);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * (D / 64))), dim3(64), 0, st, tile_e,
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
-                       (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
+                       blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   }
   int rc = check_launch(fn);
   if (rc) return rc;
