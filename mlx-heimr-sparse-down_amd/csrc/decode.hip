@@ -11,10 +11,10 @@
 //     team (j, phase) owns the live rows n of group g0+j with n % 2 == phase; lane l owns
 //     weight word 16c+l (8 outputs, a 64-byte piece of every row per team).
 //       1. one round trip: the slot's expert id and gain, and the group's 64 activations
-//          (4 per lane); 4 wave ballots give the live mask and an ascending live-row
-//          list in LDS (+-0 dead, NaN live);
-//       2. one round trip: the live rows' words (4 B per lane) and, once per group, its
-//          16-byte scale and bias vectors;
+//          (4 per lane); the group's 16-byte scale and bias vectors follow as soon as the
+//          id is in, overlapping the activations' latency; 4 wave ballots give the live
+//          mask and an ascending live-row list in LDS (+-0 dead, NaN live);
+//       2. one round trip: the live rows' words (4 B per lane), up to 16 rows per team;
 //       3. acc[t] = sum h_i q_{i,t}, hsum = sum h_i (fp32); term = s*acc + b*hsum (the
 //          group factorisation of decode.py:125-128);
 //       4. terms summed in (group, phase) order, times the slot's gain -> part[b, p, chunk].
@@ -31,7 +31,7 @@ constexpr int kThreads = 256 * kRS;
 constexpr int kWPC = 16;                 // weight words per D chunk (one lane each)
 constexpr int kDC = kWPC * 8;            // outputs per D chunk
 constexpr int kGPW = 16;                 // groups per workgroup
-constexpr int kRB = (16 + kRS - 1) / kRS;  // rows per lane per batch (16 live rows a group)
+constexpr int kRB = 16;                  // rows per team per batch (a phase has 32 rows)
 
 struct Geom {
   int D, F, FS, topk, E, NR, NW;
@@ -95,21 +95,36 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   const int grp = g0 + j;
   const bool jv = j < ng;
 
-  // ---- round trip 1: expert id, gain and activations, issued together. The id/gain are
-  // fetched as vector loads (an opaque zero lane offset) so that the activation loads do
-  // not wait on them through the scalar-load counter.
+  // ---- round trip 1: expert id, gain and activations, issued together and never under a
+  // branch (a load inside a branch makes the compiler wait for all earlier loads where the
+  // paths merge). The id/gain are vector loads (an opaque zero lane offset) so that the
+  // activation loads do not wait on them through the scalar-load counter.
   int z;
   asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-  const int e = routed ? sel[b * g.topk + k + z] : 0;
+  const int eraw = sel[b * g.topk + (routed ? k : g.topk - 1) + z];  // shared: unused
   const float gain = gains[b * (g.topk + 1) + k + z];
+  const int grc = jv ? grp : g0;                     // groups past the end re-read g0, unused
   const uint32_t hoff = (uint32_t)b * (uint32_t)g.NR + (uint32_t)(routed ? k * g.F : g.topk * g.F) +
-                        (uint32_t)grp * 64u;
+                        (uint32_t)grc * 64u;
+  HT hr4[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) hr4[v] = h[hoff + 16 * v + l];
+  __builtin_amdgcn_sched_barrier(0);
+  const int e = routed ? eraw : 0;
+  const bool ok = !routed || (unsigned)e < (unsigned)g.E;
+  // the group's scale and bias vectors depend on the expert id alone: issued as soon as
+  // the id is in, while the activations are still on their way
+  const int w = c * kWPC + l;
+  const size_t es = ok ? (size_t)e : 0;
+  const uint16_t* sb = routed ? ps + es * (size_t)g.gpr * g.D : sps;
+  const uint16_t* bb = routed ? pb + es * (size_t)g.gpr * g.D : spb;
+  const size_t soff = ((size_t)grc * g.D + 8u * (uint32_t)w) * 2u;
+  const uint4 sv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(sb) + soff);
+  const uint4 bv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(bb) + soff);
+  __builtin_amdgcn_sched_barrier(0);
   HT hv[4];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) hv[v] = jv ? h[hoff + 16 * v + l] : (HT)0;
-  __builtin_amdgcn_sched_barrier(0);
-  const bool ok = !routed || (unsigned)e < (unsigned)g.E;
-  if (!ok && tid == 0 && c == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+  for (int v = 0; v < 4; ++v) hv[v] = jv ? hr4[v] : (HT)0;
 
   // ---- live mask (4 ballots over the wave's 4 teams) and the compacted row list
   const int sh = 16 * (team & 3);
@@ -135,18 +150,13 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- round trip 2: live rows of this phase, and the group's scales/biases
-  const int w = c * kWPC + l;
-  const size_t es = ok ? (size_t)e : 0;
-  const uint16_t* sb = routed ? ps + es * (size_t)g.gpr * g.D : sps;
-  const uint16_t* bb = routed ? pb + es * (size_t)g.gpr * g.D : spb;
+  // ---- round trip 2: live rows of this phase
   const uint32_t* wb = routed ? pw + es * (size_t)g.F * g.NW : spw;
   const uint32_t row0 = (uint32_t)grp * 64u * (uint32_t)g.NW + (uint32_t)w;
   float acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
   float hsum = 0.0f;
-  uint4 sv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
   const int nmine = cnt;                              // this team's rows
   int nmax = nmine;                                   // most rows of any team of the wave
   nmax = max(nmax, __shfl_xor(nmax, 16, 64));
@@ -163,11 +173,6 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
       if (idx[r] >= 0)
         q[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(wb) +
                                                   (size_t)(row0 + (uint32_t)idx[r] * (uint32_t)g.NW) * 4u);
-    }
-    if (r0 == 0 && cnt > 0) {
-      const size_t off = ((size_t)grp * g.D + 8u * (uint32_t)w) * 2u;
-      sv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(sb) + off);
-      bv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(bb) + off);
     }
     HT hr[kRB];
 #pragma unroll
@@ -226,6 +231,7 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
     for (int s = 1; s < kL1; ++s) v += sum2[tid][s];
     part[((size_t)b * g.nparts + p) * g.D + (size_t)c * kDC + tid] = gain * v;
   }
+  if (!ok && tid == 0 && c == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
 }
 
 template <int YDT, int NP>
