@@ -34,6 +34,29 @@ from hsd import _native as N  # noqa: E402
 METRIC = "batch-1 decode tok/s (sparse+MTP2); sparse-down HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.txt")
+
+
+def pmc_traffic(workload):
+    """HBM bytes per dispatch of a workload's kernel(s), from the committed rocprofv3 counter
+    summary: FETCH_SIZE x fetch_factor + WRITE_SIZE x write_factor (KiB per dispatch, factors
+    from a device copy of known size). None when the summary or its line is absent."""
+    try:
+        lines = open(TRAFFIC_SUMMARY).read().splitlines()
+    except OSError:
+        return None
+    fields = {}
+    for ln in lines:
+        tok = ln.split()
+        if tok[:1] == ["calibration"]:
+            fields["cal"] = dict(t.split("=", 1) for t in tok[1:])
+        elif tok[:2] == ["traffic", workload]:
+            fields["kib"] = dict(t.split("=", 1) for t in tok[2:])
+    if "cal" not in fields or "kib" not in fields:
+        return None
+    cal, kib = fields["cal"], fields["kib"]
+    return int(1024 * (float(kib["fetch_kib"]) * float(cal["fetch_factor"])
+                       + float(kib["write_kib"]) * float(cal["write_factor"])))
 NL = 23                      # MoE layers
 D, F, FS, E, K = S.D, S.F, S.FS, S.E, S.TOPK
 NR = K * F + FS
@@ -265,7 +288,7 @@ def bench_decode(args):
                            zero_frac=args.zero_frac, hot_neurons=bool(args.hot), experts=E, topk=K, D=D, F=F,
                            FS=FS, group=64, tokens_rotated=ntok, weights_gb=round(NL * 364.8e6 / 1e9, 2)),
                roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                             frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                             frac=round(achieved / HBM_PEAK_GBS, 4), traffic=pmc_traffic("decode"),
                              kernel="k_sparse_down_part + k_sum_parts (one decode call)",
                              bytes_per_launch=int(per_launch_bytes), us_per_launch=round(per_launch_us, 3)),
                cpu_baseline=cpu,
@@ -341,8 +364,8 @@ def bench_prefill(args):
                 dtype="bf16 MFMA, f32 accumulate", data="synthetic",
                 config=dict(workload="prefill: 2048-token prompt in chunks of 512, Zipf(1.1) top-6 routing",
                             layers=nl, tt=tt, zero_frac=args.zero_frac),
-                roofline=dict(bound="hbm", achieved=round(tflops, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                              frac=round(tflops / BF16_PEAK_TFLOPS, 4), traffic=None,
+                roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                              frac=round(tflops / BF16_PEAK_TFLOPS, 4), traffic=pmc_traffic("prefill"),
                               hbm_frac_dense_weights=round(wbytes / (ms_gemm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
                 prefill_tok_s=round(T / (ms_all * 1e-3), 1), gflop_per_prompt=round(flops / 1e9, 2))
 
@@ -396,7 +419,8 @@ def bench_mtp(args):
                 data="synthetic",
                 config=dict(workload="MTP verify + rollback: 23 Mamba-2 layers, 3 rows, P(0,1,2)=(.15,.35,.5)"),
                 roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                              frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None, bytes_per_layer_step=per_layer))
+                              frac=round(gbs / HBM_PEAK_GBS, 4), traffic=pmc_traffic("mtp"),
+                              bytes_per_layer_step=per_layer))
 
 
 def main():

@@ -72,6 +72,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also waits for every
+// outstanding global access of the wave (the hardware counts loads and stores together),
+// which would end the flight of loads issued ahead of the barrier for later use.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
 // softplus(x) = log(1 + e^x); above 20 it equals x in fp32.

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 // out group by group, each group padded to whole 16-row k-blocks, so one k-block never
 // mixes two groups' scales.
 //
-//   k_stage   kSplit workgroups per tile, each for every kSplit-th slot: the union list
+//   k_stage   4 MS workgroups per tile, each for every (4 MS)-th slot: the union list
 //             copied to LDS, group starts in it, the padded row
 //             list (row byte offsets, kPadRow for padding), the A fragments of every
 //             k-block in MFMA lane order (h at the padded rows, bf16), hs[m, g] summed
@@ -235,7 +235,8 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
 //             expert id is out of range contribute nothing.
 constexpr int kGMax = 63;          // groups per expert (F/64, FS/64), one per lane
 constexpr int kST = 256;           // threads of the staging kernel
-constexpr int kSplit = 16;         // staging workgroups per tile (slot m goes to m % kSplit)
+// staging workgroups per tile (slot m goes to workgroup m % stage_split(MS)): 8 slots each
+__host__ __device__ constexpr int stage_split(int ms) { return 4 * ms; }
 constexpr int kPadRow = 0x7FFF0000;  // padding row offset: past every expert's weights
 constexpr int kPD = 8;             // k-blocks in flight per wavefront (32-slot tiles); tiles pad to it
 constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
@@ -250,20 +251,39 @@ __global__ __launch_bounds__(kST) void k_stage(
     const uint16_t* __restrict__ h, const int32_t* __restrict__ tile_e,
     const int32_t* __restrict__ tile_slot, const int32_t* __restrict__ ulist,
     const int32_t* __restrict__ ucount, int32_t* __restrict__ kbg, int32_t* __restrict__ krow,
-    uint4* __restrict__ hc, uint4* __restrict__ hcor, int D, int F, int FS, int topk, int E,
-    int umax, int GMX) {
-  constexpr int TT = 32 * MS, SPM = TT / kSplit;  // slots staged by this workgroup
-  __shared__ int uls[kGMax * 64];  // the tile's union list
+    uint4* __restrict__ hc, uint4* __restrict__ hcor, uint4* __restrict__ dump, int D, int F,
+    int FS, int topk, int E, int umax, int GMX) {
+  constexpr int TT = 32 * MS, kSplit = stage_split(MS), SPM = TT / kSplit;  // slots staged here
+  constexpr int NUL = (kGMax * 64 + kST - 1) / kST;  // union list entries per thread
+  // h rows of a gather batch, per slot GB groups x 64 values plus 8 of padding, so that
+  // the slots' rows start in different LDS banks: they share the union list's space
+  constexpr int GB = 16, HP = GB * 64 + 8;
+  constexpr int ULS = NUL * kST > SPM * HP / 2 ? NUL * kST : SPM * HP / 2;
+  __shared__ __attribute__((aligned(16))) int uls[ULS];  // the tile's union list (entries past
+                                                         // its end unused)
   __shared__ int gs[kGMax + 1];    // first union position of each group
   __shared__ int kbs[kGMax + 1];   // first k-block of each group
-  __shared__ int prow[16 * kb_max(kGMax)];
-  __shared__ int hoff[SPM];
+  __shared__ __attribute__((aligned(16))) int prow[16 * kb_max(kGMax)];
   __shared__ float hsl[SPM][kGMax];
   __shared__ int kreal;            // k-blocks before the padding to a multiple of kPD
   const int tile = blockIdx.x / kSplit, sp = blockIdx.x % kSplit, tid = threadIdx.x;
   const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
   int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
+  // h is gathered in batches of GB groups: a batch is every 16-byte piece (8 per group,
+  // the group's 64 values) of each of the SPM slots' rows, NLI pieces per thread.
+  constexpr int NBT = (kGMax + GB - 1) / GB;
+  constexpr int NLI = SPM * GB * 8 / kST;
+  // Two memory round trips: the tile's expert, union size and the slots of this thread's
+  // pieces; then the whole union list and every batch's pieces. Loads are never under a
+  // branch (a load inside a branch makes the compiler wait for every earlier load where
+  // the paths merge), and only LDS barriers follow them, so they stay in flight through
+  // the list work below. A dead piece (slot not in the tile, group past the expert's end)
+  // reads h[0..7]: its values reach only rows that are never written out or read.
   const int e = tile_e[tile];
+  const int ucnt = ucount[tile];
+  int slot[NLI];
+#pragma unroll
+  for (int i = 0; i < NLI; ++i) slot[i] = tile_slot[tile * TT + sp + kSplit * ((tid + kST * i) / (GB * 8))];
   if (e < 0) {
     if (sp == 0)
       for (int g = tid; g <= GMX; g += kST) kbgT[g] = 0;
@@ -272,14 +292,28 @@ __global__ __launch_bounds__(kST) void k_stage(
   const bool shared = e >= E;
   const int FF = shared ? FS : F, G = FF / 64;
   const int NR = topk * F + FS;
-  const int U = min(max(ucount[tile], 0), min(umax, FF));
+  const int U = min(max(ucnt, 0), min(umax, FF));
   const int32_t* ul = ulist + (size_t)tile * umax;
-  for (int i = tid; i < U; i += kST) uls[i] = ul[i];
-  if (tid < SPM) {
-    const int s = tile_slot[tile * TT + sp + kSplit * tid];
-    hoff[tid] = s < 0 ? -1 : (shared ? s * NR + topk * F : (s / topk) * NR + (s % topk) * F);
+  int uv[NUL];  // entries past the list's end re-read its last slot and are unused
+#pragma unroll
+  for (int i = 0; i < NUL; ++i) uv[i] = ul[min(tid + kST * i, umax - 1)];
+  uint4 pv[NBT][NLI];
+#pragma unroll
+  for (int i = 0; i < NLI; ++i) {
+    const int s = slot[i];
+    const int o = s < 0 ? -1 : (shared ? s * NR + topk * F : (s / topk) * NR + (s % topk) * F);
+    const int item = tid + kST * i, pc = item % 8;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+      const int g = GB * bt + (item / 8) % GB;
+      const bool ok = o >= 0 && g < G;
+      pv[bt][i] = *reinterpret_cast<const uint4*>(h + (ok ? (size_t)o + 64 * g + 8 * pc : 0));
+    }
   }
-  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < NUL; ++i) uls[tid + kST * i] = uv[i];
+  lds_barrier();
   for (int g = tid; g <= G; g += kST) {  // lower bound of 64 g in the ascending list
     int lo = 0, hi = U;
     while (lo < hi) {
@@ -288,7 +322,7 @@ __global__ __launch_bounds__(kST) void k_stage(
     }
     gs[g] = lo;
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < 64) {  // k-blocks per group, exclusive scan over the groups (one wavefront)
     const int n = tid < G ? (min(max(gs[tid + 1] - gs[tid], 0), 64) + 15) >> 4 : 0;  // <= 4
     int incl = n;
@@ -304,12 +338,13 @@ __global__ __launch_bounds__(kST) void k_stage(
     if (tid <= G) kbs[tid] = incl - n == run ? padded : incl - n;
     if (tid == 0) kreal = run;
   }
-  __syncthreads();
+  lds_barrier();
   const int nkb = kbs[G], nreal = kreal;
   if (sp == 0)
     for (int g = tid; g <= GMX; g += kST) kbgT[g] = kbs[g < G ? g : G];
   // padded row list: position 16 kbs[g] + j holds union row gs[g] + j of group g; the
   // rest of the group's k-blocks and the trailing zero k-blocks are padding
+#pragma unroll 4
   for (int it = tid; it < 64 * G; it += kST) {
     const int g = it >> 6, j = it & 63;
     const int nb_g = min(kbs[g + 1], nreal) - kbs[g];  // real k-blocks of group g
@@ -327,39 +362,60 @@ __global__ __launch_bounds__(kST) void k_stage(
     prow[p] = -1;
     if (sp == 0) krow[(size_t)tile * KMX + p] = kPadRow;
   }
-  __syncthreads();
-  // A fragments. Eight lanes per (slot, group) pair, one per (k-block, half) of the group:
-  // lane sub = kb offset * 2 + half gathers h[slot] at the 8 padded positions
-  // 16 kb + 8 half + 0..7, stores the fragment of MFMA lane (m % 32) + 32 half, and the
-  // pair's 8 lanes sum hs[m, g] in a fixed butterfly order.
-  const int npair = SPM * G;
-  const int nround = (npair + kST / 8 - 1) / (kST / 8);
-  for (int rd = 0; rd < nround; ++rd) {
-    const int q = rd * (kST / 8) + (tid >> 3), sub = tid & 7;
-    const int jj = q / G, g = q - (q / G) * G;
-    const int kb = q < npair ? kbs[g] + (sub >> 1) : 0;  // a group has at most 4 real k-blocks
-    const bool live = q < npair && kb < min(kbs[g + 1], nreal);
-    const int o = live ? hoff[jj] : -1;
-    const int half = sub & 1;
-    uint32_t v[8];
+  lds_barrier();
+  // A fragments, a batch of GB groups at a time: its pieces (loaded above) go to LDS over
+  // the union list, no longer needed, and the 8 lanes of a (slot, group) sum hs[m, g] in a
+  // fixed butterfly order (a column outside the union is zero in every slot of the tile,
+  // so the sum over the row is the sum over the union); then each fragment (slot,
+  // k-block, half) picks its 8 padded rows from LDS.
+  uint16_t* hbuf = reinterpret_cast<uint16_t*>(uls);  // [SPM][HP]: group gl at gl * 64
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = live ? prow[16 * kb + 8 * half + i] : -1;
-      v[i] = (o >= 0 && r >= 0) ? (uint32_t)h[(size_t)o + r] : 0u;
+  for (int bt = 0; bt < NBT; ++bt) {
+    const int g0 = GB * bt;
+    if (g0 >= G) break;
+    lds_barrier();  // the previous batch is assembled (the union list read)
+#pragma unroll
+    for (int i = 0; i < NLI; ++i) {
+      const int item = tid + kST * i, jj = item / (GB * 8), gl = (item / 8) % GB, pc = item % 8;
+      *reinterpret_cast<uint4*>(&hbuf[jj * HP + gl * 64 + 8 * pc]) = pv[bt][i];
+      const uint32_t w[4] = {pv[bt][i].x, pv[bt][i].y, pv[bt][i].z, pv[bt][i].w};
+      float s8 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s8 += bf16_bits_to_f32((j & 1) ? w[j >> 1] >> 16 : w[j >> 1] & 0xFFFFu);
+      s8 += __shfl_xor(s8, 1, 64);
+      s8 += __shfl_xor(s8, 2, 64);
+      s8 += __shfl_xor(s8, 4, 64);
+      if (pc == 0 && g0 + gl < G) hsl[jj][g0 + gl] = s8;
     }
-    float s8 = 0.0f;
+    lds_barrier();
+    // A batch has at most 4 k-blocks per group, so NFR fragments per thread. All are made,
+    // then all are stored, fragments past the batch's end to a dump row: the number of
+    // stores is fixed, so the waits for later batches' pieces never wait for these stores
+    // (the hardware counts loads and stores together, in issue order).
+    const int kb0 = kbs[g0], nfr = (min(kbs[min(g0 + GB, G)], nreal) - kb0) * SPM * 2;
+    constexpr int NFR = 4 * GB * SPM * 2 / kST;
+    uint4 fr[NFR];
+    uint4* dst[NFR];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s8 += bf16_bits_to_f32(v[i]);
-    if (live) {
+    for (int f = 0; f < NFR; ++f) {
+      const int it = tid + kST * f;
+      const bool live = it < nfr;
+      const int kb = kb0 + (live ? it / (2 * SPM) : 0), jj = (it >> 1) % SPM, half = it & 1;
+      const int4 r0 = *reinterpret_cast<const int4*>(&prow[16 * kb + 8 * half]);
+      const int4 r1 = *reinterpret_cast<const int4*>(&prow[16 * kb + 8 * half + 4]);
+      const int r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+      uint32_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)  // a union row r of this batch: group r / 64, column r % 64
+        v[i] = live && r[i] >= 0 ? hbuf[jj * HP + r[i] - 64 * g0] : 0u;
       const int m = sp + kSplit * jj;
-      hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] =
-          make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
-                     v[6] | (v[7] << 16));
+      fr[f] = make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                         v[6] | (v[7] << 16));
+      dst[f] = live ? hc + (((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half
+                    : dump + tid;
     }
-    s8 += __shfl_xor(s8, 1, 64);
-    s8 += __shfl_xor(s8, 2, 64);
-    s8 += __shfl_xor(s8, 4, 64);
-    if (sub == 0 && q < npair) hsl[jj][g] = s8;
+#pragma unroll
+    for (int f = 0; f < NFR; ++f) *dst[f] = fr[f];
   }
   // the padding k-blocks (at most kPD - 1) hold zero fragments
   for (int it = tid; it < (nkb - nreal) * SPM * 2; it += kST) {
@@ -367,7 +423,7 @@ __global__ __launch_bounds__(kST) void k_stage(
     const int m = sp + kSplit * jj;
     hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] = make_uint4(0, 0, 0, 0);
   }
-  __syncthreads();
+  lds_barrier();
   // correction A fragments of this workgroup's slots, 16 groups per chunk: sections
   // [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo]; hs = hs_hi + hs_lo to about 16 bits, -128 x
   // is exact in bf16
@@ -821,21 +877,44 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
 }
 
-template <int YDT>
+// One thread per 4 consecutive outputs of a token. K > 0: topk known at compile time, all
+// ids and partials are loaded before any is used (out-of-range slots are dropped by a
+// select, not a branch around a load); K == 0: any topk.
+template <int YDT, int K>
 __global__ __launch_bounds__(256) void k_sum_slots(const float* __restrict__ part,
                                                    const int32_t* __restrict__ sel,
                                                    typename Elem<YDT>::T* __restrict__ y, int T,
                                                    int D, int topk, int E) {
+  const int D4 = D / 4;
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)T * D) return;
-  const size_t t = idx / D, o = idx - t * D;
-  const float* p = part + t * (topk + 1) * D + o;
+  if (idx >= (size_t)T * D4) return;
+  const size_t t = idx / D4, o = (idx - t * D4) * 4;
+  const float4* p = reinterpret_cast<const float4*>(part + t * (topk + 1) * D + o);
   const int32_t* st = sel + t * topk;
-  float s = (unsigned)st[0] < (unsigned)E ? p[0] : 0.0f;
-  for (int k = 1; k < topk; ++k)
-    if ((unsigned)st[k] < (unsigned)E) s += p[(size_t)k * D];
-  s += p[(size_t)topk * D];
-  Elem<YDT>::store(y, idx, s);
+  auto add = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
+  float4 s;
+  if constexpr (K > 0) {
+    int e[K];
+    float4 v[K + 1];
+#pragma unroll
+    for (int k = 0; k < K; ++k) e[k] = st[k];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) v[k] = p[(size_t)k * D4];
+    s = (unsigned)e[0] < (unsigned)E ? v[0] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 1; k < K; ++k) s = (unsigned)e[k] < (unsigned)E ? add(s, v[k]) : s;
+    s = add(s, v[K]);
+  } else {
+    s = (unsigned)st[0] < (unsigned)E ? p[0] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 1; k < topk; ++k)
+      if ((unsigned)st[k] < (unsigned)E) s = add(s, p[(size_t)k * D4]);
+    s = add(s, p[(size_t)topk * D4]);
+  }
+  const size_t yo = t * D + o;
+  Elem<YDT>::store(y, yo, s.x);
+  Elem<YDT>::store(y, yo + 1, s.y);
+  Elem<YDT>::store(y, yo + 2, s.z);
+  Elem<YDT>::store(y, yo + 3, s.w);
 }
 
 }  // namespace
@@ -908,9 +987,10 @@ namespace {
 // Workspace of hsd_prefill_gemm, in this order, each piece 256-byte aligned:
 //   part [T*(topk+1), D] f32 | kbg [NT, GMX+1] i32 | krow [NT, 16 KB] i32 |
 //   hc [NT, KB, MS, 64] uint4 | hcor [NT, ceil(GMX/16), 4, MS, 64] uint4 |
-//   blk [NT * D * MS / 128] i32 (the GEMM's block schedule), KB = kb_max(GMX)
+//   blk [NT * D * MS / 128] i32 (the GEMM's block schedule) | dump [256] uint4 (staging
+//   stores of unused fragments), KB = kb_max(GMX)
 struct GemmWs {
-  size_t part, kbg, krow, hc, hcor, blk, total;
+  size_t part, kbg, krow, hc, hcor, blk, dump, total;
 };
 inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E, int64_t tt) {
@@ -923,7 +1003,8 @@ GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_
   w.hc = w.krow + al256((size_t)NT * 16 * kb_max((int)GMX) * sizeof(int32_t));
   w.hcor = w.hc + al256((size_t)NT * kb_max((int)GMX) * MS * 64 * sizeof(uint4));
   w.blk = w.hcor + al256((size_t)NT * nch_max((int)GMX) * 4 * MS * 64 * sizeof(uint4));
-  w.total = w.blk + al256((size_t)NT * (D * MS / 128) * sizeof(int32_t));
+  w.dump = w.blk + al256((size_t)NT * (D * MS / 128) * sizeof(int32_t));
+  w.total = w.dump + al256((size_t)kST * sizeof(uint4));
   return w;
 }
 }  // namespace
@@ -960,6 +1041,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
     return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
   const uintptr_t al = (uintptr_t)ps | (uintptr_t)pb | (uintptr_t)sps | (uintptr_t)spb;
   if (al & 15u) return set_error(HSD_ERR_ALIGN, "%s: scales/biases must be 16-byte aligned", fn);
+  if ((uintptr_t)h & 15u) return set_error(HSD_ERR_ALIGN, "%s: h must be 16-byte aligned", fn);
   const GemmWs w = gemm_ws(T, D, F, FS, topk, E, tt);
   if (!workspace || workspace_bytes < w.total)
     return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, w.total);
@@ -971,11 +1053,12 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   uint4* hc = reinterpret_cast<uint4*>(ws + w.hc);
   uint4* hcor = reinterpret_cast<uint4*>(ws + w.hcor);
   int32_t* blk = reinterpret_cast<int32_t*>(ws + w.blk);
+  uint4* dump = reinterpret_cast<uint4*>(ws + w.dump);
   const int GMX = (int)((F > FS ? F : FS) / 64);
   if (tt == 32) {
-    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
-                       ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
-                       (int)E, (int)umax, GMX);
+    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)(NT * stage_split(1))), dim3(kST), 0, st, h, tile_e, tile_slot,
+                       ulist, ucount, kbg, krow, hc, hcor, dump, (int)D, (int)F, (int)FS,
+                       (int)topk, (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
     if (rc) return rc;
     hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
@@ -986,9 +1069,9 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
                        blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   } else {
-    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)(NT * kSplit)), dim3(kST), 0, st, h, tile_e, tile_slot,
-                       ulist, ucount, kbg, krow, hc, hcor, (int)D, (int)F, (int)FS, (int)topk,
-                       (int)E, (int)umax, GMX);
+    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)(NT * stage_split(2))), dim3(kST), 0, st, h, tile_e, tile_slot,
+                       ulist, ucount, kbg, krow, hc, hcor, dump, (int)D, (int)F, (int)FS,
+                       (int)topk, (int)E, (int)umax, GMX);
     int rc = check_launch(fn);
     if (rc) return rc;
     hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
@@ -1001,13 +1084,18 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   }
   int rc = check_launch(fn);
   if (rc) return rc;
-  const unsigned sg = (unsigned)((T * D + 255) / 256);
+  const unsigned sg = (unsigned)((T * (D / 4) + 255) / 256);
   switch (y_dtype) {
 #define HSD_SUMS(DT)                                                                          \
   case DT:                                                                                    \
-    hipLaunchKernelGGL(k_sum_slots<DT>, dim3(sg), dim3(256), 0, st, part, sel,               \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)T, (int)D, (int)topk, \
-                       (int)E);                                                               \
+    if (topk == 6)                                                                            \
+      hipLaunchKernelGGL((k_sum_slots<DT, 6>), dim3(sg), dim3(256), 0, st, part, sel,        \
+                         reinterpret_cast<typename Elem<DT>::T*>(y), (int)T, (int)D,         \
+                         (int)topk, (int)E);                                                  \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_sum_slots<DT, 0>), dim3(sg), dim3(256), 0, st, part, sel,        \
+                         reinterpret_cast<typename Elem<DT>::T*>(y), (int)T, (int)D,         \
+                         (int)topk, (int)E);                                                  \
     break;
     HSD_SUMS(HSD_DT_BF16)
     HSD_SUMS(HSD_DT_F16)

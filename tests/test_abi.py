@@ -78,12 +78,12 @@ def test_workspace_sizes():
     assert lib.hsd_prefill_num_tiles(2048, 6, 128, 32) == 576
     # partials [T*7, D] f32, then per tile: group starts (59), padded rows (16 per k-block,
     # 4*58+8 k-blocks), A fragments (1 KiB per k-block), correction fragments (4 x 4 KiB),
-    # the GEMM's block schedule (21 column blocks per tile)
+    # the GEMM's block schedule (21 column blocks per tile), the staging kernel's dump row
     def al(x):
         return (x + 255) // 256 * 256
     kb = 4 * 58 + 8
     want = (al(512 * 7 * 2688 * 4) + al(240 * 59 * 4) + al(240 * 16 * kb * 4) + al(240 * kb * 1024)
-            + al(240 * 4 * 4 * 1024) + al(240 * 21 * 4))
+            + al(240 * 4 * 4 * 1024) + al(240 * 21 * 4) + al(256 * 16))
     assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 32) == want
     assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 48) == 0
     assert lib.hsd_mamba_workspace_bytes(3, 64, 64) == 3 * 4096 * 4
