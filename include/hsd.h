@@ -135,7 +135,7 @@ int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const float* gains,
 /* ------------------------------------------------------------------ Mamba-2
  * Replaces the state update of hsd/mamba.py:19-44 `mamba_verify` (depthwise conv,
  * silu, mlx-lm `ssm_update` over L rows, gated RMSNorm) for L in 1..nslab-1 rows.
- * State lives in a ring of nslab slabs: ssm_slabs [nslab, H, P, N] f32,
+ * State lives in a ring of nslab slabs: ssm_slabs [nslab, H, P, N] f32 (16-byte aligned),
  * conv_slabs [nslab, K-1, CD] bf16 (K = 4); *cur (device int32) names the current slab.
  * Row r (0-based) reads the state after row r-1 and writes the state after row r to
  * slab (cur+1+r) % nslab -- the per-row checkpoints. *cur is not changed here.

@@ -13,9 +13,11 @@
 // G=8 groups, conv K=4, CD = 4096 + 2*8*128 = 6144 channels):
 //   one workgroup = (head h, block of 16 head_dim rows p): 256 WGs. It computes the conv
 //   + silu of its 16 x channels and of its group's 128 B and 128 C channels for all L
-//   rows (LDS), then each wave streams 4 state rows S[h, p, :] (128 fp32 = 2 per lane)
-//   through the L rows: S = dA*S + (x*dt)*B, y = sum_n S*C + D*x (butterfly sum), and
-//   writes each row's S to its checkpoint slab. HBM: read S once, write L checkpoints.
+//   rows (LDS), then each wave streams 4 state rows S[h, p, :] (128 fp32: 16 lanes per
+//   row, 8 elements each) through the L rows: S = dA*S + (x*dt)*B, y = sum_n S*C + D*x
+//   (a lane's 8 products, then a butterfly over the row's 16 lanes), and writes each
+//   row's S to its checkpoint slab. HBM: read S once, write L checkpoints; all loads in
+//   two round trips (the ring index, then what depends on it).
 // The gated RMSNorm (groups of 512 = 8 heads) runs as a second small kernel.
 #include "hsd_common.h"
 
@@ -24,7 +26,7 @@ namespace {
 
 constexpr int kMT = 256;
 constexpr int kPB = 16;      // head_dim rows per workgroup
-constexpr int kN = 128;      // state size (2 per lane)
+constexpr int kN = 128;      // state size (16 lanes per state row, 8 elements each)
 constexpr int kK = 4;        // conv kernel
 constexpr int kLMax = 7;     // rows per verify (nslab <= 8)
 
@@ -36,49 +38,78 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     const int32_t* __restrict__ cur_ptr, int nslab, float* __restrict__ y_pre, int L, int H,
     int P, int G, float dt_lo, float dt_hi) {
   __shared__ float xs[kLMax][kPB];
-  __shared__ float Bs[kLMax][kN];
-  __shared__ float Cs[kLMax][kN];
+  __shared__ __attribute__((aligned(16))) float Bs[kLMax][kN];
+  __shared__ __attribute__((aligned(16))) float Cs[kLMax][kN];
   __shared__ float dtv[kLMax], dA[kLMax];
   const int npb = P / kPB;
   const int hh = blockIdx.x / npb, pblk = blockIdx.x - (blockIdx.x / npb) * npb;
   const int tid = threadIdx.x;
-  const int cur = *cur_ptr;
-  if ((unsigned)cur >= (unsigned)nslab) return;  // a corrupt ring index: touch nothing
   const int DI = H * P, GN = G * kN, CD = DI + 2 * GN;
   const int hpg = H / G;
   const int g = hh / hpg;
   const bool owner_bc = (hh % hpg == 0) && pblk == 0;  // writes the B/C conv checkpoints
-
-  // ---- the state rows this workgroup streams: issued first, they do not depend on the
-  // conv, so their latency overlaps it
-  const int lane = tid & 63, wave = tid >> 6;
-  constexpr int kRPW = kPB / (kMT / 64);
-  float2 S[kRPW];
-  const size_t slab_sz = (size_t)H * P * kN;
+  // Loads in two round trips, never under a branch (a load inside a branch makes the
+  // compiler wait for every earlier load where the paths merge): first the ring index
+  // with every input that does not depend on it, then the state rows and conv windows.
+  // Rows past L re-read row L - 1 and are unused.
+  const int cur = *cur_ptr;
+  // conv channels: thread t owns channel t of [16 x | 128 B | 128 C] and, for t < 16, also
+  // channel 256 + t; the others repeat channel t for the second and drop it
+  constexpr int NCH = kPB + 2 * kN;
+  auto chan = [&](int t) {
+    return t < kPB ? hh * P + pblk * kPB + t
+                   : (t < kPB + kN ? DI + g * kN + (t - kPB) : DI + GN + g * kN + (t - kPB - kN));
+  };
+  const int t1 = tid, t2 = tid + kMT < NCH ? tid + kMT : tid;
+  const int ch1 = chan(t1), ch2 = chan(t2);
+  uint16_t in1[kLMax], in2[kLMax];
 #pragma unroll
-  for (int i = 0; i < kRPW; ++i) {
-    const int p = pblk * kPB + wave * kRPW + i;
-    S[i] = *reinterpret_cast<const float2*>(ssm + (size_t)cur * slab_sz +
-                                            ((size_t)hh * P + p) * kN + 2 * lane);
+  for (int r = 0; r < kLMax; ++r) {
+    in1[r] = conv_in[(size_t)min(r, L - 1) * cin_ld + ch1];
+    in2[r] = conv_in[(size_t)min(r, L - 1) * cin_ld + ch2];
   }
+  uint16_t w1[kK], w2[kK];
+#pragma unroll
+  for (int j = 0; j < kK; ++j) {
+    w1[j] = conv_w[(size_t)ch1 * kK + j];
+    w2[j] = conv_w[(size_t)ch2 * kK + j];
+  }
+  const uint16_t b1 = conv_b[ch1], b2 = conv_b[ch2];
+  const int rd = min(tid, L - 1);
+  const uint16_t dtr = dt_raw[(size_t)rd * dt_ld + hh];
+  const float Alog = A_log[hh], dtb = dt_bias[hh], Dh = Dp[hh];
+  if ((unsigned)cur >= (unsigned)nslab) return;  // a corrupt ring index: touch nothing
 
-  // ---- depthwise causal conv + silu of the channels this workgroup needs
+  // the state rows: wave w owns rows 4w .. 4w+3 of the block, lane = 16 i + c holds
+  // elements 8c .. 8c+7 of row 4w + i
+  const int lane = tid & 63, wave = tid >> 6, ri = lane >> 4, c8 = lane & 15;
+  const int pl = wave * (kPB / (kMT / 64)) + ri, p = pblk * kPB + pl;
+  const size_t slab_sz = (size_t)H * P * kN;
+  const size_t soff = ((size_t)hh * P + p) * kN + 8 * c8;
+  float4 S0 = *reinterpret_cast<const float4*>(ssm + (size_t)cur * slab_sz + soff);
+  float4 S1 = *reinterpret_cast<const float4*>(ssm + (size_t)cur * slab_sz + soff + 4);
   const uint16_t* cs0 = convs + (size_t)cur * (kK - 1) * CD;
-  for (int t = tid; t < kPB + 2 * kN; t += kMT) {
-    int ch;
-    if (t < kPB) ch = hh * P + pblk * kPB + t;
-    else if (t < kPB + kN) ch = DI + g * kN + (t - kPB);
-    else ch = DI + GN + g * kN + (t - kPB - kN);
+  uint16_t s1[kK - 1], s2[kK - 1];
+#pragma unroll
+  for (int i = 0; i < kK - 1; ++i) {
+    s1[i] = cs0[(size_t)i * CD + ch1];
+    s2[i] = cs0[(size_t)i * CD + ch2];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- depthwise causal conv + silu of the channels this workgroup needs, and the conv
+  // checkpoint after row r (window rows r+1 .. r+3)
+  auto conv = [&](int t, int ch, const uint16_t (&st)[kK - 1], const uint16_t (&in)[kLMax],
+                  const uint16_t (&wr)[kK], uint16_t bb) {
     uint16_t win[kK - 1 + kLMax];
 #pragma unroll
-    for (int i = 0; i < kK - 1; ++i) win[i] = cs0[(size_t)i * CD + ch];
+    for (int i = 0; i < kK - 1; ++i) win[i] = st[i];
 #pragma unroll
-    for (int r = 0; r < kLMax; ++r)
-      win[kK - 1 + r] = r < L ? conv_in[(size_t)r * cin_ld + ch] : (uint16_t)0;
+    for (int r = 0; r < kLMax; ++r) win[kK - 1 + r] = in[r];
     float wj[kK];
 #pragma unroll
-    for (int j = 0; j < kK; ++j) wj[j] = bf16_bits_to_f32(conv_w[(size_t)ch * kK + j]);
-    const float bias = bf16_bits_to_f32(conv_b[ch]);
+    for (int j = 0; j < kK; ++j) wj[j] = bf16_bits_to_f32(wr[j]);
+    const float bias = bf16_bits_to_f32(bb);
 #pragma unroll
     for (int r = 0; r < kLMax; ++r) {
       if (r < L) {
@@ -91,7 +122,7 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
         else Cs[r][t - kPB - kN] = co;
       }
     }
-    if (t < kPB || owner_bc) {  // conv checkpoint after row r: window rows r+1 .. r+3
+    if (t < kPB || owner_bc) {
 #pragma unroll
       for (int r = 0; r < kLMax; ++r) {
         if (r < L) {
@@ -101,33 +132,51 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
         }
       }
     }
-  }
+  };
+  conv(t1, ch1, s1, in1, w1, b1);
+  if (tid + kMT < NCH) conv(t2, ch2, s2, in2, w2, b2);
   if (tid < L) {
-    const float A = -expf(A_log[hh]);
-    const float v = softplus_f32(bf16_bits_to_f32(dt_raw[(size_t)tid * dt_ld + hh]) + dt_bias[hh]);
+    const float A = -expf(Alog);
+    const float v = softplus_f32(bf16_bits_to_f32(dtr) + dtb);
     const float d = fminf(fmaxf(v, dt_lo), dt_hi);
     dtv[tid] = d;
     dA[tid] = expf(A * d);
   }
-  const float Dh = Dp[hh];
-  __syncthreads();
+  lds_barrier();
 
-  // ---- the state rows: 4 per wave, 2 state elements per lane
+  // ---- the state rows through the L rows: S = dA*S + (x*dt)*B, written to the row's
+  // checkpoint slab; y = sum_n S*C (8 elements per lane, then 16 lanes) + D*x
   for (int r = 0; r < L; ++r) {
-    const float B0 = Bs[r][2 * lane], B1 = Bs[r][2 * lane + 1];
-    const float C0 = Cs[r][2 * lane], C1 = Cs[r][2 * lane + 1];
-    float* dst = ssm + (size_t)((cur + 1 + r) % nslab) * slab_sz;
-#pragma unroll
-    for (int i = 0; i < kRPW; ++i) {
-      const int pl = wave * kRPW + i, p = pblk * kPB + pl;
-      const float x = xs[r][pl];
-      const float xdt = x * dtv[r];
-      S[i].x = fmaf(dA[r], S[i].x, xdt * B0);
-      S[i].y = fmaf(dA[r], S[i].y, xdt * B1);
-      *reinterpret_cast<float2*>(dst + ((size_t)hh * P + p) * kN + 2 * lane) = S[i];
-      const float y = wave_sum(fmaf(S[i].y, C1, S[i].x * C0));
-      if (lane == 0) y_pre[(size_t)r * DI + (size_t)hh * P + p] = y + x * Dh;
-    }
+    const float4 B0 = *reinterpret_cast<const float4*>(&Bs[r][8 * c8]);
+    const float4 B1 = *reinterpret_cast<const float4*>(&Bs[r][8 * c8 + 4]);
+    const float4 C0 = *reinterpret_cast<const float4*>(&Cs[r][8 * c8]);
+    const float4 C1 = *reinterpret_cast<const float4*>(&Cs[r][8 * c8 + 4]);
+    const float x = xs[r][pl];
+    const float xdt = x * dtv[r], a = dA[r];
+    S0.x = fmaf(a, S0.x, xdt * B0.x);
+    S0.y = fmaf(a, S0.y, xdt * B0.y);
+    S0.z = fmaf(a, S0.z, xdt * B0.z);
+    S0.w = fmaf(a, S0.w, xdt * B0.w);
+    S1.x = fmaf(a, S1.x, xdt * B1.x);
+    S1.y = fmaf(a, S1.y, xdt * B1.y);
+    S1.z = fmaf(a, S1.z, xdt * B1.z);
+    S1.w = fmaf(a, S1.w, xdt * B1.w);
+    float* dst = ssm + (size_t)((cur + 1 + r) % nslab) * slab_sz + soff;
+    *reinterpret_cast<float4*>(dst) = S0;
+    *reinterpret_cast<float4*>(dst + 4) = S1;
+    float y = S0.x * C0.x;
+    y = fmaf(S0.y, C0.y, y);
+    y = fmaf(S0.z, C0.z, y);
+    y = fmaf(S0.w, C0.w, y);
+    y = fmaf(S1.x, C1.x, y);
+    y = fmaf(S1.y, C1.y, y);
+    y = fmaf(S1.z, C1.z, y);
+    y = fmaf(S1.w, C1.w, y);
+    y += __shfl_xor(y, 1, 64);
+    y += __shfl_xor(y, 2, 64);
+    y += __shfl_xor(y, 4, 64);
+    y += __shfl_xor(y, 8, 64);
+    if (c8 == 0) y_pre[(size_t)r * DI + (size_t)hh * P + p] = y + x * Dh;
   }
 }
 
@@ -260,7 +309,7 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
     return set_error(HSD_ERR_SHAPE, "%s: norm_group must be a multiple of 256, <= 2048, dividing H*P", fn);
   if (conv_in_ld < CD || dt_ld < H || gate_ld < DI)
     return set_error(HSD_ERR_SHAPE, "%s: row strides smaller than the rows", fn);
-  if ((uintptr_t)ssm_slabs & 7u) return set_error(HSD_ERR_ALIGN, "%s: ssm_slabs must be 8-byte aligned", fn);
+  if ((uintptr_t)ssm_slabs & 15u) return set_error(HSD_ERR_ALIGN, "%s: ssm_slabs must be 16-byte aligned", fn);
   if (H * (P / kPB) > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
   const size_t need = hsd_mamba_workspace_bytes(L, H, P);
   if (!workspace || workspace_bytes < need)
