@@ -451,7 +451,8 @@ __global__ __launch_bounds__(kST) void k_stage(
 // The GEMM's block schedule. GEMM workgroup b runs on XCD b % 8 (the hardware deals
 // workgroups to the XCDs in turn) and takes entry xcd_remap(b, n) of blk, so XCD x owns
 // the contiguous range [start_x, start_x + q_x) of blk, q_x = n / 8 or n / 8 + 1. An
-// entry is a block, tile * nblk + nb (column block nb of the tile), or -1 (no work).
+// entry is a block (tile * nblk + nb for column block nb of the tile, and the tile's
+// expert), or (-1, -1): no work.
 // Work is dealt by column stripe: span consecutive column blocks of one expert, 128
 // bytes of each weight row (whole cache lines). The tiles of an expert read the same
 // weight bytes in a stripe, so a stripe stays on one XCD with its tiles side by side in
@@ -467,7 +468,7 @@ constexpr int kOT = 1024;
 constexpr int kOrderMaxE = kOT - 1;  // experts the schedule supports (E + 1 runs <= kOT)
 __global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_e,
                                                const int32_t* __restrict__ kbg,
-                                               int32_t* __restrict__ blk, int NT, int nblk,
+                                               int2* __restrict__ blk, int NT, int nblk,
                                                int span, int F, int FS, int E, int GMX) {
   __shared__ __attribute__((aligned(16))) int rkey[kOT];
   __shared__ int rlen[kOT], rmax[kOT], rrank[kOT], byrank[kOT], rcnt[kOT];
@@ -553,7 +554,7 @@ __global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_
   if (!fits) {  // identity: entry l is block l where its tile has an expert
     for (int l = tid; l < n; l += kOT) {
       const int e = tile_e[l / nblk];
-      blk[l] = e >= 0 && e <= E ? l : -1;
+      blk[l] = e >= 0 && e <= E ? make_int2(l, e) : make_int2(-1, -1);
     }
     return;
   }
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_
     int x = 0;
 #pragma unroll
     for (int y = 1; y < kXcds; ++y) x += l >= st[y];
-    if (l - st[x] >= tot[x]) blk[l] = -1;
+    if (l - st[x] >= tot[x]) blk[l] = make_int2(-1, -1);
   }
   for (int t = tid; t < NT; t += kOT) {
     const int e = tile_e[t];
@@ -570,7 +571,7 @@ __global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_
     const int o = (i * U) & (kXcds - 1);
     for (int nb = 0; nb < nblk; ++nb) {
       const int u = nb / span, j = nb - u * span, x = (u + o) & (kXcds - 1);
-      blk[st[x] + base[x][i] + ((u / kXcds) * span + j) * L + k] = t * nblk + nb;
+      blk[st[x] + base[x][i] + ((u / kXcds) * span + j) * L + k] = make_int2(t * nblk + nb, e);
     }
   }
 }
@@ -582,13 +583,13 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 
 template <int MS>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(
-    const int32_t* __restrict__ tile_e, const int32_t* __restrict__ tile_slot,
-    const float* __restrict__ gains, const int32_t* __restrict__ kbg,
+    const int32_t* __restrict__ tile_slot, const float* __restrict__ gains,
+    const int32_t* __restrict__ kbg,
     const int32_t* __restrict__ krow, const uint4* __restrict__ hc,
     const uint4* __restrict__ hcor, const uint32_t* __restrict__ pw,
     const uint16_t* __restrict__ ps, const uint16_t* __restrict__ pb,
     const uint32_t* __restrict__ spw, const uint16_t* __restrict__ sps,
-    const uint16_t* __restrict__ spb, float* __restrict__ part, const int32_t* __restrict__ blk,
+    const uint16_t* __restrict__ spb, float* __restrict__ part, const int2* __restrict__ blk,
     int D, int F, int FS, int topk, int E, int NT, int GMX) {
   constexpr int TT = 32 * MS, NWC = 16 / MS, NMF = 4 / MS, NCOL = 8 * NWC;
   constexpr int RP = 40;  // ring pitch per column (bf16): b of 16 groups, s of 16 groups, pad
@@ -601,11 +602,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   constexpr int PD = MS == 1 ? kPD : kPD / 2;  // register ring depth (a divisor of kPD)
   constexpr int LPR = NWC / 4;                 // lanes loading one row segment, 16 B each
   const int nblk = D / NCOL;
-  const int bv = blk[xcd_remap((int)blockIdx.x, NT * nblk)];
-  if (bv < 0) return;
-  const int tile = bv / nblk, nb = bv - (bv / nblk) * nblk;
-  const int e = tile_e[tile];
-  if (e < 0) return;
+  const int2 bv = blk[xcd_remap((int)blockIdx.x, NT * nblk)];  // (tile * nblk + nb, expert)
+  if (bv.x < 0 || bv.y < 0) return;
+  const int tile = bv.x / nblk, nb = bv.x - (bv.x / nblk) * nblk;
+  const int e = bv.y;
   const bool shared = e >= E;
   const int FF = shared ? FS : F, G = FF / 64;
   const int l = threadIdx.x, khalf = l >> 5, c = (l & 31) % NWC, jq = (l & 31) / NWC;
@@ -618,14 +618,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int sl = tile_slot[(size_t)tile * TT + (l & (TT - 1))];
   const int gi = sl < 0 ? -1 : shared ? sl * (topk + 1) + topk : (sl / topk) * (topk + 1) + (sl % topk);
   const float gn = gains[max(gi, 0)];
-  const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
-  const int kv = l <= G ? kbgT[l] : 0;
-  const int kn = l < G ? kbgT[l + 1] : 0;
-  const uint64_t nonempty = __ballot(l < G && kn > kv);
-  // k-blocks of this tile: a multiple of kPD and at most kb_max(G) by construction; the
-  // clamp keeps a corrupted workspace from driving the loop out of its buffers
-  const int nkb = min(max(__builtin_amdgcn_readlane(kv, G), 0), kb_max(G)) / kPD * kPD;
-
+  // The correction's first chunk (below) depends on the tile and expert only: its loads
+  // go out now, with the tile's group starts and slots.
+  const uint16_t* sb = (shared ? sps : ps + (size_t)e * (F / 64) * D) + n0 + lcol;
+  const uint16_t* bb = (shared ? spb : pb + (size_t)e * (F / 64) * D) + n0 + lcol;
+  const uint4* hq = hcor + (size_t)tile * NCHMX * 4 * MS * 64 + l;
+  const int NCH = (G + 15) >> 4;
+  constexpr int V8 = NCOL / 8;       // uint4 pieces per row segment
+  constexpr int NIT = 32 * V8 / 64;  // 32 row segments (b, s of 16 groups)
+  auto load_chunk = [&](int ch, uint4 (&a)[4][MS], uint4 (&v)[NIT]) {
+#pragma unroll
+    for (int sec = 0; sec < 4; ++sec)
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) a[sec][ms] = hq[(((size_t)ch * 4 + sec) * MS + ms) * 64];
+#pragma unroll
+    for (int t = 0; t < NIT; ++t) {
+      const int item = l + 64 * t, r = item / V8, c8 = item % V8;
+      const int gg = min(16 * ch + (r & 15), G - 1);
+      v[t] = *reinterpret_cast<const uint4*>((r < 16 ? bb : sb) - lcol + (size_t)gg * D + 8 * c8);
+    }
+  };
+  uint4 a0[4][MS], v0[NIT], a1[4][MS], v1[NIT];
+  load_chunk(0, a0, v0);
   f32x16 y[MS][NMF];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
@@ -633,6 +647,60 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     for (int i = 0; i < NMF; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) y[ms][i][v] = 0.0f;
+
+  // The correction sum_g [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo] x [b, b, s, s], 16 groups
+  // at a time: the groups' b and s rows of this column block go through the LDS ring
+  // [column][b of 16 groups | s of 16 groups | pad], then 4 MFMA k-blocks start y. The
+  // next chunk's loads are in flight while a chunk is processed. Loads are never
+  // conditional (a branch around a load makes the compiler wait for every load at the
+  // merge): rows past G re-read row G - 1 and are zeroed, chunks past the last re-read it.
+  auto process = [&](int ch, const uint4 (&a)[4][MS], const uint4 (&v)[NIT]) {
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NIT; ++t) {
+      const int item = l + 64 * t, r = item / V8, c8 = item % V8;
+      const bool live = 16 * ch + (r & 15) < G;
+      const uint32_t w[4] = {live ? v[t].x : 0u, live ? v[t].y : 0u, live ? v[t].z : 0u,
+                             live ? v[t].w : 0u};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        ring[(8 * c8 + j) * RP + 16 * (r >> 4) + (r & 15)] =
+            (uint16_t)((j & 1) ? w[j >> 1] >> 16 : w[j >> 1]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sec = 0; sec < 4; ++sec)
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(&ring[(lcol + i) * RP + (sec >> 1) * 16 + 8 * khalf]);
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms)
+          y[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[sec][ms]), as_bf16x8(bv), y[ms][i], 0, 0, 0);
+      }
+  };
+  // Chunks go in pairs; a chunk past the last one (odd NCH) has all rows zeroed and adds
+  // exact zeros. Nothing is conditional, so no load sinks into a branch, and the
+  // scheduling barriers keep each chunk's loads ahead of the work before them. The
+  // correction runs for every tile: with no k-block, hs and so y are zero.
+  {
+    for (int ch = 0; ch < NCH; ch += 2) {
+      load_chunk(min(ch + 1, NCH - 1), a1, v1);
+      __builtin_amdgcn_sched_barrier(0);
+      process(ch, a0, v0);
+      load_chunk(min(ch + 2, NCH - 1), a0, v0);
+      __builtin_amdgcn_sched_barrier(0);
+      process(ch + 1, a1, v1);
+    }
+  }
+
+  const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
+  const int kv0 = kbgT[min(l, G)], kn0 = kbgT[min(l + 1, G)];  // unconditional loads
+  const int kv = l <= G ? kv0 : 0;
+  const int kn = l < G ? kn0 : 0;
+  const uint64_t nonempty = __ballot(l < G && kn > kv);
+  // k-blocks of this tile: a multiple of kPD and at most kb_max(G) by construction; the
+  // clamp keeps a corrupted workspace from driving the loop out of its buffers
+  const int nkb = min(max(__builtin_amdgcn_readlane(kv, G), 0), kb_max(G)) / kPD * kPD;
 
   if (nkb > 0) {
     f32x16 acc[MS][NMF];
@@ -643,8 +711,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[ms][i][v] = 0.0f;
     const uint32_t* wb = shared ? spw : pw + (size_t)e * F * (D / 8);
-    const uint16_t* sb = (shared ? sps : ps + (size_t)e * (F / 64) * D) + n0 + lcol;
-    const uint16_t* bb = (shared ? spb : pb + (size_t)e * (F / 64) * D) + n0 + lcol;
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, FF * (D / 2), 0x00020000);
     const int lr = (l / LPR) & 15, la = l % LPR;     // this lane's row and 16-byte piece
@@ -658,68 +724,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                   : (bsel | 0x0C00u | (bsel + 4) << 16 | 0x0C000000u);
     const int32_t* kr = krow + (size_t)tile * KMX + lr;
     const uint4* ha = hc + (size_t)tile * KBMX * MS * 64 + l;
-    const uint4* hq = hcor + (size_t)tile * NCHMX * 4 * MS * 64 + l;
-
-    // The correction sum_g [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo] x [b, b, s, s], 16 groups
-    // at a time: the groups' b and s rows of this column block go through the LDS ring
-    // [column][b of 16 groups | s of 16 groups | pad], then 4 MFMA k-blocks start y. The
-    // next chunk's loads are in flight while a chunk is processed. Loads are never
-    // conditional (a branch around a load makes the compiler wait for every load at the
-    // merge): rows past G re-read row G - 1 and are zeroed, chunks past the last re-read it.
-    const int NCH = (G + 15) >> 4;
-    constexpr int V8 = NCOL / 8;       // uint4 pieces per row segment
-    constexpr int NIT = 32 * V8 / 64;  // 32 row segments (b, s of 16 groups)
-    auto load_chunk = [&](int ch, uint4 (&a)[4][MS], uint4 (&v)[NIT]) {
-#pragma unroll
-      for (int sec = 0; sec < 4; ++sec)
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms) a[sec][ms] = hq[(((size_t)ch * 4 + sec) * MS + ms) * 64];
-#pragma unroll
-      for (int t = 0; t < NIT; ++t) {
-        const int item = l + 64 * t, r = item / V8, c8 = item % V8;
-        const int gg = min(16 * ch + (r & 15), G - 1);
-        v[t] = *reinterpret_cast<const uint4*>((r < 16 ? bb : sb) - lcol + (size_t)gg * D + 8 * c8);
-      }
-    };
-    auto process = [&](int ch, const uint4 (&a)[4][MS], const uint4 (&v)[NIT]) {
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < NIT; ++t) {
-        const int item = l + 64 * t, r = item / V8, c8 = item % V8;
-        const bool live = 16 * ch + (r & 15) < G;
-        const uint32_t w[4] = {live ? v[t].x : 0u, live ? v[t].y : 0u, live ? v[t].z : 0u,
-                               live ? v[t].w : 0u};
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          ring[(8 * c8 + j) * RP + 16 * (r >> 4) + (r & 15)] =
-              (uint16_t)((j & 1) ? w[j >> 1] >> 16 : w[j >> 1]);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int sec = 0; sec < 4; ++sec)
-#pragma unroll
-        for (int i = 0; i < NMF; ++i) {
-          const uint4 bv = *reinterpret_cast<const uint4*>(&ring[(lcol + i) * RP + (sec >> 1) * 16 + 8 * khalf]);
-#pragma unroll
-          for (int ms = 0; ms < MS; ++ms)
-            y[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[sec][ms]), as_bf16x8(bv), y[ms][i], 0, 0, 0);
-        }
-    };
-    // Chunks go in pairs; a chunk past the last one (odd NCH) has all rows zeroed and adds
-    // exact zeros. Nothing is conditional, so no load sinks into a branch, and the
-    // scheduling barriers keep each chunk's loads ahead of the work before them.
-    {
-      uint4 a0[4][MS], v0[NIT], a1[4][MS], v1[NIT];
-      load_chunk(0, a0, v0);
-      for (int ch = 0; ch < NCH; ch += 2) {
-        load_chunk(min(ch + 1, NCH - 1), a1, v1);
-        __builtin_amdgcn_sched_barrier(0);
-        process(ch, a0, v0);
-        load_chunk(min(ch + 2, NCH - 1), a0, v0);
-        __builtin_amdgcn_sched_barrier(0);
-        process(ch + 1, a1, v1);
-      }
-    }
 
     // the scale table s[g][n0 .. n0 + NCOL) of all groups, so that the k-block loop issues
     // no global load inside its group-end branch: every load first, then the stores.
@@ -987,7 +991,7 @@ namespace {
 // Workspace of hsd_prefill_gemm, in this order, each piece 256-byte aligned:
 //   part [T*(topk+1), D] f32 | kbg [NT, GMX+1] i32 | krow [NT, 16 KB] i32 |
 //   hc [NT, KB, MS, 64] uint4 | hcor [NT, ceil(GMX/16), 4, MS, 64] uint4 |
-//   blk [NT * D * MS / 128] i32 (the GEMM's block schedule) | dump [256] uint4 (staging
+//   blk [NT * D * MS / 128] int2 (the GEMM's block schedule) | dump [256] uint4 (staging
 //   stores of unused fragments), KB = kb_max(GMX)
 struct GemmWs {
   size_t part, kbg, krow, hc, hcor, blk, dump, total;
@@ -1003,7 +1007,7 @@ GemmWs gemm_ws(int64_t T, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_
   w.hc = w.krow + al256((size_t)NT * 16 * kb_max((int)GMX) * sizeof(int32_t));
   w.hcor = w.hc + al256((size_t)NT * kb_max((int)GMX) * MS * 64 * sizeof(uint4));
   w.blk = w.hcor + al256((size_t)NT * nch_max((int)GMX) * 4 * MS * 64 * sizeof(uint4));
-  w.dump = w.blk + al256((size_t)NT * (D * MS / 128) * sizeof(int32_t));
+  w.dump = w.blk + al256((size_t)NT * (D * MS / 128) * sizeof(int2));
   w.total = w.dump + al256((size_t)kST * sizeof(uint4));
   return w;
 }
@@ -1052,7 +1056,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   int32_t* krow = reinterpret_cast<int32_t*>(ws + w.krow);
   uint4* hc = reinterpret_cast<uint4*>(ws + w.hc);
   uint4* hcor = reinterpret_cast<uint4*>(ws + w.hcor);
-  int32_t* blk = reinterpret_cast<int32_t*>(ws + w.blk);
+  int2* blk = reinterpret_cast<int2*>(ws + w.blk);
   uint4* dump = reinterpret_cast<uint4*>(ws + w.dump);
   const int GMX = (int)((F > FS ? F : FS) / 64);
   if (tt == 32) {
@@ -1065,7 +1069,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
                        (int)(D / 128), 2, (int)F, (int)FS, (int)E, GMX);
     rc = check_launch(fn);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * (D / 128))), dim3(64), 0, st, tile_e,
+    hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * (D / 128))), dim3(64), 0, st,
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
                        blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   } else {
@@ -1078,7 +1082,7 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
                        (int)(D / 64), 4, (int)F, (int)FS, (int)E, GMX);
     rc = check_launch(fn);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * (D / 64))), dim3(64), 0, st, tile_e,
+    hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * (D / 64))), dim3(64), 0, st,
                        tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
                        blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   }

@@ -83,7 +83,7 @@ def test_workspace_sizes():
         return (x + 255) // 256 * 256
     kb = 4 * 58 + 8
     want = (al(512 * 7 * 2688 * 4) + al(240 * 59 * 4) + al(240 * 16 * kb * 4) + al(240 * kb * 1024)
-            + al(240 * 4 * 4 * 1024) + al(240 * 21 * 4) + al(256 * 16))
+            + al(240 * 4 * 4 * 1024) + al(240 * 21 * 8) + al(256 * 16))
     assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 32) == want
     assert lib.hsd_prefill_gemm_workspace_bytes(512, 2688, 1856, 3712, 6, 128, 48) == 0
     assert lib.hsd_mamba_workspace_bytes(3, 64, 64) == 3 * 4096 * 4
