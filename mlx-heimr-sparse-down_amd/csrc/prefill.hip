@@ -592,11 +592,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const uint16_t* __restrict__ spb, float* __restrict__ part, const int2* __restrict__ blk,
     int D, int F, int FS, int topk, int E, int NT, int GMX) {
   constexpr int TT = 32 * MS, NWC = 16 / MS, NMF = 4 / MS, NCOL = 8 * NWC;
-  constexpr int RP = 40;  // ring pitch per column (bf16): b of 16 groups, s of 16 groups, pad
+  // The correction ring: per column 8 blocks of 8 bf16 (RP = 64), of which 4 are used (b of
+  // groups 0-7, 8-15, s of groups 0-7, 8-15); block beta of column col sits at block
+  // beta ^ (col / 8 % 8), so the 16 columns that one write instruction covers (8 apart)
+  // fall in different LDS banks.
+  constexpr int RP = 64;
   // LDS: first the correction ring [NCOL][RP], then the scale table [G][NCOL] of this block
   constexpr int kLds = NCOL * RP > kGMax * NCOL ? NCOL * RP : kGMax * NCOL;
   __shared__ __attribute__((aligned(16))) uint16_t ring[kLds];
-  // k-block words in transit: [word column][row], pitch 20 (conflict-free 4-byte writes)
+  // k-block words in transit: [word column][row], pitch 20 (with the row swizzle of put
+  // and get, their 4-byte writes and 16-byte reads are free of bank conflicts)
   constexpr int TP = 20;
   __shared__ __attribute__((aligned(16))) uint32_t tbuf[2][NWC * TP];  // double buffered
   constexpr int PD = MS == 1 ? kPD : kPD / 2;  // register ring depth (a divisor of kPD)
@@ -664,7 +669,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                              live ? v[t].w : 0u};
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        ring[(8 * c8 + j) * RP + 16 * (r >> 4) + (r & 15)] =
+        ring[(8 * c8 + j) * RP + 8 * (((r >> 3) & 3) ^ (c8 & 7)) + (r & 7)] =
             (uint16_t)((j & 1) ? w[j >> 1] >> 16 : w[j >> 1]);
     }
     __syncthreads();
@@ -672,7 +677,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     for (int sec = 0; sec < 4; ++sec)
 #pragma unroll
       for (int i = 0; i < NMF; ++i) {
-        const uint4 bv = *reinterpret_cast<const uint4*>(&ring[(lcol + i) * RP + (sec >> 1) * 16 + 8 * khalf]);
+        const int col = lcol + i, beta = 2 * (sec >> 1) + khalf;
+        const uint4 bv = *reinterpret_cast<const uint4*>(&ring[col * RP + 8 * (beta ^ ((col >> 3) & 7))]);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
           y[ms][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[sec][ms]), as_bf16x8(bv), y[ms][i], 0, 0, 0);
@@ -767,7 +773,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     int rq[PD];
     uint4 wq[PD];
     uint4 aq[PD][MS];
-    uint32_t w8[8];  // this lane's 8 words (rows 8 khalf + 0..7, word column c)
+    // A k-block's words reach their lanes through tbuf: k-block kb is written to
+    // tbuf[kb & 1] LA + 1 steps before its use and read back LA steps before it, into
+    // w8[kb % LA], so the LDS round trip hides behind LA steps of work. One wavefront per
+    // workgroup executes its LDS operations in order.
+    constexpr int LA = PD >= 8 ? 2 : 1;
+    uint32_t w8[LA][8];  // this lane's 8 words (rows 8 khalf + 0..7, word column c)
     auto load_row = [&](int kb, int& r) { r = kr[16 * kb]; };
     auto load_kb = [&](int kb, int r, uint4& w, uint4 (&a)[MS]) {
       // 16-byte aligned: row offsets are multiples of D/2 = 16 * D/32, colbyte of 16
@@ -775,20 +786,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) a[ms] = ha[((size_t)kb * MS + ms) * 64];
     };
-    // A k-block's words reach their lanes through tbuf[kb & 1]: written two steps and read
-    // one step before use, so the LDS round trip hides behind a step's work. One
-    // wavefront per workgroup executes its LDS operations in order.
+    // word column w keeps its rows at [w][row ^ 8 (w / 8 % 2)]: the 8-row halves of
+    // columns 8-15 are swapped, so that the four 16-byte pieces of a row (words 4 la ..)
+    // that one write instruction covers fall in different LDS banks
     auto put = [&](int buf, const uint4& w) {  // row lr, words 4 la .. 4 la + 3
-      tbuf[buf][(4 * la + 0) * TP + lr] = w.x;
-      tbuf[buf][(4 * la + 1) * TP + lr] = w.y;
-      tbuf[buf][(4 * la + 2) * TP + lr] = w.z;
-      tbuf[buf][(4 * la + 3) * TP + lr] = w.w;
+      const int pr = lr ^ (8 * ((la >> 1) & 1));
+      tbuf[buf][(4 * la + 0) * TP + pr] = w.x;
+      tbuf[buf][(4 * la + 1) * TP + pr] = w.y;
+      tbuf[buf][(4 * la + 2) * TP + pr] = w.z;
+      tbuf[buf][(4 * la + 3) * TP + pr] = w.w;
     };
-    auto get = [&](int buf) {  // this lane's rows 8 khalf + 0..7 of word column c
-      const uint4 u0 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + 8 * khalf]);
-      const uint4 u1 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + 8 * khalf + 4]);
-      w8[0] = u0.x; w8[1] = u0.y; w8[2] = u0.z; w8[3] = u0.w;
-      w8[4] = u1.x; w8[5] = u1.y; w8[6] = u1.z; w8[7] = u1.w;
+    auto get = [&](int buf, uint32_t (&w)[8]) {  // this lane's rows 8 khalf + 0..7 of column c
+      const int ph = 8 * (khalf ^ ((c >> 3) & 1));
+      const uint4 u0 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + ph]);
+      const uint4 u1 = *reinterpret_cast<const uint4*>(&tbuf[buf][c * TP + ph + 4]);
+      w[0] = u0.x; w[1] = u0.y; w[2] = u0.z; w[3] = u0.w;
+      w[4] = u1.x; w[5] = u1.y; w[6] = u1.z; w[7] = u1.w;
     };
     // Prefetches past the last k-block re-read the last one (in bounds, never used), so
     // every path issues the same loads and the waits stay partial.
@@ -806,8 +819,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     put(0, wq[0]);
     put(1, wq[1]);
     __builtin_amdgcn_wave_barrier();
-    get(0);
+#pragma unroll
+    for (int j = 0; j < LA; ++j) get(j, w8[j]);
     __builtin_amdgcn_wave_barrier();
+    if constexpr (LA == 2) put(0, wq[2]);
 
     for (int kb0 = 0; kb0 < nkb; kb0 += PD) {
 #pragma unroll
@@ -817,7 +832,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         uint32_t bf[NMF][4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-          const uint32_t x = __builtin_amdgcn_perm(w8[2 * p + 1], w8[2 * p], psel);
+          const uint32_t x = __builtin_amdgcn_perm(w8[d % LA][2 * p + 1], w8[d % LA][2 * p], psel);
 #pragma unroll
           for (int i = 0; i < NMF; ++i) bf[i][p] = ((x >> (4 * i)) & nmask) | kMagic;
         }
@@ -832,9 +847,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         load_row(min(kb + 2 * PD, klast), rq[d]);
         // The wave barriers order the lanes' LDS accesses for the compiler and document
         // the wavefront-synchronous exchange (no instruction is emitted).
-        put(d & 1, wq[(d + 2) % PD]);  // k-block kb + 2 (loaded PD - 2 steps ago)
+        put((d + 1 + LA) & 1, wq[(d + 1 + LA) % PD]);  // k-block kb + LA + 1
         __builtin_amdgcn_wave_barrier();
-        get((d + 1) & 1);              // k-block kb + 1 (written one step ago)
+        get((d + LA) & 1, w8[d % LA]);                 // k-block kb + LA (written a step ago)
         __builtin_amdgcn_wave_barrier();
         if (kb + 1 == gend) {  // end of group g: y += (s_g - s_next) * acc
           const uint64_t rest = nonempty & ~((2ull << g) - 1ull);
