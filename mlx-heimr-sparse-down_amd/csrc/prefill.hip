@@ -31,12 +31,21 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = T * topk;
   for (int e = tid; e < E; e += kTT) cnt[e] = 0;
+  // The slots are ranked kTT at a time (chunk k: slots k kTT + tid). The first kTR chunks'
+  // ids are loaded together up front and their ranks stay in registers; later chunks go
+  // through rank_ws. Loads are never under a branch: ids past n re-read slot n - 1.
+  constexpr int kTR = 4;
+  const int nch = (n + kTT - 1) / kTT;
+  int e_r[kTR], rank_r[kTR];
+#pragma unroll
+  for (int k = 0; k < kTR; ++k) e_r[k] = sel[min(k * kTT + tid, n - 1)];
   __syncthreads();
-  for (int base = 0; base < n; base += kTT) {
+  // rank of slot base + tid among the slots of its expert (stable), or -1
+  auto chunk = [&](int base, int e) {
     for (int i = tid; i < 16 * E; i += kTT) wcnt[i] = 0;
     __syncthreads();
     const int s = base + tid;
-    int e = s < n ? sel[s] : -1;
+    if (s >= n) e = -1;
     if (s < n && (unsigned)e >= (unsigned)E) {
       if (status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
       e = -1;
@@ -53,26 +62,51 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
       todo &= ~mk;
     }
     __syncthreads();
-    for (int ee = tid; ee < E; ee += kTT) {  // exclusive scan over the waves, per expert
-      int run = cnt[ee];
-      for (int w = 0; w < 16; ++w) {
-        const int c = wcnt[w * E + ee];
-        wcnt[w * E + ee] = run;
-        run += c;
+    // exclusive scan over the 16 waves, per expert: 16 lanes per expert (lane group of 16
+    // within a wave), four experts per wave and round
+    for (int e0 = wave * 4; e0 < E; e0 += 64) {
+      const int ee = e0 + (lane >> 4), w = lane & 15;
+      const int c = ee < E ? wcnt[w * E + ee] : 0;
+      const int run = ee < E ? cnt[ee] : 0;  // read by all 16 lanes before lane 15 updates it
+      int incl = c;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const int u = __shfl_up(incl, off, 16);
+        if (w >= off) incl += u;
       }
-      cnt[ee] = run;
+      if (ee < E) {
+        wcnt[w * E + ee] = run + incl - c;
+        if (w == 15) cnt[ee] = run + incl;
+      }
     }
     __syncthreads();
-    if (s < n) rank_ws[s] = e >= 0 ? wcnt[wave * E + e] + rank_w : -1;
+    const int r = e >= 0 ? wcnt[wave * E + e] + rank_w : -1;
     __syncthreads();
+    return r;
+  };
+#pragma unroll
+  for (int k = 0; k < kTR; ++k)
+    if (k < nch) rank_r[k] = chunk(k * kTT, e_r[k]);
+  for (int k = kTR; k < nch; ++k) {
+    const int s = k * kTT + tid;
+    const int r = chunk(k * kTT, sel[min(s, n - 1)]);
+    if (s < n) rank_ws[s] = r;
   }
-  if (tid == 0) {
-    int run = 0;
-    for (int ee = 0; ee < E; ++ee) {
-      tbase[ee] = run;
-      run += (cnt[ee] + tt - 1) / tt;
+  {  // tile base per expert: exclusive scan of the tile counts over the workgroup
+    int* wtot = wcnt;  // 16 wave totals (the per-wave counts are no longer needed)
+    const int nt = tid < E ? (cnt[tid] + tt - 1) / tt : 0;
+    int incl = nt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += u;
     }
-    tbase[E] = run;
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wtot[w];
+    if (tid < E) tbase[tid] = before + incl - nt;
+    if (tid == kTT - 1) tbase[E] = before + incl;
   }
   __syncthreads();
   const int nt_routed = n / tt + E;
@@ -91,7 +125,13 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
   }
   for (int i = tid; i < nt_routed * tt; i += kTT) tile_slot[i] = -1;
   __syncthreads();  // the -1 fill is ordered before the scatter below (same workgroup)
-  for (int s = tid; s < n; s += kTT) {
+#pragma unroll
+  for (int k = 0; k < kTR; ++k) {
+    const int s = k * kTT + tid;
+    if (k < nch && s < n && rank_r[k] >= 0)
+      tile_slot[(tbase[e_r[k]] + rank_r[k] / tt) * tt + rank_r[k] % tt] = s;
+  }
+  for (int s = kTR * kTT + tid; s < n; s += kTT) {
     const int r = rank_ws[s];
     if (r < 0) continue;
     const int ee = sel[s];
@@ -144,7 +184,9 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
   const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS;
   int32_t* out = ulist + (size_t)tile * umax;
+  // the tile's expert and slot together (one round trip; loads never under a branch)
   const int e = tile_e[tile];
+  const int s = tile_slot[tile * tt + min(tid, tt - 1)];
   if (e < 0) {
     for (int i = tid; i < umax; i += kUT) out[i] = -1;
     if (tid == 0) ucount[tile] = 0;
@@ -152,27 +194,26 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
   }
   const bool shared = e >= E;
   const int FF = shared ? FS : F;
-  if (tid < tt) {
-    const int s = tile_slot[tile * tt + tid];
+  if (tid < tt)
     hoff[tid] = s < 0 ? -1 : (shared ? s * NR + topk * F : (s / topk) * NR + (s % topk) * F);
-  }
   __syncthreads();
   int base = 0;
   for (int c0 = 0; c0 < FF; c0 += 8 * kUT) {
     const int c = c0 + 8 * tid;
     uint32_t live = 0;  // bit j: column c + j is live in some slot of the tile
-    if (c < FF) {
-      // 8 slots' loads in flight at a time, then their OR
-      for (int m0 = 0; m0 < tt; m0 += 8) {
-        uint32_t lm[8];
+    // 16 slots' loads in flight at a time, then their OR; dead slots and columns past the
+    // row read h[0..7] and are dropped after the load (no load under a branch)
+    for (int m0 = 0; m0 < tt; m0 += 16) {
+      uint32_t lm[16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int o = m0 + i < tt ? hoff[m0 + i] : -1;
-          lm[i] = o >= 0 ? Live8<HDT>::get(h + (size_t)o + c) : 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) live |= lm[i];
+      for (int i = 0; i < 16; ++i) {
+        const int o = m0 + i < tt ? hoff[m0 + i] : -1;
+        const bool ok = o >= 0 && c < FF;
+        lm[i] = Live8<HDT>::get(h + (ok ? (size_t)o + c : 0));
+        lm[i] = ok ? lm[i] : 0u;
       }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) live |= lm[i];
     }
     // exclusive prefix of the live counts over the workgroup, in column order
     const int n = __popc(live);
