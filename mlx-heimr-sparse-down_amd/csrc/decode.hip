@@ -77,9 +77,13 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
     const uint16_t* __restrict__ spb, float* __restrict__ part, uint64_t* __restrict__ live_out,
     int32_t* __restrict__ status, Geom g, int B, int dense) {
   using HT = typename Elem<HDT>::T;
-  __shared__ HT hs[kGPW * kRS][64];                 // per team: the group's activations
+  // Per-team rows padded by 64 bytes, so that the team strides are 16 banks mod 32 and
+  // the four teams of a wavefront (16 lanes each) write different LDS banks.
+  constexpr int kHP = 64 + 64 / (int)sizeof(HT);
+  constexpr int kRedP = 8 * kWPC + 16;
+  __shared__ HT hs[kGPW * kRS][kHP];                // per team: the group's activations
   __shared__ uint8_t lst[kGPW * kRS][64];           // per team: the group's live rows, ascending
-  __shared__ float red[kGPW * kRS][8][kWPC];        // per team: group terms
+  __shared__ float red[kGPW * kRS][kRedP];          // per team: group terms [t][word]
   __shared__ float sum2[kDC][kRS * 2 + 1];
 
   const int logical = xcd_remap((int)blockIdx.x, B * g.nwg);
@@ -198,16 +202,18 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   const uint32_t b32[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    red[team][2 * i][l] = fmaf(lo_bf16(s32[i]), acc[2 * i], lo_bf16(b32[i]) * hsum);
-    red[team][2 * i + 1][l] = fmaf(hi_bf16(s32[i]), acc[2 * i + 1], hi_bf16(b32[i]) * hsum);
+    red[team][(2 * i) * kWPC + l] = fmaf(lo_bf16(s32[i]), acc[2 * i], lo_bf16(b32[i]) * hsum);
+    red[team][(2 * i + 1) * kWPC + l] = fmaf(hi_bf16(s32[i]), acc[2 * i + 1], hi_bf16(b32[i]) * hsum);
   }
   __syncthreads();
-  // level 1: kThreads/kDC threads per output, each over a contiguous run of groups
+  // level 1: kThreads/kDC threads per output, each over a contiguous run of groups. A
+  // thread takes word lw = o % 16 and nibble t = o / 16 (output 8 lw + t), so the lanes of
+  // a wavefront read consecutive words of red.
   constexpr int kL1 = kThreads / kDC;                 // 4 sub-sums per output
   constexpr int kGPS = kGPW / kL1;                    // groups per sub-sum
   {
     const int o = tid % kDC, s = tid / kDC;
-    const int lw = o >> 3, t = o & 7;
+    const int lw = o % kWPC, t = o / kWPC, col = 8 * lw + t;
     float acc2 = 0.0f;
     bool first = true;
 #pragma unroll
@@ -216,13 +222,13 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
       if (jj < ng) {
 #pragma unroll
         for (int ph = 0; ph < kRS; ++ph) {
-          const float v = red[ph * kGPW + jj][t][lw];
+          const float v = red[ph * kGPW + jj][t * kWPC + lw];
           acc2 = first ? v : acc2 + v;
           first = false;
         }
       }
     }
-    sum2[o][s] = acc2;
+    sum2[col][s] = acc2;
   }
   __syncthreads();
   if (tid < kDC) {
