@@ -54,8 +54,10 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
     uint64_t todo = __ballot(e >= 0);
     int rank_w = 0;
     while (todo) {
-      const int leader = __builtin_ctzll(todo);
-      const int le = __shfl(e, leader, 64);
+      // the leader is wave-uniform: its id comes over the scalar path (v_readlane), not
+      // through an LDS permute and its wait
+      const int leader = __builtin_amdgcn_readfirstlane(__builtin_ctzll(todo));
+      const int le = __builtin_amdgcn_readlane(e, leader);
       const uint64_t mk = __ballot(e == le);
       if (e == le) rank_w = __popcll(mk & ((1ull << lane) - 1ull));
       if (lane == leader) wcnt[wave * E + le] = __popcll(mk);
@@ -68,12 +70,13 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
       const int ee = e0 + (lane >> 4), w = lane & 15;
       const int c = ee < E ? wcnt[w * E + ee] : 0;
       const int run = ee < E ? cnt[ee] : 0;  // read by all 16 lanes before lane 15 updates it
+      // inclusive scan over the 16 lanes of a DPP row: row_shr:1,2,4,8 (lanes shifted in
+      // from outside the row read 0)
       int incl = c;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) {
-        const int u = __shfl_up(incl, off, 16);
-        if (w >= off) incl += u;
-      }
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);
       if (ee < E) {
         wcnt[w * E + ee] = run + incl - c;
         if (w == 15) cnt[ee] = run + incl;
@@ -201,19 +204,21 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
   for (int c0 = 0; c0 < FF; c0 += 8 * kUT) {
     const int c = c0 + 8 * tid;
     uint32_t live = 0;  // bit j: column c + j is live in some slot of the tile
-    // 16 slots' loads in flight at a time, then their OR; dead slots and columns past the
-    // row read h[0..7] and are dropped after the load (no load under a branch)
-    for (int m0 = 0; m0 < tt; m0 += 16) {
-      uint32_t lm[16];
+    // kUB slots' loads in flight at a time (a whole 32-slot tile for 16-bit h), then
+    // their OR; dead slots and columns past the row read h[0..7] and are dropped after
+    // the load (no load under a branch)
+    constexpr int kUB = sizeof(typename Elem<HDT>::T) == 2 ? 32 : 16;
+    for (int m0 = 0; m0 < tt; m0 += kUB) {
+      uint32_t lm[kUB];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < kUB; ++i) {
         const int o = m0 + i < tt ? hoff[m0 + i] : -1;
         const bool ok = o >= 0 && c < FF;
         lm[i] = Live8<HDT>::get(h + (ok ? (size_t)o + c : 0));
         lm[i] = ok ? lm[i] : 0u;
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) live |= lm[i];
+      for (int i = 0; i < kUB; ++i) live |= lm[i];
     }
     // exclusive prefix of the live counts over the workgroup, in column order
     const int n = __popc(live);
@@ -284,8 +289,160 @@ constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 
 // k-blocks per tile: at most 4 per group, plus the padding to a multiple of kPD
 __host__ __device__ constexpr int kb_max(int gmx) { return 4 * gmx + kPD; }
-__host__ __device__ constexpr int nkb_cap(int g) { return kb_max(g) / kPD * kPD; }
 __host__ __device__ constexpr int nch_max(int gmx) { return (gmx + 15) / 16; }
+
+// The GEMM's block schedule. GEMM workgroup b runs on XCD b % 8 (the hardware deals
+// workgroups to the XCDs in turn) and takes entry xcd_remap(b, n) of blk, so XCD x owns
+// the contiguous range [start_x, start_x + q_x) of blk, q_x = n / 8 or n / 8 + 1. An
+// entry is a block (tile * nblk + nb for column block nb of the tile, and the tile's
+// expert), or (-1, -1): no work.
+// Work is dealt by column stripe: span consecutive column blocks of one expert, 128
+// bytes of each weight row (whole cache lines). The tiles of an expert read the same
+// weight bytes in a stripe, so a stripe stays on one XCD with its tiles side by side in
+// the dispatch order, where they share those bytes in the XCD's L2. An expert deals its
+// stripes to the XCDs in turn, starting as many XCDs further on than the expert before
+// it as it has stripes (so the remainders rotate), which gives every XCD nearly the same
+// share of every expert. Within an XCD the experts come in descending order of their
+// largest tile and then by id: the longest blocks start first and the launch ends on
+// short ones. When the blocks do not fit the XCD ranges (too few empty tiles to spare),
+// blk is the identity. Only the schedule depends on blk; every block writes its own
+// outputs.
+constexpr int kOT = 1024;
+constexpr int kOrderMaxE = kOT - 1;  // experts the schedule supports (E + 1 runs <= kOT)
+
+// LDS ints the schedule uses with NTH threads (NTH >= E + 1)
+__host__ __device__ constexpr int sched_lds_ints(int nth) {
+  return 14 * nth + 2 * (nth / 64) * kXcds + 2 * kXcds + 1;
+}
+
+// The schedule, computed by one workgroup of NTH threads (thread r handles run r: expert
+// r, or the shared expert for r = E). The order key of an expert is its largest union
+// (ucount), which k_stage turns into the tile's k-block count, group padding aside.
+template <int NTH>
+__device__ __forceinline__ void sched_body(int tid, int* __restrict__ lds,
+                                           const int32_t* __restrict__ tile_e,
+                                           const int32_t* __restrict__ ucount,
+                                           int2* __restrict__ blk, int NT, int nblk, int span,
+                                           int E) {
+  int* rkey = lds;                    // 16-byte aligned: read as int4
+  int* rlen = rkey + NTH;
+  int* rmax = rlen + NTH;
+  int* rrank = rmax + NTH;
+  int* byrank = rrank + NTH;
+  int* rcnt = byrank + NTH;
+  int* base = rcnt + NTH;             // [kXcds][NTH]: blocks of the higher-ranked experts
+  int* wsum = base + kXcds * NTH;     // [NTH / 64][kXcds]
+  int* wbase = wsum + (NTH / 64) * kXcds;
+  int* tot = wbase + (NTH / 64) * kXcds;
+  int* st = tot + kXcds;              // [kXcds + 1]
+  const int R = E + 1, n = NT * nblk;
+  const int q = n / kXcds, rr = n % kXcds;
+  rlen[tid] = 0;
+  rmax[tid] = 0;
+  rcnt[tid] = 0;
+  byrank[tid] = -1;
+  if (tid <= kXcds) st[tid] = tid < rr ? tid * (q + 1) : rr * (q + 1) + (tid - rr) * q;
+  __syncthreads();
+  for (int t = tid; t < NT; t += NTH) {
+    const int e = tile_e[t], u = ucount[t];
+    if (e < 0 || e > E) continue;
+    atomicAdd(&rlen[e], 1);
+    atomicMax(&rmax[e], min(max(u, 0), 0xFFFF));
+  }
+  __syncthreads();
+  // unique keys, larger first: the largest union, then the lower id; -1 for no tiles
+  rkey[tid] = tid < R && rlen[tid] > 0 ? (rmax[tid] << 10 | (NTH - 1 - tid)) : -1;
+  __syncthreads();
+  if (rkey[tid] >= 0) {
+    const int k = rkey[tid];
+    const int4* k4 = reinterpret_cast<const int4*>(rkey);
+    int rk = 0;
+#pragma unroll 4
+    for (int r = 0; r < (R + 3) / 4; ++r) {
+      const int4 u = k4[r];
+      rk += (u.x > k) + (u.y > k) + (u.z > k) + (u.w > k);
+    }
+    rrank[tid] = rk;
+    byrank[rk] = tid;
+  }
+  __syncthreads();
+  // blocks the expert of rank tid puts on each XCD, and their exclusive prefix over ranks.
+  // Stripe u (column blocks u*span ..) goes to XCD (u + off) % 8; the last may be short.
+  const int U = (nblk + span - 1) / span, last = nblk - (U - 1) * span;
+  int v[kXcds], inc[kXcds];
+  const int off = (tid * U) & (kXcds - 1), me = byrank[tid];
+#pragma unroll
+  for (int x = 0; x < kXcds; ++x) {
+    const int x0 = (x - off) & (kXcds - 1);
+    const int nu = x0 < U ? (U - 1 - x0) / kXcds + 1 : 0;
+    const int nbx = nu * span - ((U - 1) % kXcds == x0 ? span - last : 0);
+    v[x] = me >= 0 ? rlen[me] * nbx : 0;
+    inc[x] = v[x];
+  }
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) {
+      const int u = __shfl_up(inc[x], s, 64);
+      if (lane >= s) inc[x] += u;
+    }
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) wsum[wv * kXcds + x] = inc[x];
+  }
+  __syncthreads();
+  if (tid < kXcds) {
+    int sm = 0;
+    for (int w = 0; w < NTH / 64; ++w) {
+      wbase[w * kXcds + tid] = sm;
+      sm += wsum[w * kXcds + tid];
+    }
+    tot[tid] = sm;
+  }
+  __syncthreads();
+  bool fits = true;
+#pragma unroll
+  for (int x = 0; x < kXcds; ++x) {
+    base[x * NTH + tid] = wbase[wv * kXcds + x] + inc[x] - v[x];
+    fits = fits && tot[x] <= st[x + 1] - st[x];
+  }
+  __syncthreads();
+  if (!fits) {  // identity: entry l is block l where its tile has an expert
+    for (int l = tid; l < n; l += NTH) {
+      const int e = tile_e[l / nblk];
+      blk[l] = e >= 0 && e <= E ? make_int2(l, e) : make_int2(-1, -1);
+    }
+    return;
+  }
+  for (int l = tid; l < n; l += NTH) {  // the unused tail of each XCD's range
+    int x = 0;
+#pragma unroll
+    for (int y = 1; y < kXcds; ++y) x += l >= st[y];
+    if (l - st[x] >= tot[x]) blk[l] = make_int2(-1, -1);
+  }
+  for (int t = tid; t < NT; t += NTH) {
+    const int e = tile_e[t];
+    if (e < 0 || e > E) continue;
+    const int k = atomicAdd(&rcnt[e], 1), i = rrank[e], L = rlen[e];
+    const int o = (i * U) & (kXcds - 1);
+    for (int nb = 0; nb < nblk; ++nb) {
+      const int u = nb / span, j = nb - u * span, x = (u + o) & (kXcds - 1);
+      blk[st[x] + base[x * NTH + i] + ((u / kXcds) * span + j) * L + k] = make_int2(t * nblk + nb, e);
+    }
+  }
+}
+
+// The schedule as a kernel of its own, for more experts than a staging workgroup has
+// threads.
+__global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_e,
+                                               const int32_t* __restrict__ ucount,
+                                               int2* __restrict__ blk, int NT, int nblk,
+                                               int span, int E) {
+  __shared__ __attribute__((aligned(16))) int lds[sched_lds_ints(kOT)];
+  sched_body<kOT>((int)threadIdx.x, lds, tile_e, ucount, blk, NT, nblk, span, E);
+}
 
 template <int MS>
 __global__ __launch_bounds__(kST) void k_stage(
@@ -293,7 +450,8 @@ __global__ __launch_bounds__(kST) void k_stage(
     const int32_t* __restrict__ tile_slot, const int32_t* __restrict__ ulist,
     const int32_t* __restrict__ ucount, int32_t* __restrict__ kbg, int32_t* __restrict__ krow,
     uint4* __restrict__ hc, uint4* __restrict__ hcor, uint4* __restrict__ dump, int D, int F,
-    int FS, int topk, int E, int umax, int GMX) {
+    int FS, int topk, int E, int umax, int GMX, int2* __restrict__ blk, int NT, int nblk,
+    int span, int fuse) {
   constexpr int TT = 32 * MS, kSplit = stage_split(MS), SPM = TT / kSplit;  // slots staged here
   constexpr int NUL = (kGMax * 64 + kST - 1) / kST;  // union list entries per thread
   // h rows of a gather batch, per slot GB groups x 64 values plus 8 of padding, so that
@@ -307,7 +465,15 @@ __global__ __launch_bounds__(kST) void k_stage(
   __shared__ __attribute__((aligned(16))) int prow[16 * kb_max(kGMax)];
   __shared__ float hsl[SPM][kGMax];
   __shared__ int kreal;            // k-blocks before the padding to a multiple of kPD
-  const int tile = blockIdx.x / kSplit, sp = blockIdx.x % kSplit, tid = threadIdx.x;
+  static_assert(ULS >= sched_lds_ints(kST), "the schedule reuses the union list's LDS");
+  // fuse: workgroup 0 computes the GEMM's block schedule (dispatched first, it runs
+  // beside the staging workgroups), the others stage tiles
+  if (fuse && blockIdx.x == 0) {
+    sched_body<kST>((int)threadIdx.x, uls, tile_e, ucount, blk, NT, nblk, span, E);
+    return;
+  }
+  const int bid = (int)blockIdx.x - fuse;
+  const int tile = bid / kSplit, sp = bid % kSplit, tid = threadIdx.x;
   const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
   int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
   // h is gathered in batches of GB groups: a batch is every 16-byte piece (8 per group,
@@ -486,134 +652,6 @@ __global__ __launch_bounds__(kST) void k_stage(
     hcor[((((size_t)tile * NCHMX + ch) * 4 + sec) * MS + (m >> 5)) * 64 + (m & 31) + 32 * khalf] =
         make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
                    v[6] | (v[7] << 16));
-  }
-}
-
-// The GEMM's block schedule. GEMM workgroup b runs on XCD b % 8 (the hardware deals
-// workgroups to the XCDs in turn) and takes entry xcd_remap(b, n) of blk, so XCD x owns
-// the contiguous range [start_x, start_x + q_x) of blk, q_x = n / 8 or n / 8 + 1. An
-// entry is a block (tile * nblk + nb for column block nb of the tile, and the tile's
-// expert), or (-1, -1): no work.
-// Work is dealt by column stripe: span consecutive column blocks of one expert, 128
-// bytes of each weight row (whole cache lines). The tiles of an expert read the same
-// weight bytes in a stripe, so a stripe stays on one XCD with its tiles side by side in
-// the dispatch order, where they share those bytes in the XCD's L2. An expert deals its
-// stripes to the XCDs in turn, starting as many XCDs further on than the expert before
-// it as it has stripes (so the remainders rotate), which gives every XCD nearly the same
-// share of every expert. Within an XCD the experts come in descending order of their
-// largest tile and then by id: the longest blocks start first and the launch ends on
-// short ones. When the blocks do not fit the XCD ranges (too few empty tiles to spare),
-// blk is the identity. Only the schedule depends on blk; every block writes its own
-// outputs.
-constexpr int kOT = 1024;
-constexpr int kOrderMaxE = kOT - 1;  // experts the schedule supports (E + 1 runs <= kOT)
-__global__ __launch_bounds__(kOT) void k_sched(const int32_t* __restrict__ tile_e,
-                                               const int32_t* __restrict__ kbg,
-                                               int2* __restrict__ blk, int NT, int nblk,
-                                               int span, int F, int FS, int E, int GMX) {
-  __shared__ __attribute__((aligned(16))) int rkey[kOT];
-  __shared__ int rlen[kOT], rmax[kOT], rrank[kOT], byrank[kOT], rcnt[kOT];
-  __shared__ int base[kXcds][kOT];  // per XCD: blocks of the higher-ranked experts
-  __shared__ int wsum[kOT / 64][kXcds], wbase[kOT / 64][kXcds];
-  __shared__ int tot[kXcds], st[kXcds + 1];
-  const int tid = threadIdx.x, R = E + 1, n = NT * nblk;  // run r = expert r (r = E: shared)
-  const int q = n / kXcds, rr = n % kXcds;
-  rlen[tid] = 0;
-  rmax[tid] = 0;
-  rcnt[tid] = 0;
-  byrank[tid] = -1;
-  if (tid <= kXcds) st[tid] = tid < rr ? tid * (q + 1) : rr * (q + 1) + (tid - rr) * q;
-  __syncthreads();
-  for (int t = tid; t < NT; t += kOT) {
-    // both candidate k-block totals are loaded with the expert id (one round trip)
-    const int32_t* kg = kbg + (size_t)t * (GMX + 1);
-    const int e = tile_e[t], kr = kg[F / 64], ks = kg[FS / 64];
-    if (e < 0 || e > E) continue;
-    atomicAdd(&rlen[e], 1);
-    atomicMax(&rmax[e], min(max(e >= E ? ks : kr, 0), nkb_cap(GMX)));
-  }
-  __syncthreads();
-  // unique keys, larger first: the largest tile, then the lower id; -1 for no tiles
-  rkey[tid] = tid < R && rlen[tid] > 0 ? (rmax[tid] << 10 | (kOT - 1 - tid)) : -1;
-  __syncthreads();
-  if (rkey[tid] >= 0) {
-    const int k = rkey[tid];
-    const int4* k4 = reinterpret_cast<const int4*>(rkey);
-    int rk = 0;
-#pragma unroll 4
-    for (int r = 0; r < (R + 3) / 4; ++r) {
-      const int4 u = k4[r];
-      rk += (u.x > k) + (u.y > k) + (u.z > k) + (u.w > k);
-    }
-    rrank[tid] = rk;
-    byrank[rk] = tid;
-  }
-  __syncthreads();
-  // blocks the expert of rank tid puts on each XCD, and their exclusive prefix over ranks.
-  // Stripe u (column blocks u*span ..) goes to XCD (u + off) % 8; the last may be short.
-  const int U = (nblk + span - 1) / span, last = nblk - (U - 1) * span;
-  int v[kXcds], inc[kXcds];
-  const int off = (tid * U) & (kXcds - 1), me = byrank[tid];
-#pragma unroll
-  for (int x = 0; x < kXcds; ++x) {
-    const int x0 = (x - off) & (kXcds - 1);
-    const int nu = x0 < U ? (U - 1 - x0) / kXcds + 1 : 0;
-    const int nbx = nu * span - ((U - 1) % kXcds == x0 ? span - last : 0);
-    v[x] = me >= 0 ? rlen[me] * nbx : 0;
-    inc[x] = v[x];
-  }
-  const int lane = tid & 63, wv = tid >> 6;
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-#pragma unroll
-    for (int x = 0; x < kXcds; ++x) {
-      const int u = __shfl_up(inc[x], s, 64);
-      if (lane >= s) inc[x] += u;
-    }
-  }
-  if (lane == 63) {
-#pragma unroll
-    for (int x = 0; x < kXcds; ++x) wsum[wv][x] = inc[x];
-  }
-  __syncthreads();
-  if (tid < kXcds) {
-    int s = 0;
-    for (int w = 0; w < kOT / 64; ++w) {
-      wbase[w][tid] = s;
-      s += wsum[w][tid];
-    }
-    tot[tid] = s;
-  }
-  __syncthreads();
-  bool fits = true;
-#pragma unroll
-  for (int x = 0; x < kXcds; ++x) {
-    base[x][tid] = wbase[wv][x] + inc[x] - v[x];
-    fits = fits && tot[x] <= st[x + 1] - st[x];
-  }
-  __syncthreads();
-  if (!fits) {  // identity: entry l is block l where its tile has an expert
-    for (int l = tid; l < n; l += kOT) {
-      const int e = tile_e[l / nblk];
-      blk[l] = e >= 0 && e <= E ? make_int2(l, e) : make_int2(-1, -1);
-    }
-    return;
-  }
-  for (int l = tid; l < n; l += kOT) {  // the unused tail of each XCD's range
-    int x = 0;
-#pragma unroll
-    for (int y = 1; y < kXcds; ++y) x += l >= st[y];
-    if (l - st[x] >= tot[x]) blk[l] = make_int2(-1, -1);
-  }
-  for (int t = tid; t < NT; t += kOT) {
-    const int e = tile_e[t];
-    if (e < 0 || e > E) continue;
-    const int k = atomicAdd(&rcnt[e], 1), i = rrank[e], L = rlen[e];
-    const int o = (i * U) & (kXcds - 1);
-    for (int nb = 0; nb < nblk; ++nb) {
-      const int u = nb / span, j = nb - u * span, x = (u + o) & (kXcds - 1);
-      blk[st[x] + base[x][i] + ((u / kXcds) * span + j) * L + k] = make_int2(t * nblk + nb, e);
-    }
   }
 }
 
@@ -1115,33 +1153,38 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
   int2* blk = reinterpret_cast<int2*>(ws + w.blk);
   uint4* dump = reinterpret_cast<uint4*>(ws + w.dump);
   const int GMX = (int)((F > FS ? F : FS) / 64);
-  if (tt == 32) {
-    hipLaunchKernelGGL(k_stage<1>, dim3((unsigned)(NT * stage_split(1))), dim3(kST), 0, st, h, tile_e, tile_slot,
-                       ulist, ucount, kbg, krow, hc, hcor, dump, (int)D, (int)F, (int)FS,
-                       (int)topk, (int)E, (int)umax, GMX);
-    int rc = check_launch(fn);
+  // The schedule runs inside the staging launch (its workgroup 0) when a staging
+  // workgroup has a thread per expert; otherwise as a kernel of its own.
+  const int fuse = E + 1 <= kST ? 1 : 0;
+  const int MS = tt == 32 ? 1 : 2;
+  const int nblk = (int)(D / (128 / MS)), span = 2 * MS;
+  if (!fuse) {
+    hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, ucount, blk, (int)NT, nblk,
+                       span, (int)E);
+    const int rc = check_launch(fn);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
-                       (int)(D / 128), 2, (int)F, (int)FS, (int)E, GMX);
-    rc = check_launch(fn);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * (D / 128))), dim3(64), 0, st,
-                       tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
-                       blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
-  } else {
-    hipLaunchKernelGGL(k_stage<2>, dim3((unsigned)(NT * stage_split(2))), dim3(kST), 0, st, h, tile_e, tile_slot,
-                       ulist, ucount, kbg, krow, hc, hcor, dump, (int)D, (int)F, (int)FS,
-                       (int)topk, (int)E, (int)umax, GMX);
-    int rc = check_launch(fn);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_sched, dim3(1), dim3(kOT), 0, st, tile_e, kbg, blk, (int)NT,
-                       (int)(D / 64), 4, (int)F, (int)FS, (int)E, GMX);
-    rc = check_launch(fn);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * (D / 64))), dim3(64), 0, st,
-                       tile_slot, gains, kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part,
-                       blk, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)NT, GMX);
   }
+  const dim3 sgrid((unsigned)(NT * stage_split(MS) + fuse));
+  if (MS == 1)
+    hipLaunchKernelGGL(k_stage<1>, sgrid, dim3(kST), 0, st, h, tile_e, tile_slot, ulist, ucount, kbg,
+                       krow, hc, hcor, dump, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)umax,
+                       GMX, blk, (int)NT, nblk, span, fuse);
+  else
+    hipLaunchKernelGGL(k_stage<2>, sgrid, dim3(kST), 0, st, h, tile_e, tile_slot, ulist, ucount, kbg,
+                       krow, hc, hcor, dump, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)umax,
+                       GMX, blk, (int)NT, nblk, span, fuse);
+  {
+    const int rc = check_launch(fn);
+    if (rc) return rc;
+  }
+  if (MS == 1)
+    hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(NT * nblk)), dim3(64), 0, st, tile_slot, gains,
+                       kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part, blk, (int)D, (int)F,
+                       (int)FS, (int)topk, (int)E, (int)NT, GMX);
+  else
+    hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(NT * nblk)), dim3(64), 0, st, tile_slot, gains,
+                       kbg, krow, hc, hcor, pw, ps, pb, spw, sps, spb, part, blk, (int)D, (int)F,
+                       (int)FS, (int)topk, (int)E, (int)NT, GMX);
   int rc = check_launch(fn);
   if (rc) return rc;
   const unsigned sg = (unsigned)((T * (D / 4) + 255) / 256);

@@ -70,11 +70,12 @@ def test_prefill_gemm_matches_oracle(layer, dev, T, tt, zf):
     assert err.max() <= 1e-4 * scale
 
 
-@pytest.mark.parametrize("tt", [32, 64])
-def test_prefill_gemm_small_shapes(dev, tt):
-    """D=256, F=128, FS=192, 8 experts, top-2: two and three 64-row groups, two column
-    blocks; dense, sparse and all-zero activations."""
-    d, f, fs, e, k, T = 256, 128, 192, 8, 2, 70
+@pytest.mark.parametrize("tt,e", [(32, 8), (64, 8), (32, 300)])
+def test_prefill_gemm_small_shapes(dev, tt, e):
+    """D=256, F=128, FS=192, top-2: two and three 64-row groups, two column blocks; dense,
+    sparse and all-zero activations. 8 experts: the block schedule runs in the staging
+    launch; 300 experts (more than a staging workgroup has threads): its own kernel."""
+    d, f, fs, k, T = 256, 128, 192, 2, 70
     lay = S.moe_layer_np(5, n_experts=e, d=d, f=f, fs=fs)
     dv = {n: S.to_device(v, dev) for n, v in lay.items()}
     nm = layout.to_neuron_major(dv["w"], dv["s"], dv["b"]) + layout.to_neuron_major(dv["sw"], dv["ss"], dv["sb"])
