@@ -193,12 +193,22 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   const int ngrp = DI / NG;
   const int r = blockIdx.x / ngrp, gi = blockIdx.x - (blockIdx.x / ngrp) * ngrp;
   const int per = NG / kMT;
-  float z[8], nw[8];
-  float ss = 0.0f;
-  for (int i = 0; i < per; ++i) {  // every load (activations, gate, weight) before the reduction
-    const int c = gi * NG + i * kMT + threadIdx.x;
+  constexpr int kPerMax = 8;       // NG <= 8 kMT (checked by the host)
+  // every load (activations, gate, weight) in one round trip: slices past per re-read
+  // the last one and are dropped (no load under a branch)
+  float yv[kPerMax], gv[kPerMax], nw[kPerMax];
+#pragma unroll
+  for (int i = 0; i < kPerMax; ++i) {
+    const int c = gi * NG + min(i, per - 1) * kMT + threadIdx.x;
     nw[i] = bf16_bits_to_f32(norm_w[c]);
-    z[i] = y_pre[(size_t)r * DI + c] * silu_f32(bf16_bits_to_f32(gate[(size_t)r * gate_ld + c]));
+    yv[i] = y_pre[(size_t)r * DI + c];
+    gv[i] = bf16_bits_to_f32(gate[(size_t)r * gate_ld + c]);
+  }
+  float z[kPerMax];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPerMax; ++i) {
+    z[i] = i < per ? yv[i] * silu_f32(gv[i]) : 0.0f;
     ss = fmaf(z[i], z[i], ss);
   }
   ss = wave_sum(ss);
@@ -207,7 +217,9 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   float tot = wsum[0];
   for (int w = 1; w < kMT / 64; ++w) tot += wsum[w];
   const float inv = 1.0f / sqrtf(tot / (float)NG + eps);
-  for (int i = 0; i < per; ++i) {
+#pragma unroll
+  for (int i = 0; i < kPerMax; ++i) {
+    if (i >= per) break;
     const int c = gi * NG + i * kMT + threadIdx.x;
     Elem<YDT>::store(y, (size_t)r * DI + c, (z[i] * inv) * nw[i]);
   }
