@@ -20,80 +20,106 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kTT = 1024;  // threads of the tile-order kernel
 
 __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, int T, int topk,
-                                               int E, int tt, int32_t* __restrict__ tile_e,
+                                               int E, int tt, int P,
+                                               int32_t* __restrict__ tile_e,
                                                int32_t* __restrict__ tile_slot,
                                                int32_t* __restrict__ status,
                                                int32_t* __restrict__ rank_ws) {
   extern __shared__ int sh[];
   int* cnt = sh;                    // [E] running count per expert, then counts
   int* tbase = sh + E;              // [E + 1] tile base per expert (exclusive scan)
-  int* wcnt = sh + 2 * E + 1;       // [16][E] per-wave counts of the current chunk
+  int* wcnt = sh + 2 * E + 1;       // [P][16][E] per-(chunk, wave) counts of a pass
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = T * topk;
+  const int nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));  // bits of an expert id
   for (int e = tid; e < E; e += kTT) cnt[e] = 0;
-  // The slots are ranked kTT at a time (chunk k: slots k kTT + tid). The first kTR chunks'
-  // ids are loaded together up front and their ranks stay in registers; later chunks go
-  // through rank_ws. Loads are never under a branch: ids past n re-read slot n - 1.
+  // The slots are ranked kTT at a time (chunk k: slots k kTT + tid), P chunks per pass
+  // (P = kTR when the pass's counts fit in LDS, else 1) with one set of barriers per pass.
+  // With P = kTR the first pass's ids are loaded up front and its ranks stay in
+  // registers; the other ranks go through rank_ws. Loads are never under a branch: ids
+  // past n re-read slot n - 1.
   constexpr int kTR = 4;
   const int nch = (n + kTT - 1) / kTT;
   int e_r[kTR], rank_r[kTR];
 #pragma unroll
   for (int k = 0; k < kTR; ++k) e_r[k] = sel[min(k * kTT + tid, n - 1)];
-  __syncthreads();
-  // rank of slot base + tid among the slots of its expert (stable), or -1
-  auto chunk = [&](int base, int e) {
-    for (int i = tid; i < 16 * E; i += kTT) wcnt[i] = 0;
+  // ranks of chunks k0 .. k0 + np - 1 (np <= P), ids in ev; ranks (stable among the slots
+  // of an expert, or -1) into rk
+  auto pass = [&](int k0, int np, int (&ev)[kTR], int (&rk)[kTR]) {
+    for (int i = tid; i < np * 16 * E; i += kTT) wcnt[i] = 0;
     __syncthreads();
-    const int s = base + tid;
-    if (s >= n) e = -1;
-    if (s < n && (unsigned)e >= (unsigned)E) {
-      if (status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
-      e = -1;
-    }
-    // rank among the lanes of this wave with the same expert, lowest lane first
-    uint64_t todo = __ballot(e >= 0);
-    int rank_w = 0;
-    while (todo) {
-      // the leader is wave-uniform: its id comes over the scalar path (v_readlane), not
-      // through an LDS permute and its wait
-      const int leader = __builtin_amdgcn_readfirstlane(__builtin_ctzll(todo));
-      const int le = __builtin_amdgcn_readlane(e, leader);
-      const uint64_t mk = __ballot(e == le);
-      if (e == le) rank_w = __popcll(mk & ((1ull << lane) - 1ull));
-      if (lane == leader) wcnt[wave * E + le] = __popcll(mk);
-      todo &= ~mk;
+    int rw[kTR];
+#pragma unroll
+    for (int k = 0; k < kTR; ++k) {
+      rw[k] = 0;
+      if (k >= np) continue;  // uniform
+      const int s = (k0 + k) * kTT + tid;
+      int e = ev[k];
+      if (s >= n) e = -1;
+      if (s < n && (unsigned)e >= (unsigned)E) {
+        if (status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+        e = -1;
+      }
+      ev[k] = e;
+      // rank among the lanes of this wave with the same expert, lowest lane first: the
+      // lanes whose id equals this lane's are the AND over the id's bits of that bit's
+      // ballot or its complement (one ballot per bit, no loop over distinct experts);
+      // the lowest such lane writes the wave's count
+      uint64_t eq = __ballot(e >= 0);
+      for (int b = 0; b < nbits; ++b) {  // uniform
+        const bool bit = (e >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        eq &= bit ? m : ~m;
+      }
+      const uint64_t below = eq & ((1ull << lane) - 1ull);
+      rw[k] = __popcll(below);
+      if (e >= 0 && below == 0ull) wcnt[(k * 16 + wave) * E + e] = __popcll(eq);
     }
     __syncthreads();
-    // exclusive scan over the 16 waves, per expert: 16 lanes per expert (lane group of 16
-    // within a wave), four experts per wave and round
+    // exclusive scan over (chunk, wave) in slot order, per expert: 16 lanes per expert
+    // (one DPP row, lane w = wave w), four experts per wave and round
     for (int e0 = wave * 4; e0 < E; e0 += 64) {
       const int ee = e0 + (lane >> 4), w = lane & 15;
-      const int c = ee < E ? wcnt[w * E + ee] : 0;
-      const int run = ee < E ? cnt[ee] : 0;  // read by all 16 lanes before lane 15 updates it
-      // inclusive scan over the 16 lanes of a DPP row: row_shr:1,2,4,8 (lanes shifted in
-      // from outside the row read 0)
-      int incl = c;
-      incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);
-      incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);
-      incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);
-      incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);
-      if (ee < E) {
-        wcnt[w * E + ee] = run + incl - c;
-        if (w == 15) cnt[ee] = run + incl;
+      int run = ee < E ? cnt[ee] : 0;  // read by all 16 lanes before lane 15 updates it
+#pragma unroll
+      for (int k = 0; k < kTR; ++k) {
+        if (k >= np) continue;  // uniform
+        const int c = ee < E ? wcnt[(k * 16 + w) * E + ee] : 0;
+        // inclusive scan over the 16 lanes of a DPP row: row_shr:1,2,4,8 (lanes shifted
+        // in from outside the row read 0)
+        int incl = c;
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);
+        const int tot = __shfl(incl, lane | 15, 64);
+        if (ee < E) wcnt[(k * 16 + w) * E + ee] = run + incl - c;
+        run += tot;
       }
+      if (ee < E && w == 15) cnt[ee] = run;
     }
     __syncthreads();
-    const int r = e >= 0 ? wcnt[wave * E + e] + rank_w : -1;
-    __syncthreads();
-    return r;
-  };
 #pragma unroll
-  for (int k = 0; k < kTR; ++k)
-    if (k < nch) rank_r[k] = chunk(k * kTT, e_r[k]);
-  for (int k = kTR; k < nch; ++k) {
-    const int s = k * kTT + tid;
-    const int r = chunk(k * kTT, sel[min(s, n - 1)]);
-    if (s < n) rank_ws[s] = r;
+    for (int k = 0; k < kTR; ++k)
+      if (k < np) rk[k] = ev[k] >= 0 ? wcnt[(k * 16 + wave) * E + ev[k]] + rw[k] : -1;
+    __syncthreads();  // the counts are read before the next pass clears them
+  };
+  int k0 = 0;
+  if (P == kTR) {
+    pass(0, min(kTR, nch), e_r, rank_r);
+    k0 = kTR;
+  }
+  for (; k0 < nch; k0 += P) {
+    const int np = min(P, nch - k0);
+    int ev[kTR], rk[kTR];
+#pragma unroll
+    for (int k = 0; k < kTR; ++k) ev[k] = sel[min((k0 + min(k, np - 1)) * kTT + tid, n - 1)];
+    pass(k0, np, ev, rk);
+#pragma unroll
+    for (int k = 0; k < kTR; ++k) {
+      const int s = (k0 + k) * kTT + tid;
+      if (k < np && s < n) rank_ws[s] = rk[k];
+    }
   }
   {  // tile base per expert: exclusive scan of the tile counts over the workgroup
     int* wtot = wcnt;  // 16 wave totals (the per-wave counts are no longer needed)
@@ -128,13 +154,14 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
   }
   for (int i = tid; i < nt_routed * tt; i += kTT) tile_slot[i] = -1;
   __syncthreads();  // the -1 fill is ordered before the scatter below (same workgroup)
+  const int nreg = P == kTR ? min(kTR, nch) : 0;  // chunks whose ranks stayed in registers
 #pragma unroll
   for (int k = 0; k < kTR; ++k) {
     const int s = k * kTT + tid;
-    if (k < nch && s < n && rank_r[k] >= 0)
+    if (k < nreg && s < n && rank_r[k] >= 0)
       tile_slot[(tbase[e_r[k]] + rank_r[k] / tt) * tt + rank_r[k] % tt] = s;
   }
-  for (int s = kTR * kTT + tid; s < n; s += kTT) {
+  for (int s = nreg * kTT + tid; s < n; s += kTT) {
     const int r = rank_ws[s];
     if (r < 0) continue;
     const int ee = sel[s];
@@ -1043,10 +1070,12 @@ extern "C" int hsd_prefill_tiles(const int32_t* sel, int64_t T, int64_t topk, in
   const size_t need = hsd_prefill_tiles_workspace_bytes(T, topk, E);
   if (!workspace || workspace_bytes < need)
     return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
-  const size_t lds = (size_t)(2 * E + 1 + 16 * E) * sizeof(int);
+  // four chunks of 1024 slots per pass when their per-wave counts fit in 64 KB of LDS
+  const int P = (2 * E + 1 + 4 * 16 * E) * sizeof(int) <= 65536 ? 4 : 1;
+  const size_t lds = (size_t)(2 * E + 1 + P * 16 * E) * sizeof(int);
   if (lds > 65536) return set_error(HSD_ERR_SHAPE, "%s: E too large for LDS", fn);
   hipLaunchKernelGGL(k_tiles, dim3(1), dim3(kTT), lds, as_stream(stream), sel, (int)T, (int)topk,
-                     (int)E, (int)tt, tile_e, tile_slot, dev_status,
+                     (int)E, (int)tt, P, tile_e, tile_slot, dev_status,
                      reinterpret_cast<int32_t*>(workspace));
   return check_launch(fn);
 }
