@@ -478,7 +478,7 @@ __global__ __launch_bounds__(kST) void k_stage(
     const int32_t* __restrict__ ucount, int32_t* __restrict__ kbg, int32_t* __restrict__ krow,
     uint4* __restrict__ hc, uint4* __restrict__ hcor, uint4* __restrict__ dump, int D, int F,
     int FS, int topk, int E, int umax, int GMX, int2* __restrict__ blk, int NT, int nblk,
-    int span, int fuse) {
+    int span, int fuse, int sh0) {
   constexpr int TT = 32 * MS, kSplit = stage_split(MS), SPM = TT / kSplit;  // slots staged here
   constexpr int NUL = (kGMax * 64 + kST - 1) / kST;  // union list entries per thread
   // h rows of a gather batch, per slot GB groups x 64 values plus 8 of padding, so that
@@ -499,8 +499,14 @@ __global__ __launch_bounds__(kST) void k_stage(
     sched_body<kST>((int)threadIdx.x, uls, tile_e, ucount, blk, NT, nblk, span, E);
     return;
   }
+  // Workgroups past NT kSplit take the second half of a shared-expert tile (tiles sh0..):
+  // a shared tile has twice the groups of a routed one, so its batches of GB groups (and
+  // their correction chunks) alternate between two workgroups per slot set.
   const int bid = (int)blockIdx.x - fuse;
-  const int tile = bid / kSplit, sp = bid % kSplit, tid = threadIdx.x;
+  const bool second = bid >= NT * kSplit;
+  const int bb = second ? bid - NT * kSplit : bid;
+  const int tile = second ? sh0 + bb / kSplit : bb / kSplit, sp = bb % kSplit, tid = threadIdx.x;
+  const int nhalf = tile >= sh0 ? 2 : 1, half = second ? 1 : 0;
   const int KMX = 16 * kb_max(GMX), KBMX = kb_max(GMX), NCHMX = nch_max(GMX);
   int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
   // h is gathered in batches of GB groups: a batch is every 16-byte piece (8 per group,
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(kST) void k_stage(
 #pragma unroll
   for (int i = 0; i < NLI; ++i) slot[i] = tile_slot[tile * TT + sp + kSplit * ((tid + kST * i) / (GB * 8))];
   if (e < 0) {
-    if (sp == 0)
+    if (sp == 0 && half == 0)
       for (int g = tid; g <= GMX; g += kST) kbgT[g] = 0;
     return;
   }
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(kST) void k_stage(
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
       const int g = GB * bt + (item / 8) % GB;
-      const bool ok = o >= 0 && g < G;
+      const bool ok = o >= 0 && g < G && bt % nhalf == half;
       pv[bt][i] = *reinterpret_cast<const uint4*>(h + (ok ? (size_t)o + 64 * g + 8 * pc : 0));
     }
   }
@@ -574,7 +580,7 @@ __global__ __launch_bounds__(kST) void k_stage(
   }
   lds_barrier();
   const int nkb = kbs[G], nreal = kreal;
-  if (sp == 0)
+  if (sp == 0 && half == 0)
     for (int g = tid; g <= GMX; g += kST) kbgT[g] = kbs[g < G ? g : G];
   // padded row list: position 16 kbs[g] + j holds union row gs[g] + j of group g; the
   // rest of the group's k-blocks and the trailing zero k-blocks are padding
@@ -590,11 +596,11 @@ __global__ __launch_bounds__(kST) void k_stage(
       if ((unsigned)r >= (unsigned)FF) r = -1;
     }
     prow[p] = r;
-    if (sp == 0) krow[(size_t)tile * KMX + p] = r >= 0 ? r * (D / 2) : kPadRow;
+    if (sp == 0 && half == 0) krow[(size_t)tile * KMX + p] = r >= 0 ? r * (D / 2) : kPadRow;
   }
   for (int p = 16 * nreal + tid; p < 16 * nkb; p += kST) {
     prow[p] = -1;
-    if (sp == 0) krow[(size_t)tile * KMX + p] = kPadRow;
+    if (sp == 0 && half == 0) krow[(size_t)tile * KMX + p] = kPadRow;
   }
   lds_barrier();
   // A fragments, a batch of GB groups at a time: its pieces (loaded above) go to LDS over
@@ -607,6 +613,7 @@ __global__ __launch_bounds__(kST) void k_stage(
   for (int bt = 0; bt < NBT; ++bt) {
     const int g0 = GB * bt;
     if (g0 >= G) break;
+    if (bt % nhalf != half) continue;  // the other workgroup's batch (uniform)
     lds_barrier();  // the previous batch is assembled (the union list read)
 #pragma unroll
     for (int i = 0; i < NLI; ++i) {
@@ -652,7 +659,7 @@ __global__ __launch_bounds__(kST) void k_stage(
     for (int f = 0; f < NFR; ++f) *dst[f] = fr[f];
   }
   // the padding k-blocks (at most kPD - 1) hold zero fragments
-  for (int it = tid; it < (nkb - nreal) * SPM * 2; it += kST) {
+  for (int it = tid; it < (half == 0 ? nkb - nreal : 0) * SPM * 2; it += kST) {
     const int kb = nreal + it / (2 * SPM), jj = (it >> 1) % SPM, half = it & 1;
     const int m = sp + kSplit * jj;
     hc[(((size_t)tile * KBMX + kb) * MS + (m >> 5)) * 64 + (m & 31) + 32 * half] = make_uint4(0, 0, 0, 0);
@@ -661,10 +668,12 @@ __global__ __launch_bounds__(kST) void k_stage(
   // correction A fragments of this workgroup's slots, 16 groups per chunk: sections
   // [hs_hi, hs_lo, -128 hs_hi, -128 hs_lo]; hs = hs_hi + hs_lo to about 16 bits, -128 x
   // is exact in bf16
+  static_assert(GB == 16, "a correction chunk (16 groups) is one gather batch");
   const int NCH = (G + 15) >> 4;
   for (int it = tid; it < NCH * 4 * SPM * 2; it += kST) {
     const int khalf = it & 1, jj = (it >> 1) % SPM, sec = (it / (2 * SPM)) & 3,
               ch = it / (8 * SPM);
+    if (ch % nhalf != half) continue;  // the other workgroup's chunk: its groups' hs
     const int m = sp + kSplit * jj;
     uint32_t v[8];
 #pragma unroll
@@ -1193,15 +1202,16 @@ extern "C" int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const flo
     const int rc = check_launch(fn);
     if (rc) return rc;
   }
-  const dim3 sgrid((unsigned)(NT * stage_split(MS) + fuse));
+  const int64_t nt_shared = (T + tt - 1) / tt, sh0 = NT - nt_shared;
+  const dim3 sgrid((unsigned)((NT + nt_shared) * stage_split(MS) + fuse));
   if (MS == 1)
     hipLaunchKernelGGL(k_stage<1>, sgrid, dim3(kST), 0, st, h, tile_e, tile_slot, ulist, ucount, kbg,
                        krow, hc, hcor, dump, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)umax,
-                       GMX, blk, (int)NT, nblk, span, fuse);
+                       GMX, blk, (int)NT, nblk, span, fuse, (int)sh0);
   else
     hipLaunchKernelGGL(k_stage<2>, sgrid, dim3(kST), 0, st, h, tile_e, tile_slot, ulist, ucount, kbg,
                        krow, hc, hcor, dump, (int)D, (int)F, (int)FS, (int)topk, (int)E, (int)umax,
-                       GMX, blk, (int)NT, nblk, span, fuse);
+                       GMX, blk, (int)NT, nblk, span, fuse, (int)sh0);
   {
     const int rc = check_launch(fn);
     if (rc) return rc;
