@@ -30,6 +30,13 @@ constexpr int kN = 128;      // state size (16 lanes per state row, 8 elements e
 constexpr int kK = 4;        // conv kernel
 constexpr int kLMax = 7;     // rows per verify (nslab <= 8)
 
+// v read from another lane of the same 16-lane row by a DPP control (every source lane
+// of the controls used here is inside the row)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     const uint16_t* __restrict__ conv_in, int64_t cin_ld, const uint16_t* __restrict__ dt_raw,
     int64_t dt_ld, const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ conv_b,
@@ -172,10 +179,14 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     y = fmaf(S1.y, C1.y, y);
     y = fmaf(S1.z, C1.z, y);
     y = fmaf(S1.w, C1.w, y);
-    y += __shfl_xor(y, 1, 64);
-    y += __shfl_xor(y, 2, 64);
-    y += __shfl_xor(y, 4, 64);
-    y += __shfl_xor(y, 8, 64);
+    // the 16-lane sum with DPP, no LDS permute: xor 1 and xor 2 inside each quad
+    // (quad_perm), then the other quad of each 8 (row_half_mirror) and the other 8 of the
+    // row (row_mirror); after the first two steps a quad holds one value, so the mirrors
+    // add the same partial sums as xor 4 and xor 8
+    y += dpp_f32<0xB1>(y);   // quad_perm [1, 0, 3, 2]
+    y += dpp_f32<0x4E>(y);   // quad_perm [2, 3, 0, 1]
+    y += dpp_f32<0x141>(y);  // row_half_mirror
+    y += dpp_f32<0x140>(y);  // row_mirror
     if (c8 == 0) y_pre[(size_t)r * DI + (size_t)hh * P + p] = y + x * Dh;
   }
 }
