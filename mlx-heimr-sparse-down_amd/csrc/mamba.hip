@@ -30,13 +30,6 @@ constexpr int kN = 128;      // state size (16 lanes per state row, 8 elements e
 constexpr int kK = 4;        // conv kernel
 constexpr int kLMax = 7;     // rows per verify (nslab <= 8)
 
-// v read from another lane of the same 16-lane row by a DPP control (every source lane
-// of the controls used here is inside the row)
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
 __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     const uint16_t* __restrict__ conv_in, int64_t cin_ld, const uint16_t* __restrict__ dt_raw,
     int64_t dt_ld, const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ conv_b,

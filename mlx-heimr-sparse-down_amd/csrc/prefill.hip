@@ -623,9 +623,11 @@ __global__ __launch_bounds__(kST) void k_stage(
       float s8 = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) s8 += bf16_bits_to_f32((j & 1) ? w[j >> 1] >> 16 : w[j >> 1] & 0xFFFFu);
-      s8 += __shfl_xor(s8, 1, 64);
-      s8 += __shfl_xor(s8, 2, 64);
-      s8 += __shfl_xor(s8, 4, 64);
+      // the 8-lane sum with DPP (quad_perm xor 1, xor 2, then the other quad of the 8 by
+      // row_half_mirror), no LDS permute
+      s8 += dpp_f32<0xB1>(s8);
+      s8 += dpp_f32<0x4E>(s8);
+      s8 += dpp_f32<0x141>(s8);
       if (pc == 0 && g0 + gl < G) hsl[jj][g0 + gl] = s8;
     }
     lds_barrier();
