@@ -762,6 +762,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   };
   uint4 a0[4][MS], v0[NIT], a1[4][MS], v1[NIT];
   load_chunk(0, a0, v0);
+  // the tile's k-block group starts: with the first round trip too (unconditional loads)
+  const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
+  const int kv0 = kbgT[min(l, G)], kn0 = kbgT[min(l + 1, G)];
   f32x16 y[MS][NMF];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
@@ -816,8 +819,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
   }
 
-  const int32_t* kbgT = kbg + (size_t)tile * (GMX + 1);
-  const int kv0 = kbgT[min(l, G)], kn0 = kbgT[min(l + 1, G)];  // unconditional loads
   const int kv = l <= G ? kv0 : 0;
   const int kn = l < G ? kn0 : 0;
   const uint64_t nonempty = __ballot(l < G && kn > kv);
