@@ -95,6 +95,20 @@ __device__ __forceinline__ float softplus_f32(float x) {
   return x > 20.0f ? x : log1pf(expf(x));
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront without LDS: a DPP scan inside
+// each 16-lane row (row_shr 1, 2, 4, 8; lanes shifted in from outside the row read 0),
+// then the totals of the lower rows (v_readlane of lanes 15, 31, 47) added per row.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+
 // Deterministic butterfly sum over the 64 lanes of a wavefront (same tree on every
 // call, so equal inputs give equal bits).
 __device__ __forceinline__ float wave_sum(float v) {

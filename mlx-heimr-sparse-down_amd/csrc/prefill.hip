@@ -124,12 +124,7 @@ __global__ __launch_bounds__(kTT) void k_tiles(const int32_t* __restrict__ sel, 
   {  // tile base per expert: exclusive scan of the tile counts over the workgroup
     int* wtot = wcnt;  // 16 wave totals (the per-wave counts are no longer needed)
     const int nt = tid < E ? (cnt[tid] + tt - 1) / tt : 0;
-    int incl = nt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int u = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += u;
-    }
+    const int incl = wave_incl_scan(nt, lane);
     if (lane == 63) wtot[wave] = incl;
     __syncthreads();
     int before = 0;
@@ -249,12 +244,7 @@ __global__ __launch_bounds__(kUT) void k_union(const typename Elem<HDT>::T* __re
     }
     // exclusive prefix of the live counts over the workgroup, in column order
     const int n = __popc(live);
-    int incl = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
+    const int incl = wave_incl_scan(n, lane);
     if (lane == 63) wsum[wave] = incl;
     __syncthreads();
     int before = base, tot = 0;
@@ -408,13 +398,7 @@ __device__ __forceinline__ void sched_body(int tid, int* __restrict__ lds,
   }
   const int lane = tid & 63, wv = tid >> 6;
 #pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-#pragma unroll
-    for (int x = 0; x < kXcds; ++x) {
-      const int u = __shfl_up(inc[x], s, 64);
-      if (lane >= s) inc[x] += u;
-    }
-  }
+  for (int x = 0; x < kXcds; ++x) inc[x] = wave_incl_scan(inc[x], lane);
   if (lane == 63) {
 #pragma unroll
     for (int x = 0; x < kXcds; ++x) wsum[wv * kXcds + x] = inc[x];
@@ -565,13 +549,8 @@ __global__ __launch_bounds__(kST) void k_stage(
   lds_barrier();
   if (tid < 64) {  // k-blocks per group, exclusive scan over the groups (one wavefront)
     const int n = tid < G ? (min(max(gs[tid + 1] - gs[tid], 0), 64) + 15) >> 4 : 0;  // <= 4
-    int incl = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (tid >= off) incl += t;
-    }
-    const int run = __shfl(incl, 63, 64);
+    const int incl = wave_incl_scan(n, tid);
+    const int run = __builtin_amdgcn_readlane(incl, 63);
     // zero k-blocks (pad rows, A = 0) extend the last group to a multiple of kPD, so the
     // GEMM loop runs whole rounds of its prefetch ring
     const int padded = (run + kPD - 1) / kPD * kPD;
