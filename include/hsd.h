@@ -81,6 +81,28 @@ int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel, const
                            int32_t* dev_status, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* ------------------------------------------------------------------ MoE front end
+ * Replaces the MoE block's front end after the router, hsd/model.py:110-121: the routed
+ * experts' up projection `gather_qmm(xn, fc1.weight, fc1.scales, fc1.biases,
+ * rhs_indices=inds, transpose=True)`, the shared expert's `up_proj(xn)` and `relu2` =
+ * square(relu(.)) (model.py:49-50), written in pack's hcat layout (model.py:123-129). The
+ * router (`mix.gate`) is not part of it.
+ *   x    [B, D] bf16 (the normed token), sel [B, topk] int32 expert ids
+ *   w1 [E, F, D/8] u32, s1/b1 [E, F, D/64] bf16 (stock layout, rows = outputs);
+ *   sw1 [FS, D/8], ss1/sb1 [FS, D/64] (the shared expert)
+ *   hcat [B, topk*F + FS] bf16: square(relu(bf16(x W^T))) rounded to bf16, W = s q + b
+ *   live_masks (nullable, [B, (topk*F + FS)/64] uint64): the canonical live masks of hcat
+ *   (bit j of entry g: element 64g + j is nonzero; NaN live)
+ *   dev_status (nullable int32): ORed with HSD_STATUS_BAD_EXPERT for an id outside
+ *   [0, E); that slot's h is 0.
+ * Requirements: D % 64 == 0, D <= 4096, F % 64 == 0, FS % 64 == 0, 16-byte aligned x, w1
+ * and sw1. No workspace. */
+int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, const uint32_t* w1,
+                     const uint16_t* s1, const uint16_t* b1, const uint32_t* sw1,
+                     const uint16_t* ss1, const uint16_t* sb1, void* hcat, int64_t B, int64_t D,
+                     int64_t F, int64_t FS, int64_t topk, int64_t E, uint64_t* live_masks,
+                     int32_t* dev_status, void* stream);
+
 /* The dense 4-bit down projection on the STOCK layout -- the comparator that
  * mlx-lm's gather_qmm + quantized_matmul compute in dense mode (model.py:132-133;
  * test_layout_decode.py:145-151). w [E, D, F/8], s/b [E, D, F/64]; sw [D, FS/8],

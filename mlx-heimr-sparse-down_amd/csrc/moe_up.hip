@@ -1,0 +1,196 @@
+// The MoE front end after the router (hsd/model.py:110-121) in pack's layout
+// (model.py:123-129): for token b the 4-bit up projection of each selected expert and of
+// the shared expert, ReLU^2, written to hcat [B, topk*F + FS] (bf16), plus the canonical
+// live mask of every 64-row group (the decode kernels' compaction input).
+//
+// k_moe_up: one workgroup per (token, 64-row group of hcat): 16 wavefronts x 4 rows.
+//   1. one round trip: the token's x (to LDS), the group's expert id (a scalar load), and
+//      for each of the wave's 4 rows the lane's 16-byte pieces (lane l: pieces l and
+//      l + 64 of the row's D/32) with their groups' scale and bias;
+//   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
+//      and the sum of x over every 32-input piece;
+//   3. per piece: a shift, a mask and an OR with bf16 1.0 put each nibble in the top four
+//      mantissa bits of a bf16, so a word becomes four bf16 pairs (1 + q_n/16,
+//      1 + q_{n+4}/16) (exact); v_dot2_f32_bf16 accumulates x (1 + q/16) in fp32, and
+//      u += 16 s * acc + (b - 16 s) * sum(x): the affine dequantisation W = s q + b folded
+//      per piece. (An offset of 1 against q/16 <= 15/16 keeps the cancellation in
+//      acc - sum(x) small: 128 + q, exact as well, lost about four more bits.)
+//   4. the 64 lanes' partials of each row: DPP sums inside 16-lane rows, then the four
+//      rows' totals in a fixed order; h = square(relu(bf16(u))) rounded to bf16.
+// Bytes per token: every row of the 7 selected matrices (D/2 + 4 D/64 bytes per row),
+// 22.45 MB at the reference shape: an HBM-bound batched GEMV.
+#include "hsd_common.h"
+
+namespace hsd {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kUpThreads = 1024;  // 16 wavefronts
+constexpr int kUpRows = 4;        // rows per wavefront: 64 rows (one mask group) per workgroup
+constexpr int kUpMaxD = 4096;     // inputs per token held in LDS
+constexpr int kUpMaxP = kUpMaxD / 32;
+constexpr uint32_t kBfOne2 = 0x3F803F80u;   // bf16 1.0 in both halves
+constexpr uint32_t kNibHi = 0x00780078u;    // mantissa bits 3..6 of both halves
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+__global__ __launch_bounds__(kUpThreads) void k_moe_up(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ sel, const uint32_t* __restrict__ w1,
+    const uint16_t* __restrict__ s1, const uint16_t* __restrict__ b1, const uint32_t* __restrict__ sw1,
+    const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
+    uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
+    int E) {
+  // x pairs: piece j, word m, pair n at xp[(4 j + m) 4 + n] = (x[32 j + 8 m + n], x[.. + 4])
+  __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
+  __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
+  __shared__ int nib[kUpThreads / 64];
+  const int b = blockIdx.y, grp = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
+  const int r0 = 64 * grp;
+  const bool routed = r0 < topk * F;
+  const int k = routed ? r0 / F : topk;
+  const int f0 = routed ? r0 - k * F : r0 - topk * F;
+
+  // ---- round trip: x, the expert id, the rows' pieces and their scales (no load under a
+  // branch: indices past the end are clamped and the values dropped)
+  const int e = routed ? sel[b * topk + k] : 0;
+  const uint4 xv = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid, NW - 1)];
+  const bool ok = !routed || (unsigned)e < (unsigned)E;
+  const size_t row0 = routed ? (size_t)(ok ? e : 0) * F + f0 : (size_t)f0;
+  const uint32_t* wb = routed ? w1 : sw1;
+  const uint16_t* sb = routed ? s1 : ss1;
+  const uint16_t* bb = routed ? b1 : sb1;
+  const int j0 = min(lane, NP - 1), j1 = min(lane + 64, NP - 1);
+  uint4 q[kUpRows][2];
+  uint16_t sv[kUpRows][2], bv[kUpRows][2];
+#pragma unroll
+  for (int i = 0; i < kUpRows; ++i) {
+    const size_t row = row0 + kUpRows * wave + i;
+    const uint4* wr = reinterpret_cast<const uint4*>(wb + row * NW);
+    q[i][0] = wr[j0];
+    q[i][1] = wr[j1];
+    sv[i][0] = sb[row * NGD + j0 / 2];
+    sv[i][1] = sb[row * NGD + j1 / 2];
+    bv[i][0] = bb[row * NGD + j0 / 2];
+    bv[i][1] = bb[row * NGD + j1 / 2];
+  }
+
+  // ---- x pairs and piece sums into LDS: thread t holds inputs 8t .. 8t+7 (one word's)
+  if (tid < NW) {
+    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};  // bf16 pairs (x[8t+2c], x[8t+2c+1])
+    auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
+    uint4 pr;
+    pr.x = el(0) | (el(4) << 16);
+    pr.y = el(1) | (el(5) << 16);
+    pr.z = el(2) | (el(6) << 16);
+    pr.w = el(3) | (el(7) << 16);
+    *reinterpret_cast<uint4*>(&xp[4 * tid]) = pr;
+  }
+  float s8 = 0.0f;
+  {
+    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32((n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu);
+  }
+  s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
+  s8 += dpp_f32<0x4E>(s8);
+  if (tid < NW && (tid & 3) == 0) xh[tid >> 2] = s8;
+  lds_barrier();
+
+  // ---- per row: the lane's pieces, then the 64-lane sum
+  float u[kUpRows];
+#pragma unroll
+  for (int i = 0; i < kUpRows; ++i) {
+    float part = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = h ? j1 : j0;
+      const bool use = (h ? lane + 64 : lane) < NP;
+      const uint32_t qw[4] = {q[i][h].x, q[i][h].y, q[i][h].z, q[i][h].w};
+      float acc = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[(4 * j + m) * 4]);
+        const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
+        // nibble n (bits 4n..4n+3 of each half) to bits 3..6: a left shift by 3 for n = 0,
+        // right shifts by 1, 5, 9 for the others
+        const uint32_t w0 = qw[m] << 3, w1 = qw[m] >> 1, w2 = qw[m] >> 5, w3 = qw[m] >> 9;
+        acc = dot2_bf16(xw[0], (w0 & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xw[1], (w1 & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
+      }
+      const float sc = bf16_bits_to_f32(sv[i][h]), bi = bf16_bits_to_f32(bv[i][h]);
+      const float t = fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[j]);
+      part += use ? t : 0.0f;
+    }
+    // 16-lane sums (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then the four
+    // 16-lane totals in lane order
+    part += dpp_f32<0xB1>(part);
+    part += dpp_f32<0x4E>(part);
+    part += dpp_f32<0x141>(part);
+    part += dpp_f32<0x140>(part);
+    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
+    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16));
+    const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32));
+    const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48));
+    u[i] = ok ? ((t0 + t1) + t2) + t3 : 0.0f;
+  }
+
+  // ---- h = square(relu(bf16(u))) in bf16; lanes 0..3 write the wave's 4 rows
+  float ui = u[0];
+#pragma unroll
+  for (int i = 1; i < kUpRows; ++i) ui = lane == i ? u[i] : ui;
+  const float ub = bf16_bits_to_f32(f32_to_bf16_bits(ui));
+  const float r = ub != ub ? ub : fmaxf(ub, 0.0f);
+  const uint16_t hb = f32_to_bf16_bits(r * r);
+  if (lane < kUpRows) hcat[(size_t)b * NR + r0 + kUpRows * wave + lane] = hb;
+  const uint32_t lb = (uint32_t)(__ballot(lane < kUpRows && (hb & 0x7FFFu) != 0) & 0xFu);
+  if (lane == 0) nib[wave] = (int)lb;
+  if (live_out) {
+    lds_barrier();
+    if (tid == 0) {
+      uint64_t m = 0;
+#pragma unroll
+      for (int w = 0; w < kUpThreads / 64; ++w) m |= (uint64_t)nib[w] << (kUpRows * w);
+      live_out[(size_t)b * (NR / 64) + grp] = m;
+    }
+  }
+  if (!ok && tid == 0 && f0 == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+}
+
+}  // namespace
+}  // namespace hsd
+
+using namespace hsd;
+
+extern "C" int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, const uint32_t* w1,
+                                const uint16_t* s1, const uint16_t* b1, const uint32_t* sw1,
+                                const uint16_t* ss1, const uint16_t* sb1, void* hcat, int64_t B,
+                                int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
+                                uint64_t* live_masks, int32_t* dev_status, void* stream) {
+  const char* fn = "hsd_moe_up_relu2";
+  if (!x || !sel || !w1 || !s1 || !b1 || !sw1 || !ss1 || !sb1 || !hcat)
+    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (x_dtype != HSD_DT_BF16) return set_error(HSD_ERR_DTYPE, "%s: x must be bf16", fn);
+  if (B < 0 || topk <= 0 || E <= 0 || D <= 0 || D % 64 || D > kUpMaxD || F <= 0 || F % 64 || FS <= 0 ||
+      FS % 64)
+    return set_error(HSD_ERR_SHAPE, "%s: need D %% 64 == 0 and D <= %d, F %% 64 == 0, FS %% 64 == 0", fn,
+                     kUpMaxD);
+  if (B > 65535 || (topk * F + FS) / 64 > 0x7FFFFFFF || E * F * (D / 8) >= ((int64_t)1 << 40))
+    return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)w1 | (uintptr_t)sw1;
+  if (al & 15u) return set_error(HSD_ERR_ALIGN, "%s: x and the weights must be 16-byte aligned", fn);
+  if (B == 0) return HSD_OK;
+  const dim3 grid((unsigned)((topk * F + FS) / 64), (unsigned)B);
+  hipLaunchKernelGGL(k_moe_up, grid, dim3(kUpThreads), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F,
+                     (int)FS, (int)topk, (int)E);
+  return check_launch(fn);
+}

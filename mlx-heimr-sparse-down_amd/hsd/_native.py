@@ -43,6 +43,8 @@ _SIGS = {
                          + [_c_i64] * 6 + [_c_float] * 3 + [_vp, _c_size, _vp]),
     "hsd_mamba_select_row": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "hsd_greedy_accept": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
+    "hsd_moe_up_relu2": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+                         + [_c_i64] * 6 + [_vp, _vp, _vp]),
 }
 
 EXPORTS = tuple(_SIGS)

@@ -124,6 +124,32 @@ class MoEDown:
         return x + y.to(x.dtype)
 
 
+def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, status=None):
+    """The front end after the router (model.py:110-121) in pack's layout: x [B, D] bf16
+    (the normed token), inds [B, topk] -> hcat [B, topk*F + FS] bf16 = square(relu(x W^T))
+    of each selected expert's up projection (w1 [E, F, D/8] u32, s1/b1 [E, F, D/64] bf16,
+    the stock layout), then the shared expert's (sw1 [FS, D/8], ss1/sb1 [FS, D/64]).
+    live_masks: optional int64 tensor of B*(topk*F + FS)/64 entries that receives the
+    canonical live mask of every 64-group of hcat. status: optional int32 [1], ORed with 1
+    for an expert id outside [0, E) (that slot is then 0)."""
+    if x.dtype != torch.bfloat16:
+        raise N.HSDError("up_relu2 takes bf16 activations")
+    x = N.contig(x)
+    B, D = x.shape
+    E, F = w1.shape[0], w1.shape[1]
+    FS = sw1.shape[0]
+    NR = topk * F + FS
+    hcat = torch.empty((B, NR), dtype=torch.bfloat16, device=x.device)
+    if live_masks is not None and (live_masks.dtype != torch.int64 or not live_masks.is_contiguous()
+                                   or live_masks.numel() < B * (NR // 64)):
+        raise N.HSDError("live_masks must be a contiguous int64 tensor of B*(topk*F + FS)/64 entries")
+    N.call("hsd_moe_up_relu2", N.ptr(x), N.dtype_tag(x.dtype), N.ptr(N.contig(inds.to(torch.int32))),
+           N.ptr(N.as_words(N.contig(w1))), N.ptr(N.contig(s1)), N.ptr(N.contig(b1)),
+           N.ptr(N.as_words(N.contig(sw1))), N.ptr(N.contig(ss1)), N.ptr(N.contig(sb1)), N.ptr(hcat),
+           B, D, F, FS, topk, E, N.ptr(live_masks), N.ptr(status), N.stream(x.device))
+    return hcat
+
+
 def build_layouts(blocks, single_layout=True):
     """NemotronModel.set_mode("sparse") (model.py:233-247): every block's neuron-major
     layout, one layer at a time, so the permutation's transient stays one layer's size

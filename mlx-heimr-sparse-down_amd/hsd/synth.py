@@ -82,18 +82,38 @@ def moe_layer_np(seed, n_experts=E, d=D, f=F, fs=FS):
     return dict(w=w, s=s, b=b, sw=sw, ss=ss, sb=sb)
 
 
+def proj_torch(gen, device, lead, rows, cols):
+    """down_proj_np's distributions drawn on the device: w [*lead, rows, cols/8] (int32 bit
+    patterns), s / b [*lead, rows, cols/64] bf16."""
+    w = torch.randint(-2 ** 31, 2 ** 31, (*lead, rows, cols // 8), dtype=torch.int32,
+                      device=device, generator=gen)
+    s = (torch.rand((*lead, rows, cols // GS), device=device, generator=gen) * 0.015 + 0.005).to(torch.bfloat16)
+    b = (torch.randn((*lead, rows, cols // GS), device=device, generator=gen) * 0.01).to(torch.bfloat16)
+    return w, s, b
+
+
 def moe_layer_torch(gen, device, n_experts=E, d=D, f=F, fs=FS):
     """moe_layer_np's distributions drawn on the device (benchmark scale: 364.8 MB per
     layer). Words are int32 bit patterns."""
-    def proj(lead, rows, cols):
-        w = torch.randint(-2 ** 31, 2 ** 31, (*lead, rows, cols // 8), dtype=torch.int32,
-                          device=device, generator=gen)
-        s = (torch.rand((*lead, rows, cols // GS), device=device, generator=gen) * 0.015 + 0.005).to(torch.bfloat16)
-        b = (torch.randn((*lead, rows, cols // GS), device=device, generator=gen) * 0.01).to(torch.bfloat16)
-        return w, s, b
-    w, s, b = proj((n_experts,), d, f)
-    sw, ss, sb = proj((), d, fs)
+    w, s, b = proj_torch(gen, device, (n_experts,), d, f)
+    sw, ss, sb = proj_torch(gen, device, (), d, fs)
     return dict(w=w, s=s, b=b, sw=sw, ss=ss, sb=sb)
+
+
+def moe_up_np(seed, n_experts=E, d=D, f=F, fs=FS):
+    """The stock-layout up projections of one MoE layer (rows = outputs): routed (w1, s1,
+    b1) [E, F, ...] over D inputs, shared (sw1, ss1, sb1) [FS, ...]."""
+    rng = np.random.default_rng(seed)
+    w1, s1, b1 = down_proj_np(rng, (n_experts,), f, d)
+    sw1, ss1, sb1 = down_proj_np(rng, (), fs, d)
+    return dict(w1=w1, s1=s1, b1=b1, sw1=sw1, ss1=ss1, sb1=sb1)
+
+
+def moe_up_torch(gen, device, n_experts=E, d=D, f=F, fs=FS):
+    """moe_up_np's distributions drawn on the device (int32 words)."""
+    w1, s1, b1 = proj_torch(gen, device, (n_experts,), f, d)
+    sw1, ss1, sb1 = proj_torch(gen, device, (), fs, d)
+    return dict(w1=w1, s1=s1, b1=b1, sw1=sw1, ss1=ss1, sb1=sb1)
 
 
 def live_mask_np(rng, shape, zero_frac, hot=None):

@@ -94,6 +94,44 @@ def dequantize(w, s, b, dtype=np.float64):
     return sf * q + bf
 
 
+# ------------------------------------------------ MoE front end: up projection + ReLU^2
+def up_proj_f64(x, w, s, b):
+    """One stock-layout 4-bit projection applied to x (the `transpose=True` product of
+    mx.gather_qmm / mx.quantized_matmul, model.py:117-120): u[.., o] = sum_i W[o, i] x[i]
+    with W = s * q + b (layout.py:3-7). x float [.., I]; w [O, I/8] u32, s/b [O, I/64]
+    bf16 bits -> float64 [.., O]."""
+    W = dequantize(w, s, b)
+    return np.asarray(x, dtype=np.float64) @ W.T
+
+
+def relu2_bf16(u):
+    """model.py:49-50 `square(relu(x))` on a bf16 tensor: u rounded to bf16 (the product's
+    output dtype), relu, the square rounded to bf16. NaN stays NaN. -> bf16 bits."""
+    ub = bf16_to_f32(f32_to_bf16(np.asarray(u, dtype=np.float32))).astype(np.float64)
+    r = np.where(np.isnan(ub), ub, np.maximum(ub, 0.0))
+    return f32_to_bf16((r * r).astype(np.float32))
+
+
+def up_relu2(x_bits, sel, w1, s1, b1, sw1, ss1, sb1, *, F, FS, topk, E=None):
+    """The MoE front end after the router (model.py:110-121) followed by pack's layout
+    (model.py:123-129): for token b, routed slot k uses expert sel[b, k]'s up projection
+    (w1 [E, F, D/8], s1/b1 [E, F, D/64]) and the shared expert its own (sw1 [FS, D/8],
+    ss1/sb1 [FS, D/64]); h = relu2(x @ W^T) in bf16 (test_layout_decode.py:111-120).
+    -> hcat [B, topk*F + FS] bf16 bits. A routed id outside [0, E) gives a zero slot (hsd
+    indexes the weights with it unchecked)."""
+    x = bf16_to_f32(np.asarray(x_bits, dtype=np.uint16)).astype(np.float64)
+    B = x.shape[0]
+    E = w1.shape[0] if E is None else E
+    out = np.zeros((B, topk * F + FS), dtype=np.uint16)
+    for bi in range(B):
+        for k in range(topk):
+            e = int(sel[bi, k])
+            if 0 <= e < E:
+                out[bi, k * F:(k + 1) * F] = relu2_bf16(up_proj_f64(x[bi], w1[e], s1[e], b1[e]))
+        out[bi, topk * F:] = relu2_bf16(up_proj_f64(x[bi], sw1, ss1, sb1))
+    return out
+
+
 # -------------------------------------------------------------- a5 compaction
 def live_masks(hcat, F, FS, topk):
     """Canonical compaction of hsd/decode.py:84-101 (Appendix A.3 of the hot-path
@@ -368,6 +406,11 @@ def greedy_accept(draft, tgt):
 
 
 PINNING = {
+    "up_proj_f64": "brute force on tiny shapes (scalar loops over words and nibbles); the nibble order "
+                   "is unpack_nibbles', pinned with the layout",
+    "relu2_bf16": "special values (negative, -0, +0, NaN) and exact squares of bf16 values",
+    "up_relu2": "slot layout of pack (model.py:123-129) by construction from up_proj_f64 and relu2_bf16; "
+                "a bad id gives a zero slot",
     "nibble_transpose": "closed form on tiny shapes (scalar loop), self-inverse, hand-made known answer, "
                         "dequantisation invariance (test_layout_decode.py:70-83)",
     "to_neuron_major": "dequantisation invariance; scales/biases moved bit for bit",

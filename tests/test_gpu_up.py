@@ -1,0 +1,110 @@
+"""GPU parity of the MoE front end after the router (hsd/model.py:110-121, 49-50): the
+4-bit up projections of the selected and shared experts, ReLU^2, in pack's hcat layout
+(model.py:123-129), with the canonical live masks.
+
+Bars:
+* h within one bf16 ulp of the pre-activation of the float64 oracle: the kernel
+  accumulates in fp32 and rounds u to bf16 before squaring, so a u on a rounding boundary
+  can land one ulp away, which moves h = u^2 by at most 2^-5 relative; |h - ref| <=
+  2^-5 |ref| + 1e-4 (the absolute term covers the fp32 summation error of a u near 0);
+  at least 99 % of the elements are bit-identical, and zero / nonzero disagree on at most
+  1e-3 of them;
+* integer work bit-exact: the live masks equal those of the kernel's own h;
+* a routed id outside [0, E): status flag, that slot exactly 0, the others unchanged.
+"""
+import numpy as np
+import pytest
+import torch
+
+from hsd import decode, layout, synth as S
+from hsd.moe import up_relu2
+from oracle import hsd_oracle as O
+
+pytestmark = pytest.mark.gpu
+D, F, FS, K, E = 2688, 1856, 3712, 6, 128
+
+
+def inputs(seed, B, E=E, D=D):
+    rng = np.random.default_rng(seed)
+    x = O.f32_to_bf16((rng.standard_normal((B, D)) * 0.5).astype(np.float32))
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(B)]).astype(np.int32)
+    return x, sel
+
+
+def masks_of(h_bits):
+    live = (h_bits & 0x7FFF) != 0
+    w = 1 << np.arange(64, dtype=np.uint64)
+    return (live.reshape(live.shape[0], -1, 64).astype(np.uint64) * w).sum(-1, dtype=np.uint64).reshape(-1)
+
+
+def check(h, ref):
+    hf, rf = O.bf16_to_f32(h).astype(np.float64), O.bf16_to_f32(ref).astype(np.float64)
+    nz = (hf != 0) & (rf != 0)
+    assert np.mean(h == ref) >= 0.99
+    assert np.all(np.abs(hf - rf)[nz] <= 2 ** -5 * np.abs(rf[nz]) + 1e-4)
+    assert np.mean((hf == 0) != (rf == 0)) <= 1e-3
+
+
+@pytest.fixture(scope="module")
+def up(dev):
+    lay = S.moe_up_np(5)
+    return lay, {k: S.to_device(v, dev) for k, v in lay.items()}
+
+
+def test_up_relu2_matches_oracle(up, dev):
+    lay, dv = up
+    x, sel = inputs(6, 2)
+    masks = torch.zeros(2 * (K * F + FS) // 64, dtype=torch.int64, device=dev)
+    h = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"],
+                 dv["sb1"], topk=K, live_masks=masks)
+    hb = h.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=F, FS=FS, topk=K)
+    check(hb, ref)
+    assert np.array_equal(masks.cpu().numpy().view(np.uint64), masks_of(hb))
+
+
+def test_bad_expert_id(up, dev):
+    lay, dv = up
+    x, sel = inputs(7, 1)
+    bad = sel.copy()
+    bad[0, 3] = E + 9
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    args = (dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"], dv["sb1"])
+    h = up_relu2(S.to_device(x, dev), S.to_device(bad, dev), *args, topk=K, status=status)
+    h0 = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), *args, topk=K)
+    assert int(status.item()) == 1
+    assert torch.all(h[0, 3 * F:4 * F].view(torch.int16) == 0)
+    keep = torch.ones(K * F + FS, dtype=torch.bool, device=dev)
+    keep[3 * F:4 * F] = False
+    assert torch.equal(h[0, keep].view(torch.int16), h0[0, keep].view(torch.int16))
+
+
+def test_small_shape(dev):
+    """D=256 (8 pieces per row: most lanes idle), F=128, FS=192, 4 experts, top-2."""
+    d, f, fs, e, k = 256, 128, 192, 4, 2
+    lay = S.moe_up_np(8, n_experts=e, d=d, f=f, fs=fs)
+    dv = {n: S.to_device(v, dev) for n, v in lay.items()}
+    rng = np.random.default_rng(9)
+    x = O.f32_to_bf16((rng.standard_normal((3, d)) * 0.5).astype(np.float32))
+    sel = np.stack([rng.permutation(e)[:k] for _ in range(3)]).astype(np.int32)
+    h = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"],
+                 dv["sb1"], topk=k)
+    ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=f, FS=fs, topk=k)
+    check(h.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+def test_front_end_feeds_the_down_projection(up, dev):
+    """hcat from the front end goes straight into the sparse down projection; its live
+    masks are the ones the down kernel derives from the same hcat."""
+    lay, dv = up
+    x, sel = inputs(10, 1)
+    m_up = torch.zeros((K * F + FS) // 64, dtype=torch.int64, device=dev)
+    h = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"],
+                 dv["sb1"], topk=K, live_masks=m_up)
+    down = S.moe_layer_np(11)
+    dd = {k2: S.to_device(v, dev) for k2, v in down.items()}
+    nm = layout.to_neuron_major(dd["w"], dd["s"], dd["b"]) + layout.to_neuron_major(dd["sw"], dd["ss"], dd["sb"])
+    gains = torch.cat([torch.rand((1, K), device=dev), torch.ones((1, 1), device=dev)], dim=1)
+    m_dn = torch.zeros_like(m_up)
+    decode.sparse_down(h, S.to_device(sel, dev), gains, *nm, F=F, FS=FS, D=D, topk=K, live_masks=m_dn)
+    assert torch.equal(m_up, m_dn)
