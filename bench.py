@@ -12,6 +12,9 @@ timed region; inputs are resident in HBM.
 Other workloads, each printing one JSON line of its own:
   --workload prefill   2048-token prompt in chunks of 512, Zipf(1.1) routing, 23 layers
   --workload mtp       MTP-2 verify (3 rows) + rollback over 23 Mamba-2 layers
+  --workload up        the MoE front end after the router: 4-bit up projections of the 6
+                       selected and the shared expert + ReLU^2 into hcat, 23 layers,
+                       batch 1; also the front end followed by the sparse down projection
 """
 from __future__ import annotations
 
@@ -28,7 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-heimr-sparse-down_amd"))
 import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
-from hsd import decode, layout, mamba as M, mtp, prefill, synth as S  # noqa: E402
+from hsd import decode, layout, mamba as M, moe, mtp, prefill, synth as S  # noqa: E402
 from hsd import _native as N  # noqa: E402
 
 METRIC = "batch-1 decode tok/s (sparse+MTP2); sparse-down HBM GB/s vs peak"
@@ -423,12 +426,66 @@ def bench_mtp(args):
                               bytes_per_layer_step=per_layer))
 
 
+# ------------------------------------------------------------------ MoE front end
+def bench_up(args):
+    dev = torch.device("cuda:0")
+    nl = args.layers
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 7)
+    ups = [S.moe_up_torch(gen, dev) for _ in range(nl)]
+    downs, _, _ = make_layers(dev, args.seed, keep_stock=False)
+    ntok = args.ntok
+    x = (torch.randn((ntok, nl, D), device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    sel = torch.stack([torch.stack([torch.randperm(E, device=dev, generator=gen)[:K] for _ in range(nl)])
+                       for _ in range(ntok)]).to(torch.int32)
+    gains = torch.cat([torch.rand((ntok, nl, K), device=dev, generator=gen),
+                       torch.ones((ntok, nl, 1), device=dev)], dim=-1).float()
+    hbuf = [None] * nl
+    ws = [torch.empty(N.lib().hsd_sparse_down_workspace_bytes(1, D, F, FS, K), dtype=torch.uint8, device=dev)
+          for _ in range(nl)]
+
+    def up_layer(t, l):
+        u = ups[l]
+        hbuf[l] = moe.up_relu2(x[t, l:l + 1], sel[t, l:l + 1], u["w1"], u["s1"], u["b1"], u["sw1"], u["ss1"],
+                               u["sb1"], topk=K)
+
+    def chain_layer(t, l):
+        up_layer(t, l)
+        decode.sparse_down(hbuf[l], sel[t, l:l + 1], gains[t, l:l + 1], *downs[l]["nm"], F=F, FS=FS, D=D, topk=K,
+                           workspace=ws[l])
+
+    graphs = capture_steps(up_layer, ntok) if nl == NL else None
+    if graphs is None:
+        raise SystemExit("--workload up times all 23 layers")
+    ms = time_graphs(graphs, args.steps, args.warmup)
+    per_call = NR * (D // 2 + 4 * (D // 64)) + D * 2 + NR * 2 + K * 4
+    gbs = per_call * nl * args.steps / (ms * 1e-3) / 1e9
+    del graphs
+    cgraphs = capture_steps(chain_layer, ntok)
+    cms = time_graphs(cgraphs, args.steps, args.warmup)
+    log(f"[up] front end (up projections + ReLU^2), 23 layers: {1e3 * ms / args.steps:.1f} us/token, "
+        f"{gbs:.0f} GB/s over {per_call / 1e6:.2f} MB/layer")
+    log(f"[up] front end + sparse down, 23 layers: {1e3 * cms / args.steps:.1f} us/token")
+    return dict(metric="MoE front end (4-bit up projections + ReLU^2), batch 1, 23 layers: HBM GB/s",
+                value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+                ms_per_step=round(ms / args.steps, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
+                dtype="bf16 x, 4-bit weights, f32 accumulate (bf16 dot2)", data="synthetic",
+                config=dict(workload="MoE front end after the router: 6 routed + shared up projections, ReLU^2, "
+                                     "batch 1, 23 layers", experts=E, topk=K, D=D, F=F, FS=FS,
+                            tokens_rotated=ntok),
+                roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                              frac=round(gbs / HBM_PEAK_GBS, 4), traffic=pmc_traffic("up"),
+                              kernel="k_moe_up", bytes_per_launch=per_call,
+                              us_per_launch=round(1e3 * ms / args.steps / nl, 3)),
+                front_plus_down_us_per_token=round(1e3 * cms / args.steps, 2))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "mtp"))
+    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "mtp", "up"))
     ap.add_argument("--zero-frac", type=float, default=0.9)
     ap.add_argument("--hot", action="store_true", help="hot-neuron activation variant")
     ap.add_argument("--ntok", type=int, default=32, help="distinct tokens rotated (one graph each)")
@@ -446,7 +503,7 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    fn = dict(decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp)[args.workload]
+    fn = dict(decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp, up=bench_up)[args.workload]
     rec = fn(args)
     rec["device"] = torch.cuda.get_device_name(0)
     rec["torch"] = torch.__version__

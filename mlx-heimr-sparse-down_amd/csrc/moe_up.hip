@@ -4,9 +4,10 @@
 // live mask of every 64-row group (the decode kernels' compaction input).
 //
 // k_moe_up: one workgroup per (token, 64-row group of hcat): 16 wavefronts x 4 rows.
-//   1. one round trip: the token's x (to LDS), the group's expert id (a scalar load), and
-//      for each of the wave's 4 rows the lane's 16-byte pieces (lane l: pieces l and
-//      l + 64 of the row's D/32) with their groups' scale and bias;
+//   1. one round trip: the token's x, the group's expert id (a scalar load), the 64 rows'
+//      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
+//      share of its 4 rows' 16-byte pieces (4 D/32 pieces dealt over the 64 lanes in
+//      turn, so every lane has the same count but the last round);
 //   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
 //      and the sum of x over every 32-input piece;
 //   3. per piece: a shift, a mask and an OR with bf16 1.0 put each nibble in the top four
@@ -48,6 +49,8 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
   __shared__ int nib[kUpThreads / 64];
+  __shared__ __attribute__((aligned(16))) uint16_t sl[64 * (kUpMaxD / 64)];  // [row][group]
+  __shared__ __attribute__((aligned(16))) uint16_t bl[64 * (kUpMaxD / 64)];
   const int b = blockIdx.y, grp = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
@@ -65,19 +68,23 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   const uint32_t* wb = routed ? w1 : sw1;
   const uint16_t* sb = routed ? s1 : ss1;
   const uint16_t* bb = routed ? b1 : sb1;
-  const int j0 = min(lane, NP - 1), j1 = min(lane + 64, NP - 1);
-  uint4 q[kUpRows][2];
-  uint16_t sv[kUpRows][2], bv[kUpRows][2];
+  // the 64 rows' scales and biases: 64 NGD bf16 each, contiguous and 16-byte aligned (64
+  // rows x 2 NGD bytes); threads [0, 8 NGD) load s, [8 NGD, 16 NGD) load b
+  const int nsc = 8 * NGD;
+  const int sc_i = tid < nsc ? tid : min(tid - nsc, nsc - 1);
+  const uint4 scv = reinterpret_cast<const uint4*>((tid < nsc ? sb : bb) + row0 * NGD)[sc_i];
+  // pieces: index p = lane + 64 it over the wave's 4 rows x NP pieces
+  constexpr int kIt = (kUpRows * kUpMaxP + 63) / 64;
+  const int npw = kUpRows * NP, nit = (npw + 63) / 64;
+  uint4 q[kIt];
+  int prow[kIt], pj[kIt];
 #pragma unroll
-  for (int i = 0; i < kUpRows; ++i) {
-    const size_t row = row0 + kUpRows * wave + i;
-    const uint4* wr = reinterpret_cast<const uint4*>(wb + row * NW);
-    q[i][0] = wr[j0];
-    q[i][1] = wr[j1];
-    sv[i][0] = sb[row * NGD + j0 / 2];
-    sv[i][1] = sb[row * NGD + j1 / 2];
-    bv[i][0] = bb[row * NGD + j0 / 2];
-    bv[i][1] = bb[row * NGD + j1 / 2];
+  for (int it = 0; it < kIt; ++it) {
+    const int p = min(lane + 64 * it, npw - 1);
+    prow[it] = p / NP;
+    pj[it] = p - prow[it] * NP;
+    const uint4* wr = reinterpret_cast<const uint4*>(wb + (row0 + kUpRows * wave + prow[it]) * NW);
+    q[it] = wr[pj[it]];  // rounds past nit re-read the last piece, unused
   }
 
   // ---- x pairs and piece sums into LDS: thread t holds inputs 8t .. 8t+7 (one word's)
@@ -100,18 +107,19 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
   s8 += dpp_f32<0x4E>(s8);
   if (tid < NW && (tid & 3) == 0) xh[tid >> 2] = s8;
+  if (tid < 2 * nsc) *reinterpret_cast<uint4*>((tid < nsc ? sl : bl) + 8 * sc_i) = scv;
   lds_barrier();
 
-  // ---- per row: the lane's pieces, then the 64-lane sum
-  float u[kUpRows];
+  // ---- the lane's pieces into its 4 row partials, then per row the 64-lane sum
+  float pr[kUpRows];
 #pragma unroll
-  for (int i = 0; i < kUpRows; ++i) {
-    float part = 0.0f;
+  for (int i = 0; i < kUpRows; ++i) pr[i] = 0.0f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = h ? j1 : j0;
-      const bool use = (h ? lane + 64 : lane) < NP;
-      const uint32_t qw[4] = {q[i][h].x, q[i][h].y, q[i][h].z, q[i][h].w};
+  for (int it = 0; it < kIt; ++it) {
+    if (it < nit) {  // uniform
+      const int j = pj[it], rl = kUpRows * wave + prow[it];  // piece, row within the 64
+      const bool use = lane + 64 * it < npw;
+      const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
       float acc = 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -125,10 +133,16 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
         acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
         acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
       }
-      const float sc = bf16_bits_to_f32(sv[i][h]), bi = bf16_bits_to_f32(bv[i][h]);
-      const float t = fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[j]);
-      part += use ? t : 0.0f;
+      const float sc = bf16_bits_to_f32(sl[rl * NGD + j / 2]), bi = bf16_bits_to_f32(bl[rl * NGD + j / 2]);
+      const float t = use ? fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[j]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < kUpRows; ++i) pr[i] += prow[it] == i ? t : 0.0f;
     }
+  }
+  float u[kUpRows];
+#pragma unroll
+  for (int i = 0; i < kUpRows; ++i) {
+    float part = pr[i];
     // 16-lane sums (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then the four
     // 16-lane totals in lane order
     part += dpp_f32<0xB1>(part);
