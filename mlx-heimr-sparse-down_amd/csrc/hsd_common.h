@@ -88,7 +88,11 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+// silu(x) = x / (1 + e^-x), with the hardware exponential and reciprocal (a few ulp;
+// the IEEE division and the libm exponential are long dependent sequences).
+__device__ __forceinline__ float silu_f32(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 // softplus(x) = log(1 + e^x); above 20 it equals x in fp32.
 __device__ __forceinline__ float softplus_f32(float x) {
