@@ -53,14 +53,17 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   // with every input that does not depend on it, then the state rows and conv windows.
   // Rows past L re-read row L - 1 and are unused.
   const int cur = *cur_ptr;
-  // conv channels: thread t owns channel t of [16 x | 128 B | 128 C] and, for t < 16, also
-  // channel 256 + t; the others repeat channel t for the second and drop it
+  // conv channels: thread t owns channel t of [16 x | 128 B | 128 C]; the last NCH - kMT
+  // threads (wave 3) also own channels kMT .. NCH - 1, and wave 1 computes dt and dA, so
+  // no wave carries both extras; the others repeat channel t for the second and drop it
   constexpr int NCH = kPB + 2 * kN;
   auto chan = [&](int t) {
     return t < kPB ? hh * P + pblk * kPB + t
                    : (t < kPB + kN ? DI + g * kN + (t - kPB) : DI + GN + g * kN + (t - kPB - kN));
   };
-  const int t1 = tid, t2 = tid + kMT < NCH ? tid + kMT : tid;
+  constexpr int kExtra = NCH - kMT;  // channels past one per thread
+  static_assert(kExtra > 0 && kExtra <= 64 && kMT >= 128, "the extra channels fit the last wave");
+  const int t1 = tid, t2 = tid >= kMT - kExtra ? tid + kExtra : tid;
   const int ch1 = chan(t1), ch2 = chan(t2);
   uint16_t in1[kLMax], in2[kLMax];
 #pragma unroll
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     w2[j] = conv_w[(size_t)ch2 * kK + j];
   }
   const uint16_t b1 = conv_b[ch1], b2 = conv_b[ch2];
-  const int rd = min(tid, L - 1);
+  const int rd = min(max(tid - 64, 0), L - 1);  // wave 1's first L lanes: dt and dA
   const uint16_t dtr = dt_raw[(size_t)rd * dt_ld + hh];
   const float Alog = A_log[hh], dtb = dt_bias[hh], Dh = Dp[hh];
   if ((unsigned)cur >= (unsigned)nslab) return;  // a corrupt ring index: touch nothing
@@ -134,13 +137,13 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     }
   };
   conv(t1, ch1, s1, in1, w1, b1);
-  if (tid + kMT < NCH) conv(t2, ch2, s2, in2, w2, b2);
-  if (tid < L) {
+  if (t2 != t1) conv(t2, ch2, s2, in2, w2, b2);
+  if (tid >= 64 && tid < 64 + L) {
     const float A = -expf(Alog);
     const float v = softplus_f32(bf16_bits_to_f32(dtr) + dtb);
     const float d = fminf(fmaxf(v, dt_lo), dt_hi);
-    dtv[tid] = d;
-    dA[tid] = expf(A * d);
+    dtv[tid - 64] = d;
+    dA[tid - 64] = expf(A * d);
   }
   lds_barrier();
 
