@@ -113,6 +113,21 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
 }
 
+// Sum over the 64 lanes of a wavefront without LDS, the same in every lane: DPP sums
+// inside each 16-lane row (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then the
+// four row sums in a fixed order. Needs every lane active.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
 // Deterministic butterfly sum over the 64 lanes of a wavefront (same tree on every
 // call, so equal inputs give equal bits).
 __device__ __forceinline__ float wave_sum(float v) {

@@ -189,7 +189,9 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
 
 // out[r, i] = norm_w[i] * z_i / sqrt(mean_group(z^2) + eps), z = y_pre * silu(gate);
 // one workgroup per (row, norm group).
-template <int YDT>
+// PER > 0: NG = PER kMT at compile time (no slice past the group is loaded); PER == 0:
+// any NG <= 8 kMT.
+template <int YDT, int PER>
 __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_pre,
                                                     const uint16_t* __restrict__ gate,
                                                     int64_t gate_ld,
@@ -199,8 +201,8 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   __shared__ float wsum[kMT / 64];
   const int ngrp = DI / NG;
   const int r = blockIdx.x / ngrp, gi = blockIdx.x - (blockIdx.x / ngrp) * ngrp;
-  const int per = NG / kMT;
-  constexpr int kPerMax = 8;       // NG <= 8 kMT (checked by the host)
+  const int per = PER > 0 ? PER : NG / kMT;
+  constexpr int kPerMax = PER > 0 ? PER : 8;  // NG <= 8 kMT (checked by the host)
   // every load (activations, gate, weight) in one round trip: slices past per re-read
   // the last one and are dropped (no load under a branch)
   float yv[kPerMax], gv[kPerMax], nw[kPerMax];
@@ -218,12 +220,13 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
     z[i] = i < per ? yv[i] * silu_f32(gv[i]) : 0.0f;
     ss = fmaf(z[i], z[i], ss);
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
-  __syncthreads();
+  lds_barrier();
   float tot = wsum[0];
+#pragma unroll
   for (int w = 1; w < kMT / 64; ++w) tot += wsum[w];
-  const float inv = 1.0f / sqrtf(tot / (float)NG + eps);
+  const float inv = __builtin_amdgcn_rsqf(tot / (float)NG + eps);
 #pragma unroll
   for (int i = 0; i < kPerMax; ++i) {
     if (i >= per) break;
@@ -342,10 +345,17 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
   int rc = check_launch(fn);
   if (rc) return rc;
   const unsigned ngrid = (unsigned)(L * (DI / norm_group));
-#define HSD_NORM(DT)                                                                        \
-  hipLaunchKernelGGL(k_gated_norm<DT>, dim3(ngrid), dim3(kMT), 0, st, y_pre, gate, gate_ld, \
-                     norm_w, reinterpret_cast<typename Elem<DT>::T*>(y), (int)DI,           \
+#define HSD_NORM_P(DT, PER)                                                                   \
+  hipLaunchKernelGGL((k_gated_norm<DT, PER>), dim3(ngrid), dim3(kMT), 0, st, y_pre, gate, gate_ld, \
+                     norm_w, reinterpret_cast<typename Elem<DT>::T*>(y), (int)DI,               \
                      (int)norm_group, eps)
+#define HSD_NORM(DT)                                          \
+  switch (norm_group / kMT) {                                 \
+    case 1: HSD_NORM_P(DT, 1); break;                         \
+    case 2: HSD_NORM_P(DT, 2); break;                         \
+    case 4: HSD_NORM_P(DT, 4); break;                         \
+    default: HSD_NORM_P(DT, 0); break;                        \
+  }
   switch (y_dtype) {
     case HSD_DT_BF16: HSD_NORM(HSD_DT_BF16); break;
     case HSD_DT_F16: HSD_NORM(HSD_DT_F16); break;
@@ -353,6 +363,7 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
     default: return set_error(HSD_ERR_DTYPE, "%s: y_dtype %d", fn, y_dtype);
   }
 #undef HSD_NORM
+#undef HSD_NORM_P
   return check_launch(fn);
 }
 
