@@ -162,10 +162,10 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
   float hsum = 0.0f;
   const int nmine = cnt;                              // this team's rows
-  int nmax = nmine;                                   // most rows of any team of the wave
-  nmax = max(nmax, __shfl_xor(nmax, 16, 64));
-  nmax = max(nmax, __shfl_xor(nmax, 32, 64));
-  nmax = __builtin_amdgcn_readfirstlane(nmax);
+  // most rows of any team of the wave: a team is one 16-lane row, so lanes 0, 16, 32
+  // and 48 hold the four counts (scalar reads, no LDS permute in front of the row loads)
+  const int nmax = max(max(__builtin_amdgcn_readlane(nmine, 0), __builtin_amdgcn_readlane(nmine, 16)),
+                       max(__builtin_amdgcn_readlane(nmine, 32), __builtin_amdgcn_readlane(nmine, 48)));
   for (int r0 = 0; r0 < nmax; r0 += kRB) {            // one batch unless > 16 live rows
     int idx[kRB];
 #pragma unroll
