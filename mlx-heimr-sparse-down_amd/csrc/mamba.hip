@@ -42,7 +42,11 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   __shared__ __attribute__((aligned(16))) float Cs[kLMax][kN];
   __shared__ float dtv[kLMax], dA[kLMax];
   const int npb = P / kPB;
-  const int hh = blockIdx.x / npb, pblk = blockIdx.x - (blockIdx.x / npb) * npb;
+  // xcd_remap: consecutive heads (a B/C group's, and a norm group's) run on one XCD, so
+  // their shared B/C conv inputs and their y rows stay in that XCD's L2; k_gated_norm's
+  // workgroup for norm group g runs on XCD g % 8 as well
+  const int lb = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int hh = lb / npb, pblk = lb - (lb / npb) * npb;
   const int tid = threadIdx.x;
   const int DI = H * P, GN = G * kN, CD = DI + 2 * GN;
   const int hpg = H / G;
