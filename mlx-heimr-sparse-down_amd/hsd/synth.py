@@ -116,6 +116,61 @@ def moe_up_torch(gen, device, n_experts=E, d=D, f=F, fs=FS):
     return dict(w1=w1, s1=s1, b1=b1, sw1=sw1, ss1=ss1, sb1=sb1)
 
 
+def write_checkpoint(model_dir, seed, *, pattern="MEME", n_experts=E, d=D, f=F, fs=FS, topk=TOPK,
+                     shards=2):
+    """A synthetic MLX-format checkpoint of random 4-bit MoE layers: config.json, the
+    shard files and model.safetensors.index.json (shards > 1) or one model.safetensors,
+    with the names hsd.checkpoint reads. Layers marked "E" in `pattern` get a MoE layer
+    (moe_layer_np + moe_up_np, seeds seed + 2l and seed + 2l + 1); other layers get one
+    small placeholder tensor each. Returns {layer: {"down": moe_layer_np dict, "up":
+    moe_up_np dict}} (host arrays, bf16 as uint16 bits)."""
+    import json
+    import os
+    from safetensors.torch import save_file
+
+    def tens(a):
+        a = np.ascontiguousarray(a)
+        if a.dtype == np.uint16:
+            return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+        return torch.from_numpy(a)
+
+    os.makedirs(model_dir, exist_ok=True)
+    tensors, arrays = {}, {}
+    for l, kind in enumerate(pattern):
+        p = f"backbone.layers.{l}.mixer"
+        if kind != "E":
+            tensors[f"{p}.placeholder"] = torch.zeros(4, dtype=torch.float32)
+            continue
+        dn = moe_layer_np(seed + 2 * l, n_experts, d, f, fs)
+        up = moe_up_np(seed + 2 * l + 1, n_experts, d, f, fs)
+        arrays[l] = dict(down=dn, up=up)
+        for k, (wk, sk, bk), src in (("switch_mlp.fc1", ("w1", "s1", "b1"), up),
+                                     ("switch_mlp.fc2", ("w", "s", "b"), dn),
+                                     ("shared_experts.up_proj", ("sw1", "ss1", "sb1"), up),
+                                     ("shared_experts.down_proj", ("sw", "ss", "sb"), dn)):
+            tensors[f"{p}.{k}.weight"] = tens(src[wk])
+            tensors[f"{p}.{k}.scales"] = tens(src[sk])
+            tensors[f"{p}.{k}.biases"] = tens(src[bk])
+    names = sorted(tensors)
+    if shards <= 1:
+        save_file(tensors, os.path.join(model_dir, "model.safetensors"), metadata={"format": "mlx"})
+    else:
+        wmap = {}
+        for i in range(shards):
+            fn = f"model-{i + 1:05d}-of-{shards:05d}.safetensors"
+            part = {n: tensors[n] for n in names[i::shards]}
+            save_file(part, os.path.join(model_dir, fn), metadata={"format": "mlx"})
+            wmap.update({n: fn for n in part})
+        with open(os.path.join(model_dir, "model.safetensors.index.json"), "w") as fh:
+            json.dump({"metadata": {}, "weight_map": wmap}, fh)
+    cfg = dict(hidden_size=d, moe_intermediate_size=f, moe_shared_expert_intermediate_size=fs,
+               n_routed_experts=n_experts, num_experts_per_tok=topk, hybrid_override_pattern=pattern,
+               quantization=dict(group_size=GS, bits=4))
+    with open(os.path.join(model_dir, "config.json"), "w") as fh:
+        json.dump(cfg, fh)
+    return arrays
+
+
 def live_mask_np(rng, shape, zero_frac, hot=None):
     """Bernoulli(1 - zero_frac) live mask; `hot` = (hot_mask [.., width], p_hot, p_cold)
     gives per-neuron rates instead."""
