@@ -6,8 +6,8 @@
 // the arithmetic, then a fixed-order sum (the reference's partial + reduce structure,
 // decode.py:37-144). At the BASELINE shape (D=2688, F=1856, FS=3712, top-6 of 128 +
 // shared) a token row has 232 64-neuron groups:
-//   * k_sparse_down_part: one workgroup = (128-output chunk c, part p of <=16 groups of
-//     one slot): 21 x 16 = 336 workgroups per row. 512 threads = 32 teams of 16 lanes;
+//   * k_sparse_down_part: one workgroup = (128-output chunk c, part p of <=8 groups of
+//     one slot): 21 x 32 = 672 workgroups per row. 256 threads = 16 teams of 16 lanes;
 //     team (j, phase) owns the live rows n of group g0+j with n % 2 == phase; lane l owns
 //     weight word 16c+l (8 outputs, a 64-byte piece of every row per team).
 //       1. one round trip: the slot's expert id and gain, and the group's 64 activations
@@ -18,7 +18,9 @@
 //       3. acc[t] = sum h_i q_{i,t}, hsum = sum h_i (fp32); term = s*acc + b*hsum (the
 //          group factorisation of decode.py:125-128);
 //       4. terms summed in (group, phase) order, times the slot's gain -> part[b, p, chunk].
-//   * k_sum_parts: y[b, o] = sum over the 16 parts in part order.
+//   * k_sum_parts: y[b, o] = sum over the 32 parts in part order.
+// Eight groups per workgroup measured fastest: 16 (512 threads) and 32 (1024) were 4 % and
+// 6 % slower per call, 4 (128 threads, 63 parts) 6 % slower.
 // No atomics, no inter-workgroup signalling: results are bit-reproducible, and a row
 // of a B-row call is computed exactly as that row alone.
 #include "hsd_common.h"
@@ -27,10 +29,11 @@ namespace hsd {
 namespace {
 
 constexpr int kRS = 2;                   // row phases per group
-constexpr int kThreads = 256 * kRS;
+constexpr int kGPW = 8;                  // groups per workgroup
 constexpr int kWPC = 16;                 // weight words per D chunk (one lane each)
+constexpr int kThreads = kGPW * kWPC * kRS;
 constexpr int kDC = kWPC * 8;            // outputs per D chunk
-constexpr int kGPW = 16;                 // groups per workgroup
+constexpr int kL1 = kThreads / kDC;      // first-level sub-sums per output
 constexpr int kRB = 16;                  // rows per team per batch (a phase has 32 rows)
 
 struct Geom {
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   __shared__ HT hs[kGPW * kRS][kHP];                // per team: the group's activations
   __shared__ uint8_t lst[kGPW * kRS][64];           // per team: the group's live rows, ascending
   __shared__ float red[kGPW * kRS][kRedP];          // per team: group terms [t][word]
-  __shared__ float sum2[kDC][kRS * 2 + 1];
+  __shared__ float sum2[kDC][kL1 + 1];
 
   const int logical = xcd_remap((int)blockIdx.x, B * g.nwg);
   const int b = logical / g.nwg;
@@ -209,7 +212,6 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   // level 1: kThreads/kDC threads per output, each over a contiguous run of groups. A
   // thread takes word lw = o % 16 and nibble t = o / 16 (output 8 lw + t), so the lanes of
   // a wavefront read consecutive words of red.
-  constexpr int kL1 = kThreads / kDC;                 // 4 sub-sums per output
   constexpr int kGPS = kGPW / kL1;                    // groups per sub-sum
   {
     const int o = tid % kDC, s = tid / kDC;
@@ -436,8 +438,8 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
   const int n = (int)(B * D);
   const dim3 rgrid((unsigned)((n + 255) / 256));
 #define HSD_SUM(DT)                                                                                  \
-  if (g.nparts == 16)                                                                                \
-    hipLaunchKernelGGL((k_sum_parts<DT, 16>), rgrid, dim3(256), 0, st, part,                         \
+  if (g.nparts == 32)                                                                                \
+    hipLaunchKernelGGL((k_sum_parts<DT, 32>), rgrid, dim3(256), 0, st, part,                         \
                        reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n);            \
   else                                                                                               \
     hipLaunchKernelGGL((k_sum_parts<DT, 0>), rgrid, dim3(256), 0, st, part,                          \

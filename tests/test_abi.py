@@ -70,9 +70,10 @@ def test_argument_errors_are_reported():
 
 def test_workspace_sizes():
     lib = N.lib()
-    # 16 parts per token row x D fp32 partials
-    assert lib.hsd_sparse_down_workspace_bytes(1, 2688, 1856, 3712, 6) == 16 * 2688 * 4
-    assert lib.hsd_sparse_down_workspace_bytes(3, 2688, 1856, 3712, 6) == 3 * 16 * 2688 * 4
+    # 32 parts per token row (4 per routed slot of 29 groups, 8 for the shared expert's 58,
+    # 8 groups each) x D fp32 partials
+    assert lib.hsd_sparse_down_workspace_bytes(1, 2688, 1856, 3712, 6) == 32 * 2688 * 4
+    assert lib.hsd_sparse_down_workspace_bytes(3, 2688, 1856, 3712, 6) == 3 * 32 * 2688 * 4
     assert lib.hsd_prefill_num_tiles(512, 6, 128, 32) == 240
     assert lib.hsd_prefill_num_tiles(512, 6, 128, 64) == 184
     assert lib.hsd_prefill_num_tiles(2048, 6, 128, 32) == 576
