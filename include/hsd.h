@@ -95,8 +95,8 @@ int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel, const
  *   (bit j of entry g: element 64g + j is nonzero; NaN live)
  *   dev_status (nullable int32): ORed with HSD_STATUS_BAD_EXPERT for an id outside
  *   [0, E); that slot's h is 0.
- * Requirements: D % 64 == 0, D <= 4096, F % 64 == 0, FS % 64 == 0, 16-byte aligned x, w1
- * and sw1. No workspace. */
+ * Requirements: D % 64 == 0, D <= 4096, F % 64 == 0, FS % 64 == 0, 16-byte aligned x, w1,
+ * sw1 and the four scale/bias arrays. No workspace. */
 int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, const uint32_t* w1,
                      const uint16_t* s1, const uint16_t* b1, const uint32_t* sw1,
                      const uint16_t* ss1, const uint16_t* sb1, void* hcat, int64_t B, int64_t D,

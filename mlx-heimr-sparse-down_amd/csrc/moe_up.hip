@@ -3,8 +3,9 @@
 // the shared expert, ReLU^2, written to hcat [B, topk*F + FS] (bf16), plus the canonical
 // live mask of every 64-row group (the decode kernels' compaction input).
 //
-// k_moe_up: one workgroup per (token, 64-row group of hcat): 16 wavefronts x 4 rows.
-//   1. one round trip: the token's x, the group's expert id (a scalar load), the 64 rows'
+// k_moe_up: one workgroup per (token, 16-row block of hcat): 4 wavefronts x 4 rows, so a
+// 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
+//   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
 //      share of its 4 rows' 16-byte pieces (4 D/32 pieces dealt over the 64 lanes in
 //      turn, so every lane has the same count but the last round);
@@ -27,10 +28,16 @@ namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kUpThreads = 1024;  // 16 wavefronts
-constexpr int kUpRows = 4;        // rows per wavefront: 64 rows (one mask group) per workgroup
-constexpr int kUpMaxD = 4096;     // inputs per token held in LDS
+constexpr int kUpWaves = 4;
+constexpr int kUpThreads = 64 * kUpWaves;
+constexpr int kUpRows = 4;                      // rows per wavefront
+constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (a quarter mask group)
+constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS
 constexpr int kUpMaxP = kUpMaxD / 32;
+constexpr int kUpXIt = (kUpMaxD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
+// Workgroups of 16 rows measured faster than 64-row ones (1024 threads): a workgroup
+// starts its arithmetic as soon as its own loads are in, and 928 workgroups fill all CUs
+// at the reference shape where 232 left 24 idle.
 constexpr uint32_t kBfOne2 = 0x3F803F80u;   // bf16 1.0 in both halves
 constexpr uint32_t kNibHi = 0x00780078u;    // mantissa bits 3..6 of both halves
 
@@ -48,13 +55,13 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   // x pairs: piece j, word m, pair n at xp[(4 j + m) 4 + n] = (x[32 j + 8 m + n], x[.. + 4])
   __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
-  __shared__ int nib[kUpThreads / 64];
-  __shared__ __attribute__((aligned(16))) uint16_t sl[64 * (kUpMaxD / 64)];  // [row][group]
-  __shared__ __attribute__((aligned(16))) uint16_t bl[64 * (kUpMaxD / 64)];
-  const int b = blockIdx.y, grp = blockIdx.x;
+  __shared__ int nib[kUpWaves];
+  __shared__ __attribute__((aligned(16))) uint16_t sl[kUpBlk * (kUpMaxD / 64)];  // [row][group]
+  __shared__ __attribute__((aligned(16))) uint16_t bl[kUpBlk * (kUpMaxD / 64)];
+  const int b = blockIdx.y, blk = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
-  const int r0 = 64 * grp;
+  const int r0 = kUpBlk * blk;
   const bool routed = r0 < topk * F;
   const int k = routed ? r0 / F : topk;
   const int f0 = routed ? r0 - k * F : r0 - topk * F;
@@ -62,15 +69,18 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   // ---- round trip: x, the expert id, the rows' pieces and their scales (no load under a
   // branch: indices past the end are clamped and the values dropped)
   const int e = routed ? sel[b * topk + k] : 0;
-  const uint4 xv = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid, NW - 1)];
+  uint4 xv[kUpXIt];
+#pragma unroll
+  for (int i = 0; i < kUpXIt; ++i)
+    xv[i] = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid + kUpThreads * i, NW - 1)];
   const bool ok = !routed || (unsigned)e < (unsigned)E;
   const size_t row0 = routed ? (size_t)(ok ? e : 0) * F + f0 : (size_t)f0;
   const uint32_t* wb = routed ? w1 : sw1;
   const uint16_t* sb = routed ? s1 : ss1;
   const uint16_t* bb = routed ? b1 : sb1;
-  // the 64 rows' scales and biases: 64 NGD bf16 each, contiguous and 16-byte aligned (64
-  // rows x 2 NGD bytes); threads [0, 8 NGD) load s, [8 NGD, 16 NGD) load b
-  const int nsc = 8 * NGD;
+  // the 16 rows' scales and biases: 16 NGD bf16 each, contiguous and 16-byte aligned (16
+  // rows x 2 NGD bytes); threads [0, 2 NGD) load s, [2 NGD, 4 NGD) load b (4 NGD <= 256)
+  const int nsc = 2 * NGD;
   const int sc_i = tid < nsc ? tid : min(tid - nsc, nsc - 1);
   const uint4 scv = reinterpret_cast<const uint4*>((tid < nsc ? sb : bb) + row0 * NGD)[sc_i];
   // pieces: index p = lane + 64 it over the wave's 4 rows x NP pieces
@@ -87,26 +97,27 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
     q[it] = wr[pj[it]];  // rounds past nit re-read the last piece, unused
   }
 
-  // ---- x pairs and piece sums into LDS: thread t holds inputs 8t .. 8t+7 (one word's)
-  if (tid < NW) {
-    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};  // bf16 pairs (x[8t+2c], x[8t+2c+1])
-    auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
-    uint4 pr;
-    pr.x = el(0) | (el(4) << 16);
-    pr.y = el(1) | (el(5) << 16);
-    pr.z = el(2) | (el(6) << 16);
-    pr.w = el(3) | (el(7) << 16);
-    *reinterpret_cast<uint4*>(&xp[4 * tid]) = pr;
-  }
-  float s8 = 0.0f;
-  {
-    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+  // ---- x pairs and piece sums into LDS: word t = tid + 256 i holds inputs 8t .. 8t+7
 #pragma unroll
-    for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32((n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu);
+  for (int i = 0; i < kUpXIt; ++i) {
+    const int t = tid + kUpThreads * i;
+    const uint32_t w[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};  // bf16 pairs (x[8t+2c], x[8t+2c+1])
+    auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
+    if (t < NW) {
+      uint4 pr;
+      pr.x = el(0) | (el(4) << 16);
+      pr.y = el(1) | (el(5) << 16);
+      pr.z = el(2) | (el(6) << 16);
+      pr.w = el(3) | (el(7) << 16);
+      *reinterpret_cast<uint4*>(&xp[4 * t]) = pr;
+    }
+    float s8 = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32(el(n));
+    s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
+    s8 += dpp_f32<0x4E>(s8);
+    if (t < NW && (t & 3) == 0) xh[t >> 2] = s8;
   }
-  s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
-  s8 += dpp_f32<0x4E>(s8);
-  if (tid < NW && (tid & 3) == 0) xh[tid >> 2] = s8;
   if (tid < 2 * nsc) *reinterpret_cast<uint4*>((tid < nsc ? sl : bl) + 8 * sc_i) = scv;
   lds_barrier();
 
@@ -169,10 +180,13 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   if (live_out) {
     lds_barrier();
     if (tid == 0) {
-      uint64_t m = 0;
+      // this block's 16 bits of the group's 64-bit mask (little-endian: quarter q of
+      // group g is 16-bit word 4 g + q)
+      uint32_t m = 0;
 #pragma unroll
-      for (int w = 0; w < kUpThreads / 64; ++w) m |= (uint64_t)nib[w] << (kUpRows * w);
-      live_out[(size_t)b * (NR / 64) + grp] = m;
+      for (int w = 0; w < kUpWaves; ++w) m |= (uint32_t)nib[w] << (kUpRows * w);
+      reinterpret_cast<uint16_t*>(live_out)[((size_t)b * (NR / 64) + r0 / 64) * 4 + (r0 % 64) / kUpBlk] =
+          (uint16_t)m;
     }
   }
   if (!ok && tid == 0 && f0 == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
@@ -198,10 +212,12 @@ extern "C" int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, 
                      kUpMaxD);
   if (B > 65535 || (topk * F + FS) / 64 > 0x7FFFFFFF || E * F * (D / 8) >= ((int64_t)1 << 40))
     return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
-  const uintptr_t al = (uintptr_t)x | (uintptr_t)w1 | (uintptr_t)sw1;
-  if (al & 15u) return set_error(HSD_ERR_ALIGN, "%s: x and the weights must be 16-byte aligned", fn);
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)w1 | (uintptr_t)sw1 | (uintptr_t)s1 | (uintptr_t)b1 |
+                       (uintptr_t)ss1 | (uintptr_t)sb1;
+  if (al & 15u)
+    return set_error(HSD_ERR_ALIGN, "%s: x, the weights, scales and biases must be 16-byte aligned", fn);
   if (B == 0) return HSD_OK;
-  const dim3 grid((unsigned)((topk * F + FS) / 64), (unsigned)B);
+  const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
   hipLaunchKernelGGL(k_moe_up, grid, dim3(kUpThreads), 0, as_stream(stream),
                      reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,
                      reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F,

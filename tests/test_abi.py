@@ -59,6 +59,12 @@ def test_argument_errors_are_reported():
     odd = ctypes.c_void_p(18)
     args2 = [dummy, 0, dummy, dummy, dummy, odd] + [dummy] * 4 + [dummy, 0]
     assert lib.hsd_sparse_down_decode(*args2, 1, 2688, 1856, 3712, 6, 128, 0, None, None, None, 0, None) == -4
+    # front end: misaligned scales (each of the four arrays is loaded 16 bytes at a time)
+    for i in range(4):
+        sc = [dummy] * 4
+        sc[i] = odd
+        assert lib.hsd_moe_up_relu2(dummy, 0, dummy, dummy, sc[0], sc[1], dummy, sc[2], sc[3], dummy,
+                                    1, 2688, 1856, 3712, 6, 128, None, None, None) == -4
     assert lib.hsd_mamba_verify(*([dummy, 10304] * 3), *([dummy] * 9), 4, dummy, 0,
                                 3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, dummy, 1 << 20, None) == -2  # N != 128
     assert lib.hsd_mamba_select_row(dummy, None, 4, 4, None) == -1                 # n_keep >= nslab
