@@ -3,11 +3,11 @@
 // the shared expert, ReLU^2, written to hcat [B, topk*F + FS] (bf16), plus the canonical
 // live mask of every 64-row group (the decode kernels' compaction input).
 //
-// k_moe_up: one workgroup per (token, 16-row block of hcat): 4 wavefronts x 4 rows, so a
-// 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
-//   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
+// k_moe_up: one workgroup per (token, 8-row block of hcat): 4 wavefronts x 2 rows, so a
+// 64-row mask group takes eight workgroups (each writes its byte of the group's mask).
+//   1. one round trip: the token's x, the block's expert id (a scalar load), the 8 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
-//      share of its 4 rows' 16-byte pieces (4 D/32 pieces dealt over the 64 lanes in
+//      share of its 2 rows' 16-byte pieces (2 D/32 pieces dealt over the 64 lanes in
 //      turn, so every lane has the same count but the last round);
 //   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
 //      and the sum of x over every 32-input piece;
@@ -30,14 +30,17 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kUpWaves = 4;
 constexpr int kUpThreads = 64 * kUpWaves;
-constexpr int kUpRows = 4;                      // rows per wavefront
-constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (a quarter mask group)
+constexpr int kUpRows = 2;                      // rows per wavefront
+constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (an eighth of a mask group)
 constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS
 constexpr int kUpMaxP = kUpMaxD / 32;
 constexpr int kUpXIt = (kUpMaxD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
-// Workgroups of 16 rows measured faster than 64-row ones (1024 threads): a workgroup
-// starts its arithmetic as soon as its own loads are in, and 928 workgroups fill all CUs
-// at the reference shape where 232 left 24 idle.
+static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
+              "a block is a quarter or an eighth of a mask group; one scale load per thread");
+// Small workgroups measured faster than 64-row ones (1024 threads; 9.0 us per call with 8
+// rows, 9.1 with 16, 10.1 with 64): a workgroup starts its arithmetic as soon as its own
+// loads are in, and 1856 workgroups fill all CUs at the reference shape where 232 left 24
+// idle.
 constexpr uint32_t kBfOne2 = 0x3F803F80u;   // bf16 1.0 in both halves
 constexpr uint32_t kNibHi = 0x00780078u;    // mantissa bits 3..6 of both halves
 
@@ -78,9 +81,9 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   const uint32_t* wb = routed ? w1 : sw1;
   const uint16_t* sb = routed ? s1 : ss1;
   const uint16_t* bb = routed ? b1 : sb1;
-  // the 16 rows' scales and biases: 16 NGD bf16 each, contiguous and 16-byte aligned (16
-  // rows x 2 NGD bytes); threads [0, 2 NGD) load s, [2 NGD, 4 NGD) load b (4 NGD <= 256)
-  const int nsc = 2 * NGD;
+  // the block's scales and biases: kUpBlk NGD bf16 each, contiguous and 16-byte aligned;
+  // threads [0, nsc) load s, [nsc, 2 nsc) load b (2 nsc <= kUpThreads)
+  const int nsc = kUpBlk * NGD / 8;
   const int sc_i = tid < nsc ? tid : min(tid - nsc, nsc - 1);
   const uint4 scv = reinterpret_cast<const uint4*>((tid < nsc ? sb : bb) + row0 * NGD)[sc_i];
   // pieces: index p = lane + 64 it over the wave's 4 rows x NP pieces
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
     if (it < nit) {  // uniform
-      const int j = pj[it], rl = kUpRows * wave + prow[it];  // piece, row within the 64
+      const int j = pj[it], rl = kUpRows * wave + prow[it];  // piece, row within the block
       const bool use = lane + 64 * it < npw;
       const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
       float acc = 0.0f;
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   const float r = ub != ub ? ub : fmaxf(ub, 0.0f);
   const uint16_t hb = f32_to_bf16_bits(r * r);
   if (lane < kUpRows) hcat[(size_t)b * NR + r0 + kUpRows * wave + lane] = hb;
-  const uint32_t lb = (uint32_t)(__ballot(lane < kUpRows && (hb & 0x7FFFu) != 0) & 0xFu);
+  const uint32_t lb = (uint32_t)(__ballot(lane < kUpRows && (hb & 0x7FFFu) != 0) & ((1u << kUpRows) - 1u));
   if (lane == 0) nib[wave] = (int)lb;
   if (live_out) {
     lds_barrier();
@@ -185,8 +188,11 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
       uint32_t m = 0;
 #pragma unroll
       for (int w = 0; w < kUpWaves; ++w) m |= (uint32_t)nib[w] << (kUpRows * w);
-      reinterpret_cast<uint16_t*>(live_out)[((size_t)b * (NR / 64) + r0 / 64) * 4 + (r0 % 64) / kUpBlk] =
-          (uint16_t)m;
+      const size_t piece = ((size_t)b * (NR / 64) + r0 / 64) * (64 / kUpBlk) + (r0 % 64) / kUpBlk;
+      if constexpr (kUpBlk == 16)
+        reinterpret_cast<uint16_t*>(live_out)[piece] = (uint16_t)m;
+      else
+        reinterpret_cast<uint8_t*>(live_out)[piece] = (uint8_t)m;
     }
   }
   if (!ok && tid == 0 && f0 == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
