@@ -23,6 +23,9 @@
 // 6 % slower per call, 4 (128 threads, 63 parts) 6 % slower.
 // k_sum_parts runs one wavefront per workgroup (42 at D = 2688): 2.5 % faster per call than
 // 256-thread workgroups (11).
+// Two row phases per group: one phase (128-thread workgroups) was 0.9 % faster at 90 % zeros
+// but needs a second batch of row loads once a group has more than 16 live rows (denser
+// activations, the dense-h control); four phases were 17 % slower.
 // No atomics, no inter-workgroup signalling: results are bit-reproducible, and a row
 // of a B-row call is computed exactly as that row alone.
 #include "hsd_common.h"
