@@ -1,6 +1,6 @@
 """GPU parity of the prefill path (hsd/prefill.py:48-321): tile order and union lists
 bit-exact against the oracle; the MFMA grouped GEMM against the float64 oracle within
-the north-star bound (bf16 operands, fp32 accumulation): |y - ref| <= 2e-2 + 1e-2*|ref|
+the bf16 parity bound (bf16 operands, fp32 accumulation): |y - ref| <= 2e-2 + 1e-2*|ref|
 elementwise and max|y - ref| <= 1e-2 * max|ref|."""
 import numpy as np
 import pytest
