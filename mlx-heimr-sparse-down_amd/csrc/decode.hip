@@ -4,7 +4,7 @@
 //
 // Split over (D chunk x groups) so that every CU gets an even share of the bytes and of
 // the arithmetic, then a fixed-order sum (the reference's partial + reduce structure,
-// decode.py:37-144). At the BASELINE shape (D=2688, F=1856, FS=3712, top-6 of 128 +
+// decode.py:37-144). At the Nemotron-3.5 MoE shape (D=2688, F=1856, FS=3712, top-6 of 128 +
 // shared) a token row has 232 64-neuron groups:
 //   * k_sparse_down_part: one workgroup = (128-output chunk c, part p of <=8 groups of
 //     one slot): 21 x 32 = 672 workgroups per row. 256 threads = 16 teams of 16 lanes;

@@ -9,7 +9,7 @@
 // same instruction sequence whatever L is, so L rows equal L single-row calls bit for
 // bit.
 //
-// Work split of the state update (BASELINE: H=64 heads x P=64 head_dim x N=128 state,
+// Work split of the state update (Nemotron-3.5 Mamba-2 layer: H=64 heads x P=64 head_dim x N=128 state,
 // G=8 groups, conv K=4, CD = 4096 + 2*8*128 = 6144 channels):
 //   one workgroup = (head h, block of 16 head_dim rows p): 256 WGs. It computes the conv
 //   + silu of its 16 x channels and of its group's 128 B and 128 C channels for all L

@@ -1,5 +1,5 @@
 """GPU parity of the sparse decode down projection (hsd/decode.py:37-186) at the
-BASELINE shape (D=2688, F=1856, FS=3712, top-6 of 128 + shared, affine 4-bit g64).
+Nemotron-3.5 MoE shape (D=2688, F=1856, FS=3712, top-6 of 128 + shared, affine 4-bit g64).
 
 Bars:
 * integer work bit-exact: the canonical live masks equal the oracle's;

@@ -1,6 +1,6 @@
 """GPU parity of the Mamba-2 multi-row verify with per-row checkpoints and rollback
 (hsd/mamba.py:19-56) and of the device greedy acceptance (hsd/model.py:419-427), at the
-BASELINE shape (64 heads x head_dim 64, state 128, 8 groups, conv 4, fp32 state).
+Nemotron-3.5 Mamba-2 shape (64 heads x head_dim 64, state 128, 8 groups, conv 4, fp32 state).
 
 Bars: the verify of L rows is BIT-IDENTICAL to L single-row calls (y, ssm and conv
 checkpoints); against the float64 oracle the fp32 states are within 1e-4 relative and
