@@ -81,6 +81,25 @@ int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel, const
                            int32_t* dev_status, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture that must not call hipMalloc, tight serving loops, harnesses
+ * that forbid allocation): hsd_sparse_down_decode without the workspace argument. The
+ * partial sums live in a static 4 MiB device array inside libhsd (one per GPU, held
+ * until the process ends; looked up with hipGetSymbolAddress on the first call on a
+ * device, with that device current -- `stream` must belong to the current device).
+ * Sizes whose partial sums exceed 4 MiB (hsd_sparse_down_workspace_bytes) are rejected
+ * with HSD_ERR_SHAPE: B <= 12 rows at the Nemotron-3.5 MoE shape. Every element of the
+ * array is written before it is read, so nothing is cleared between calls. Calls that
+ * overlap on one GPU (distinct streams, or concurrent host threads) share the array and
+ * race: serialise them. Same arguments, results and bit-for-bit output as
+ * hsd_sparse_down_decode. */
+int hsd_sparse_down_decode_noalloc(const void* h, int h_dtype, const int32_t* sel,
+                                   const float* gains, const uint32_t* pw, const uint16_t* ps,
+                                   const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
+                                   const uint16_t* spb, void* y, int y_dtype, int64_t B, int64_t D,
+                                   int64_t F, int64_t FS, int64_t topk, int64_t E, int dense,
+                                   uint64_t* live_masks, int32_t* dev_status, void* stream);
+
 /* ------------------------------------------------------------------ MoE front end
  * Replaces the MoE block's front end after the router, hsd/model.py:110-121: the routed
  * experts' up projection `gather_qmm(xn, fc1.weight, fc1.scales, fc1.biases,

@@ -30,6 +30,8 @@
 // of a B-row call is computed exactly as that row alone.
 #include "hsd_common.h"
 
+#include <mutex>
+
 namespace hsd {
 namespace {
 
@@ -400,33 +402,18 @@ extern "C" size_t hsd_sparse_down_workspace_bytes(int64_t B, int64_t D, int64_t 
   return (bytes + 255) & ~(size_t)255;
 }
 
-extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel,
-                                      const float* gains, const uint32_t* pw, const uint16_t* ps,
-                                      const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
-                                      const uint16_t* spb, void* y, int y_dtype, int64_t B,
-                                      int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
-                                      int dense, uint64_t* live_masks, int32_t* dev_status,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "hsd_sparse_down_decode";
-  if (!h || !sel || !gains || !pw || !ps || !pb || !spw || !sps || !spb || !y)
-    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
-  if (B < 0 || topk <= 0 || E <= 0) return set_error(HSD_ERR_SHAPE, "%s: bad B/topk/E", fn);
-  if (D <= 0 || D % kDC || F <= 0 || F % 64 || FS <= 0 || FS % 64)
-    return set_error(HSD_ERR_SHAPE, "%s: need D %% %d == 0, F %% 64 == 0, FS %% 64 == 0 (D=%lld F=%lld FS=%lld)",
-                     fn, kDC, (long long)D, (long long)F, (long long)FS);
-  if (topk * F + FS > (int64_t)1 << 30 || D > 65536 || B > 65535 ||
-      B * (topk * F + FS) >= ((int64_t)1 << 32) || F * (D / 8) >= ((int64_t)1 << 32) ||
-      FS * (D / 8) >= ((int64_t)1 << 32))
-    return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
-  if (!aligned16(ps) || !aligned16(pb) || !aligned16(sps) || !aligned16(spb))
-    return set_error(HSD_ERR_ALIGN, "%s: scales/biases must be 16-byte aligned", fn);
-  if (B == 0) return HSD_OK;
+namespace hsd {
+namespace {
+
+// The checks and the two launches of a sparse decode call, with the partial sums in
+// `part` (B * nparts * D floats; every element is written before it is read).
+int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t* sel,
+                       const float* gains, const uint32_t* pw, const uint16_t* ps,
+                       const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
+                       const uint16_t* spb, void* y, int y_dtype, int64_t B, int64_t D,
+                       int64_t F, int64_t FS, int64_t topk, int64_t E, int dense,
+                       uint64_t* live_masks, int32_t* dev_status, float* part, hipStream_t st) {
   const Geom g = make_geom(D, F, FS, topk, E);
-  const size_t need = hsd_sparse_down_workspace_bytes(B, D, F, FS, topk);
-  if (!workspace || workspace_bytes < need)
-    return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
-  float* part = reinterpret_cast<float*>(workspace);
-  hipStream_t st = as_stream(stream);
   const int64_t nblk = B * (int64_t)g.nwg;
   if (nblk > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too many workgroups", fn);
 #define HSD_PART(DT)                                                                          \
@@ -459,6 +446,108 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
   }
 #undef HSD_SUM
   return check_launch(fn);
+}
+
+// Argument checks shared by both sparse decode entry points.
+int check_sparse_down_args(const char* fn, const void* h, const int32_t* sel, const float* gains,
+                           const uint32_t* pw, const uint16_t* ps, const uint16_t* pb,
+                           const uint32_t* spw, const uint16_t* sps, const uint16_t* spb,
+                           const void* y, int64_t B, int64_t D, int64_t F, int64_t FS,
+                           int64_t topk, int64_t E) {
+  if (!h || !sel || !gains || !pw || !ps || !pb || !spw || !sps || !spb || !y)
+    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (B < 0 || topk <= 0 || E <= 0) return set_error(HSD_ERR_SHAPE, "%s: bad B/topk/E", fn);
+  if (D <= 0 || D % kDC || F <= 0 || F % 64 || FS <= 0 || FS % 64)
+    return set_error(HSD_ERR_SHAPE, "%s: need D %% %d == 0, F %% 64 == 0, FS %% 64 == 0 (D=%lld F=%lld FS=%lld)",
+                     fn, kDC, (long long)D, (long long)F, (long long)FS);
+  if (topk * F + FS > (int64_t)1 << 30 || D > 65536 || B > 65535 ||
+      B * (topk * F + FS) >= ((int64_t)1 << 32) || F * (D / 8) >= ((int64_t)1 << 32) ||
+      FS * (D / 8) >= ((int64_t)1 << 32))
+    return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  if (!aligned16(ps) || !aligned16(pb) || !aligned16(sps) || !aligned16(spb))
+    return set_error(HSD_ERR_ALIGN, "%s: scales/biases must be 16-byte aligned", fn);
+  return HSD_OK;
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// The partial sums of hsd_sparse_down_decode_noalloc live in this file-scope device array
+// (one copy per GPU, held until the process ends). Host code never passes the array's
+// name to a kernel: on the host it is only a stand-in for the symbol. Its device address
+// is looked up once per device with hipGetSymbolAddress and kept in g_scratch_dev.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on the first call on that device,
+// with that device current). nullptr with the error set on failure.
+float* scratch_for_current_device(const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(HSD_ERR_LAUNCH, "%s: hipGetDevice failed (%s)", fn, hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(HSD_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d (%s)", fn, dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_dev[dev] = reinterpret_cast<float*>(p);
+  }
+  return g_scratch_dev[dev];
+}
+
+}  // namespace
+}  // namespace hsd
+
+extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel,
+                                      const float* gains, const uint32_t* pw, const uint16_t* ps,
+                                      const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
+                                      const uint16_t* spb, void* y, int y_dtype, int64_t B,
+                                      int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
+                                      int dense, uint64_t* live_masks, int32_t* dev_status,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "hsd_sparse_down_decode";
+  int rc = check_sparse_down_args(fn, h, sel, gains, pw, ps, pb, spw, sps, spb, y, B, D, F, FS, topk, E);
+  if (rc) return rc;
+  if (B == 0) return HSD_OK;
+  const size_t need = hsd_sparse_down_workspace_bytes(B, D, F, FS, topk);
+  if (!workspace || workspace_bytes < need)
+    return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
+  return launch_sparse_down(fn, h, h_dtype, sel, gains, pw, ps, pb, spw, sps, spb, y, y_dtype, B, D, F, FS,
+                            topk, E, dense, live_masks, dev_status, reinterpret_cast<float*>(workspace),
+                            as_stream(stream));
+}
+
+extern "C" int hsd_sparse_down_decode_noalloc(const void* h, int h_dtype, const int32_t* sel,
+                                              const float* gains, const uint32_t* pw,
+                                              const uint16_t* ps, const uint16_t* pb,
+                                              const uint32_t* spw, const uint16_t* sps,
+                                              const uint16_t* spb, void* y, int y_dtype, int64_t B,
+                                              int64_t D, int64_t F, int64_t FS, int64_t topk,
+                                              int64_t E, int dense, uint64_t* live_masks,
+                                              int32_t* dev_status, void* stream) {
+  const char* fn = "hsd_sparse_down_decode_noalloc";
+  int rc = check_sparse_down_args(fn, h, sel, gains, pw, ps, pb, spw, sps, spb, y, B, D, F, FS, topk, E);
+  if (rc) return rc;
+  if (B == 0) return HSD_OK;
+  const size_t need = hsd_sparse_down_workspace_bytes(B, D, F, FS, topk);
+  if (need > kNoAllocScratchBytes)
+    return set_error(HSD_ERR_SHAPE,
+                     "%s: the partial sums need %zu bytes, more than the %zu-byte static scratch "
+                     "(at most B = %zu rows at this shape)",
+                     fn, need, kNoAllocScratchBytes, kNoAllocScratchBytes / (need / (size_t)B));
+  float* part = scratch_for_current_device(fn);
+  if (!part) return HSD_ERR_LAUNCH;
+  return launch_sparse_down(fn, h, h_dtype, sel, gains, pw, ps, pb, spw, sps, spb, y, y_dtype, B, D, F, FS,
+                            topk, E, dense, live_masks, dev_status, part, as_stream(stream));
 }
 
 extern "C" int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* sel,

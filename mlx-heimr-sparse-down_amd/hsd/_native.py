@@ -30,6 +30,9 @@ _SIGS = {
     "hsd_sparse_down_decode": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp, _vp,
                                         _vp, _c_size, _vp]),
+    "hsd_sparse_down_decode_noalloc": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                                _c_int, _vp, _vp, _vp]),
     "hsd_dense_down_decode": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "hsd_prefill_num_tiles": (_c_i64, [_c_i64] * 4),
