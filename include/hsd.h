@@ -34,8 +34,27 @@ enum {
 
 enum { HSD_DT_BF16 = 0, HSD_DT_F16 = 1, HSD_DT_F32 = 2 };
 
+/* hsd_linear: what x holds, the weight format, and what is written. */
+enum { HSD_X_BF16 = 0, HSD_X_RMS = 1, HSD_X_GATED = 2 };
+enum { HSD_W_Q4 = 0, HSD_W_BF16 = 1 };
+enum { HSD_Y_BF16 = 0, HSD_Y_F32 = 1, HSD_Y_RESID = 2, HSD_Y_ARGMAX = 3 };
+
 /* Bits of the device status word some kernels OR into (`dev_status`, nullable). */
-enum { HSD_STATUS_BAD_EXPERT = 1 };
+enum { HSD_STATUS_BAD_EXPERT = 1, HSD_STATUS_BAD_STATE = 2, HSD_STATUS_BAD_TOKEN = 4 };
+
+/* The sequence state of a generation (a device int32 array of HSD_SEQ_LEN entries), read
+ * and advanced by the step kernels so that a decode or verify step replays as one graph:
+ *   POS      tokens in the target's attention caches (the position of the next row)
+ *   CUR      the Mamba ring index shared by every Mamba layer
+ *   N        tokens emitted so far; TOK the last one (the next step's input)
+ *   HEAD_POS rows in the MTP head's attention cache; HEAD_POS2 the chained call's row
+ *   R        rows the head has not seen yet (the last verify's accepted count + 1)
+ *   ACCEPT   the last verify's accepted drafts; ACC_SUM their sum; STEPS steps taken */
+enum {
+  HSD_SEQ_POS = 0, HSD_SEQ_CUR = 1, HSD_SEQ_N = 2, HSD_SEQ_TOK = 3, HSD_SEQ_HEAD_POS = 4,
+  HSD_SEQ_R = 5, HSD_SEQ_HEAD_POS2 = 6, HSD_SEQ_ACCEPT = 7, HSD_SEQ_STEPS = 8, HSD_SEQ_ACC_SUM = 9,
+  HSD_SEQ_LEN = 16
+};
 
 const char* hsd_last_error(void);
 int hsd_abi_version(void);
@@ -81,6 +100,17 @@ int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t* sel, const
                            int32_t* dev_status, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Replaces hsd/model.py:136-139 after the front end: y = bf16(x + bf16(sparse_down(...)))
+ * -- the MoE block's residual add fused into the partial sum. x, y [B, D] bf16 (y may be
+ * x). Other arguments and requirements as hsd_sparse_down_decode. */
+int hsd_sparse_down_residual(const void* h, int h_dtype, const int32_t* sel, const float* gains,
+                             const uint32_t* pw, const uint16_t* ps, const uint16_t* pb,
+                             const uint32_t* spw, const uint16_t* sps, const uint16_t* spb,
+                             const uint16_t* x, uint16_t* y, int64_t B, int64_t D, int64_t F,
+                             int64_t FS, int64_t topk, int64_t E, int dense, uint64_t* live_masks,
+                             int32_t* dev_status, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* No counterpart in the reference. For callers that cannot allocate device memory (code
  * under HIP graph capture that must not call hipMalloc, tight serving loops, harnesses
  * that forbid allocation): hsd_sparse_down_decode without the workspace argument. The
@@ -122,6 +152,22 @@ int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, const uint3
                      int64_t F, int64_t FS, int64_t topk, int64_t E, uint64_t* live_masks,
                      int32_t* dev_status, void* stream);
 
+/* Replaces the MoE block's front end WITH the router, hsd/model.py:110-121 from `mix.gate`
+ * on (the gate of mlx-lm's NemotronH MoE, restated from the model family's published
+ * gate): from the gate's logits [B, E] bf16 (hsd_linear of the normed token with the bf16
+ * gate weight), score = sigmoid(logit) (fp32), choice = score + e_bias (nullable, [E] f32);
+ * sel[b] = the topk largest choices, descending (equal choices: the smaller expert id);
+ * gains[b] = score_k / (sum of the selected scores + 1e-20) * routed_scale (norm_topk),
+ * else score_k * routed_scale, then 1.0 for the shared expert; then hcat as
+ * hsd_moe_up_relu2. E <= 256, topk <= 8. sel [B, topk] int32 and gains [B, topk+1] f32 are
+ * written for the down projection. */
+int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t* logits, const float* e_bias,
+                           float routed_scale, int norm_topk, int32_t* sel, float* gains,
+                           const uint32_t* w1, const uint16_t* s1, const uint16_t* b1,
+                           const uint32_t* sw1, const uint16_t* ss1, const uint16_t* sb1, void* hcat,
+                           int64_t B, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
+                           uint64_t* live_masks, void* stream);
+
 /* The dense 4-bit down projection on the STOCK layout -- the comparator that
  * mlx-lm's gather_qmm + quantized_matmul compute in dense mode (model.py:132-133;
  * test_layout_decode.py:145-151). w [E, D, F/8], s/b [E, D, F/64]; sw [D, FS/8],
@@ -132,6 +178,112 @@ int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* sel, const 
                           const uint32_t* sw, const uint16_t* ss, const uint16_t* sb,
                           void* y, int y_dtype, int64_t B, int64_t D, int64_t F, int64_t FS,
                           int64_t topk, int64_t E, int32_t* dev_status, void* stream);
+
+/* ------------------------------------------------------------------ dense projections
+ * Replaces mlx `quantized_matmul(x, w, scales, biases, transpose=True, group_size=64,
+ * bits=4)` -- the QuantizedLinear layers of the model (Mamba in_proj/out_proj at
+ * hsd/mamba.py:26,44; the attention q/k/v/o projections and lm_head, model.py:226-230,
+ * 287, 343) -- and the bf16 `x @ W.T` of the router gate (model.py:115) and of the MTP
+ * head's eh_proj (mtp.py:83), for B <= 4 token rows: y[b, o] = sum_i xn[b, i] W[o, i].
+ *   w_kind HSD_W_Q4: w [O, I/8] u32 (8 nibbles per word, low first), scales/biases
+ *     [O, I/64] bf16, W = s q + b; HSD_W_BF16: w [O, I] bf16 (scales/biases unused).
+ *   x_kind HSD_X_BF16: xn = x [B, I] bf16 (row stride x_ld);
+ *          HSD_X_RMS:  xn = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * norm_w)
+ *                      (mx.fast.rms_norm, the block pre-norm, model.py:114, mamba.py:25);
+ *          HSD_X_GATED: x = y [B, I] f32, z = x * silu(gate) (gate bf16, stride gate_ld),
+ *                      per group of 512: xn = bf16(bf16(z * rsqrt(mean(z^2) + eps)) * norm_w)
+ *                      (the Mamba-2 gated RMSNorm, mamba.py:43).
+ *   y_kind HSD_Y_BF16 / HSD_Y_F32: y [B, O] (stride y_ld);
+ *          HSD_Y_RESID: y = bf16(res + bf16(x W^T)) (res bf16, stride res_ld; y may be res:
+ *                      the residual add `x + mixer(x)` of every block);
+ *          HSD_Y_ARGMAX: the per-workgroup best (value, index) of the bf16-rounded outputs
+ *                      into argmax_keys [B, key_ld] (key_ld >= hsd_linear_argmax_slots),
+ *                      for hsd_argmax_keys; y, when non-null, receives the bf16 outputs.
+ *   xn_out (nullable): receives xn (bf16 [B, I], stride xn_ld).
+ * Instantiated pairs (x_kind, y_kind): 4-bit -- (RMS, BF16), (RMS, F32), (RMS, ARGMAX),
+ * (GATED, RESID), (BF16, RESID), (BF16, BF16); bf16 weights -- (RMS, BF16), (BF16, BF16).
+ * Requirements: O a multiple of 8 (4-bit) or 4 (bf16); I <= 6144, a multiple of 64 (4-bit)
+ * or 8 (bf16), of 512 for the gated norm; x, gate, norm_w, w, xn_out 16-byte aligned with
+ * row strides of whole 16-byte pieces. A token row's arithmetic does not depend on B. */
+int64_t hsd_linear_argmax_slots(int64_t O, int w_kind);
+int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
+               const uint16_t* norm_w, float eps, const void* w, const uint16_t* scales,
+               const uint16_t* biases, int w_kind, void* y, int64_t y_ld, int y_kind,
+               const uint16_t* res, int64_t res_ld, uint16_t* xn_out, int64_t xn_ld,
+               uint64_t* argmax_keys, int64_t key_ld, int64_t B, int64_t O, int64_t I,
+               void* stream);
+
+/* Replaces `mx.argmax(logits, axis=-1)` after lm_head (model.py:302, 419): tok[b] = the
+ * index of the largest key of argmax_keys[b, :slots] written by hsd_linear's HSD_Y_ARGMAX
+ * (the first index among equal bf16 values; NaN beats numbers). */
+int hsd_argmax_keys(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, int64_t B,
+                    int32_t* tok, void* stream);
+
+/* ------------------------------------------------------------------ attention
+ * Replaces the attention block's scaled_dot_product_attention over mlx-lm's KVCache for
+ * decode (model.py:287) and verify steps (model.py:343, causal mask): B <= 4 rows at
+ * positions P .. P+B-1, P = *pos (device; the cache length before the call).
+ *   qkv [B, (HQ + 2 HKV) * HD] bf16 (row stride qkv_ld): q heads, then k, then v
+ *   k_cache, v_cache [HKV, smax, HD] bf16: rows P .. P+B-1 are written from qkv; rows
+ *   below P are read. A rollback is a smaller *pos (KVCache.trim, model.py:355).
+ *   out [B, HQ * HD] bf16: softmax(scale q k^T over keys 0 .. P+r) v per query head;
+ *   query head h reads kv head h / (HQ / HKV).
+ * P + B > smax: the call writes zeros and sets HSD_STATUS_BAD_STATE. Requirements:
+ * HD == 128, (HQ / HKV) % 8 == 0, smax % 64 == 0. A row's arithmetic does not depend on
+ * B. workspace: hsd_attn_workspace_bytes(B, HQ, smax). */
+size_t hsd_attn_workspace_bytes(int64_t B, int64_t HQ, int64_t smax);
+int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, uint16_t* k_cache,
+                    uint16_t* v_cache, int64_t smax, const int32_t* pos, uint16_t* out,
+                    int64_t out_ld, int64_t HQ, int64_t HKV, int64_t HD, float scale,
+                    int32_t* dev_status, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ step glue
+ * Replaces the quantised embedding lookup (model.py:223-224, mlx QuantizedEmbedding):
+ * out[b] = bf16(s q + b) of row tok[b] of w [V, D/8] u32, s/b [V, D/64] bf16. A token
+ * outside [0, V) gives zeros and HSD_STATUS_BAD_TOKEN. */
+int hsd_embed_q4(const int32_t* tok, int64_t B, const uint32_t* w, const uint16_t* scales,
+                 const uint16_t* biases, int64_t V, int64_t D, uint16_t* out, int64_t out_ld,
+                 int32_t* dev_status, void* stream);
+
+/* Replaces the MTP head's input, hsd/mtp.py:81-83: out[b] = concat(rms_norm(e[b], we),
+ * rms_norm(h[b], wh)) in bf16, [B, 2D]. */
+int hsd_pair_norm(const uint16_t* e, int64_t e_ld, const uint16_t* h, int64_t h_ld,
+                  const uint16_t* we, const uint16_t* wh, float eps, int64_t B, int64_t D,
+                  uint16_t* out, int64_t out_ld, void* stream);
+
+/* Replaces the loop body of hsd/model.py:314-321 after the step: the greedy token (the
+ * argmax of hsd_linear's keys for the last row), out_tokens[N] = it (N < cap), and the
+ * sequence state after one row: N, POS += 1, CUR = (CUR + 1) % nslab, TOK = the token. */
+int hsd_decode_advance(const uint64_t* argmax_keys, int64_t slots, int32_t* seq, int32_t* out_tokens,
+                       int64_t cap, int64_t nslab, void* stream);
+
+/* Replaces hsd/model.py:419-427 on the device: tgt[r] = argmax of verify row r (keys
+ * [k+1, key_ld]); a = first i < k with ids[1+i] != tgt[i], else k; the emitted tokens
+ * ids[1:1+a] + [tgt[a]] go to out_tokens at N (up to cap) and to pend (nullable, the MTP
+ * head's next token rows); then the rollback: POS and N += a+1, CUR = (CUR + a + 1) %
+ * nslab (model.py:348-356 with the Mamba checkpoint ring), HEAD_POS += R, R = a+1
+ * (mtp.trim, model.py:427), TOK = tgt[a]. tgt (nullable) receives the k+1 targets. */
+int hsd_spec_accept(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, int64_t k,
+                    const int32_t* ids, int32_t* seq, int32_t* out_tokens, int64_t cap, int64_t nslab,
+                    int32_t* pend, int32_t* tgt, void* stream);
+
+/* Replaces the chaining of hsd/model.py:408-414: from the MTP head's first call over 3
+ * pending rows (R = seq[HSD_SEQ_R] valid), d1[0] = the argmax of row R-1, h2 = its normed
+ * hidden row hn[R-1] (D bf16), and seq[HSD_SEQ_HEAD_POS2] = HEAD_POS + R (the cache row of
+ * the chained call). */
+int hsd_mtp_chain(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, const uint16_t* hn,
+                  int64_t hn_ld, int64_t D, int32_t* seq, int32_t* d1, uint16_t* h2, void* stream);
+
+/* The verify ids of hsd/model.py:416: ids = [TOK, d1[0], argmax(keys2)] for k = 2 drafts.
+ * With `script` (the true continuation, indexed by N) and `accepts` (an accepted count
+ * per step, indexed by STEPS), the drafts are forced: the true token for i < a_t and a
+ * wrong one at i = a_t (scripted acceptance; the head's own drafts are not used). */
+int hsd_draft_ids(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots, int64_t k,
+                  int32_t* seq, const int32_t* script, int64_t script_len, const int32_t* accepts,
+                  int64_t n_accepts, int64_t V, int32_t* ids, void* stream);
+
+/* seq[idx] += delta on the stream (host-known adjustments, e.g. the head's prefill rows). */
+int hsd_seq_add(int32_t* seq, int64_t idx, int64_t delta, void* stream);
 
 /* ------------------------------------------------------------------ prefill
  * Replaces hsd/prefill.py:247-278 `build_tiles(sel, E, tt)`: slots t*topk+k stably
@@ -186,6 +338,9 @@ int hsd_prefill_gemm(const uint16_t* h, const int32_t* sel, const float* gains,
  *   y [L, H*P] (y_dtype): rmsnorm over groups of norm_group of y_ssm*silu(gate), times
  *   norm_w. CD = H*P + 2*G*N. Requirements: N == 128, P % 16 == 0, H % G == 0,
  *   (H*P) % norm_group == 0, norm_group % 256 == 0.
+ * D is used rounded to bf16 (the reference passes m.D.astype(x.dtype), mamba.py:38).
+ * A ring index outside [0, nslab) reads and writes no state, makes y NaN and sets
+ * HSD_STATUS_BAD_STATE in dev_status (nullable).
  * A row's arithmetic does not depend on L: a verify of L rows is bit-identical to L
  * single-row calls. workspace: hsd_mamba_workspace_bytes(). */
 size_t hsd_mamba_workspace_bytes(int64_t L, int64_t H, int64_t P);
@@ -196,15 +351,26 @@ int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t
                      float* ssm_slabs, uint16_t* conv_slabs, const int32_t* cur, int64_t nslab,
                      void* y, int y_dtype, int64_t L, int64_t H, int64_t P, int64_t N,
                      int64_t G, int64_t norm_group, float eps, float dt_lo, float dt_hi,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     int32_t* dev_status, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The conv + SSM half of hsd_mamba_verify without the gated norm: y [L, H*P] f32 =
+ * sum_n S C + D x per row, the per-row checkpoints written to the ring as above. The
+ * model's Mamba block feeds y to out_proj through hsd_linear's HSD_X_GATED prologue. */
+int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
+                  const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log,
+                  const float* dt_bias, const float* Dp, float* ssm_slabs, uint16_t* conv_slabs,
+                  const int32_t* cur, int64_t nslab, float* y, int64_t L, int64_t H, int64_t P,
+                  int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream);
 
 /* Replaces hsd/mamba.py:47-56 `mamba_rollback(records, n_keep)` and the cache half of
  * model.py:348-356: the state after the first n_keep rows of the last verify is its
  * checkpoint slab, so the rollback is *cur = (*cur + n_keep) % nslab, on the device.
  * n_keep comes from *n_keep_dev when non-null (e.g. written by hsd_greedy_accept),
- * else from n_keep_host. n_keep == 0 keeps the state from before the verify. */
+ * else from n_keep_host. n_keep == 0 keeps the state from before the verify; n_keep
+ * outside [0, L] (L = the rows of that verify) leaves cur unchanged and sets
+ * HSD_STATUS_BAD_STATE in dev_status (nullable). */
 int hsd_mamba_select_row(int32_t* cur, const int32_t* n_keep_dev, int64_t n_keep_host,
-                         int64_t nslab, void* stream);
+                         int64_t L, int64_t nslab, int32_t* dev_status, void* stream);
 
 /* ------------------------------------------------------------------ acceptance
  * Replaces the greedy acceptance of hsd/model.py:419-427 on the device (no host

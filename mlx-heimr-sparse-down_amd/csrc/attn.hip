@@ -1,0 +1,269 @@
+// GQA attention for decode and verify steps over a KV cache that rollback trims by
+// moving its length: mlx-lm's NemotronH attention block as hsd runs it (model.py:287 for
+// a decode step, model.py:343 with a causal mask for a verify step; no positional
+// encoding in this model family), after the q/k/v projections.
+//
+// B <= 4 consecutive positions P .. P+B-1 (P = the cache length before the call, a
+// device int, so a captured graph replays at any length). Row r attends to keys
+// 0 .. P+r. The new keys and values come from the projection output itself and are also
+// written into the cache at P .. P+B-1; the cache is read only below P, so no kernel reads
+// what this launch writes.
+//
+//   k_attn_part: one workgroup per (kv head, 64-key chunk, half of the kv head's query
+//     heads). The chunk's keys go to LDS (rows padded by 16 bytes against bank
+//     conflicts); lane j of wave w scores key j against query heads 2w, 2w+1 (a q.k dot in
+//     fp32 with v_dot2_f32_bf16, times the scale); a wave's max and sum over its 64 keys
+//     (DPP); then p = exp(s - m) times V (LDS) into acc[128]. Writes the chunk's (m, l, acc)
+//     per row and head.
+//   k_attn_combine: one workgroup per (row, query head): the chunks of keys 0 .. P+r in
+//     chunk order: M = max m, L = sum l e^(m-M), o = sum acc e^(m-M) / L, rounded to bf16.
+// The chunk boundaries are absolute positions and each row's chunks are combined in the
+// same order whatever B is, so a row of a B-row verify is bit-identical to that row
+// computed by a single-row decode step.
+#include "hsd_common.h"
+
+namespace hsd {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHD = 128;        // head dim
+constexpr int kCH = 64;         // keys per chunk
+constexpr int kAMaxB = 4;
+constexpr int kHPW = 8;         // query heads per workgroup (2 per wavefront)
+constexpr int kKP = kHD / 2 + 4;  // padded K row in u32 (272 bytes)
+constexpr int kAT = 256;
+constexpr int kRec = kHD + 4;     // partial record: m, l, 2 unused, acc[128] (16-byte aligned)
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+struct AttnArgs {
+  const uint16_t* qkv;
+  int64_t qkv_ld;
+  uint16_t* kc;
+  uint16_t* vc;
+  int64_t smax;
+  const int32_t* pos;
+  float* part;            // [B][HQ][nch][kRec]
+  uint16_t* out;
+  int64_t out_ld;
+  int32_t* status;
+  int B, HQ, HKV, nch;
+  float scale;
+};
+
+__global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t ks[kCH][kKP];
+  __shared__ __attribute__((aligned(16))) uint32_t vs[kCH][kHD / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t qs[kAMaxB][kHPW][kHD / 2];
+  __shared__ float ps[kAMaxB][kHPW][kCH];
+  const int nhalf = a.HQ / a.HKV / kHPW;       // workgroups per (kv head, chunk)
+  const int g = blockIdx.x / (a.nch * nhalf);
+  const int rem = blockIdx.x - g * a.nch * nhalf;
+  const int c = rem / nhalf, hh = rem - c * nhalf;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int P = *a.pos;
+  const int B = a.B;
+  if (P < 0 || P + B > a.smax) {
+    if (blockIdx.x == 0 && tid == 0 && a.status) atomicOr(a.status, (int32_t)HSD_STATUS_BAD_STATE);
+    return;
+  }
+  const int j0 = c * kCH;
+  if (j0 > P + B - 1) return;                  // no key of this chunk is visible to any row
+  const int HQ = a.HQ, QD = HQ * kHD, KD = a.HKV * kHD;
+  const int hq0 = g * (HQ / a.HKV) + hh * kHPW;  // first query head of this workgroup
+
+  // ---- loads: the chunk's K and V rows (256 bytes each: 16 lanes x 16 bytes), from the
+  // cache below P and from the projection rows at P .. P+B-1; this workgroup's query
+  // heads for every row (8 heads x 256 bytes per row)
+  {
+    const int piece = tid & 15;
+#pragma unroll
+    for (int i = 0; i < kCH / 16; ++i) {
+      const int jl = (tid >> 4) + 16 * i, j = j0 + jl;
+      const bool cached = j < P;
+      const int r = min(max(j - P, 0), B - 1);
+      const uint16_t* ksrc = cached ? a.kc + ((size_t)g * a.smax + j) * kHD
+                                    : a.qkv + (size_t)r * a.qkv_ld + QD + g * kHD;
+      const uint16_t* vsrc = cached ? a.vc + ((size_t)g * a.smax + j) * kHD
+                                    : a.qkv + (size_t)r * a.qkv_ld + QD + KD + g * kHD;
+      const uint4 kv = reinterpret_cast<const uint4*>(ksrc)[piece];
+      const uint4 vv = reinterpret_cast<const uint4*>(vsrc)[piece];
+      *reinterpret_cast<uint4*>(&ks[jl][4 * piece]) = kv;
+      *reinterpret_cast<uint4*>(&vs[jl][4 * piece]) = vv;
+      // the new rows also go to the cache (hh == 0: one writer per position)
+      if (!cached && j < P + B && hh == 0) {
+        reinterpret_cast<uint4*>(a.kc + ((size_t)g * a.smax + j) * kHD)[piece] = kv;
+        reinterpret_cast<uint4*>(a.vc + ((size_t)g * a.smax + j) * kHD)[piece] = vv;
+      }
+    }
+    // queries: B rows x 8 heads x 16 pieces
+    for (int i = tid; i < B * kHPW * 16; i += kAT) {
+      const int r = i / (kHPW * 16), rem2 = i - r * kHPW * 16, h = rem2 >> 4, pc = rem2 & 15;
+      const uint4 qv = reinterpret_cast<const uint4*>(a.qkv + (size_t)r * a.qkv_ld + (hq0 + h) * kHD)[pc];
+      *reinterpret_cast<uint4*>(&qs[r][h][4 * pc]) = qv;
+    }
+  }
+  __syncthreads();
+
+  // ---- scores: lane = key j, wave w = heads 2w, 2w+1
+  const int j = j0 + lane;
+  float m[kAMaxB][2], l[kAMaxB][2];
+  {
+    uint32_t kr[kHD / 2];
+#pragma unroll
+    for (int i = 0; i < kHD / 8; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&ks[lane][4 * i]);
+      kr[4 * i] = v.x; kr[4 * i + 1] = v.y; kr[4 * i + 2] = v.z; kr[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int r = 0; r < kAMaxB; ++r) {
+      if (r < B) {                               // uniform
+        const bool vis = j <= P + r;
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const int h = 2 * wave + hi;
+          float s = 0.0f;
+#pragma unroll
+          for (int i = 0; i < kHD / 8; ++i) {
+            const uint4 qv = *reinterpret_cast<const uint4*>(&qs[r][h][4 * i]);
+            s = dot2(qv.x, kr[4 * i], s);
+            s = dot2(qv.y, kr[4 * i + 1], s);
+            s = dot2(qv.z, kr[4 * i + 2], s);
+            s = dot2(qv.w, kr[4 * i + 3], s);
+          }
+          s = vis ? s * a.scale : -INFINITY;
+          // wave max (DPP inside rows, then the four row maxima)
+          float mx = s;
+          mx = fmaxf(mx, dpp_f32<0xB1>(mx));
+          mx = fmaxf(mx, dpp_f32<0x4E>(mx));
+          mx = fmaxf(mx, dpp_f32<0x141>(mx));
+          mx = fmaxf(mx, dpp_f32<0x140>(mx));
+          const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0));
+          const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16));
+          const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32));
+          const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48));
+          const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));  // finite: key j0 is visible
+          const float p = vis ? __expf(s - M) : 0.0f;
+          ps[r][h][lane] = p;
+          m[r][hi] = M;
+          l[r][hi] = wave_sum_dpp(p);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- acc = sum_j p_j v_j: thread = (head h = tid / 32, dims 4 (tid % 32) .. +3)
+  {
+    const int h = tid >> 5, d0 = 4 * (tid & 31);
+    float acc[kAMaxB][4];
+#pragma unroll
+    for (int r = 0; r < kAMaxB; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
+    for (int jl = 0; jl < kCH; ++jl) {
+      const uint2 vv = *reinterpret_cast<const uint2*>(&vs[jl][d0 / 2]);
+      const float v0 = bf16_bits_to_f32(vv.x & 0xFFFFu), v1 = bf16_bits_to_f32(vv.x >> 16);
+      const float v2 = bf16_bits_to_f32(vv.y & 0xFFFFu), v3 = bf16_bits_to_f32(vv.y >> 16);
+#pragma unroll
+      for (int r = 0; r < kAMaxB; ++r) {
+        if (r < B) {
+          const float p = ps[r][h][jl];
+          acc[r][0] = fmaf(p, v0, acc[r][0]);
+          acc[r][1] = fmaf(p, v1, acc[r][1]);
+          acc[r][2] = fmaf(p, v2, acc[r][2]);
+          acc[r][3] = fmaf(p, v3, acc[r][3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kAMaxB; ++r) {
+      if (r < B && j0 <= P + r) {
+        float* dst = a.part + (((size_t)r * HQ + hq0 + h) * a.nch + c) * kRec;
+        *reinterpret_cast<float4*>(dst + 4 + d0) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+      }
+    }
+  }
+  // m and l of each (row, head): lane 0 of the wave that computed them
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < kAMaxB; ++r) {
+      if (r < B && j0 <= P + r) {
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          float* dst = a.part + (((size_t)r * HQ + hq0 + 2 * wave + hi) * a.nch + c) * kRec;
+          dst[0] = m[r][hi];
+          dst[1] = l[r][hi];
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
+  const int r = blockIdx.x / a.HQ, h = blockIdx.x - r * a.HQ;
+  const int d = threadIdx.x;
+  const int P = *a.pos;
+  uint16_t* o = a.out + (size_t)r * a.out_ld + (size_t)h * kHD;
+  if (P < 0 || P + a.B > a.smax) {
+    o[d] = 0;
+    return;
+  }
+  const int nc = (P + r) / kCH + 1;
+  const float* src = a.part + ((size_t)r * a.HQ + h) * a.nch * kRec;
+  float M = -INFINITY;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, src[(size_t)c * kRec]);
+  float L = 0.0f, acc = 0.0f;
+  for (int c = 0; c < nc; ++c) {
+    const float* pc = src + (size_t)c * kRec;
+    const float e = __expf(pc[0] - M);
+    L = fmaf(pc[1], e, L);
+    acc = fmaf(pc[4 + d], e, acc);
+  }
+  o[d] = f32_to_bf16_bits(acc / L);
+}
+
+}  // namespace
+}  // namespace hsd
+
+using namespace hsd;
+
+extern "C" size_t hsd_attn_workspace_bytes(int64_t B, int64_t HQ, int64_t smax) {
+  if (B <= 0 || HQ <= 0 || smax <= 0) return 0;
+  const int64_t nch = (smax + kCH - 1) / kCH;
+  return ((size_t)B * HQ * nch * kRec * sizeof(float) + 255) & ~(size_t)255;
+}
+
+extern "C" int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, uint16_t* k_cache,
+                               uint16_t* v_cache, int64_t smax, const int32_t* pos, uint16_t* out,
+                               int64_t out_ld, int64_t HQ, int64_t HKV, int64_t HD, float scale,
+                               int32_t* dev_status, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "hsd_attn_decode";
+  if (!qkv || !k_cache || !v_cache || !pos || !out) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (HD != kHD) return set_error(HSD_ERR_SHAPE, "%s: head_dim must be %d", fn, kHD);
+  if (B < 1 || B > kAMaxB) return set_error(HSD_ERR_SHAPE, "%s: B must be in [1, %d]", fn, kAMaxB);
+  if (HKV <= 0 || HQ <= 0 || HQ % HKV || (HQ / HKV) % kHPW)
+    return set_error(HSD_ERR_SHAPE, "%s: query heads per kv head must be a multiple of %d", fn, kHPW);
+  if (smax <= 0 || smax % kCH || smax > (1 << 24))
+    return set_error(HSD_ERR_SHAPE, "%s: the cache length must be a multiple of %d", fn, kCH);
+  if (qkv_ld < (HQ + 2 * HKV) * kHD || qkv_ld % 8 || out_ld < HQ * kHD)
+    return set_error(HSD_ERR_SHAPE, "%s: row strides", fn);
+  if (((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u)
+    return set_error(HSD_ERR_ALIGN, "%s: qkv and the caches must be 16-byte aligned", fn);
+  const size_t need = hsd_attn_workspace_bytes(B, HQ, smax);
+  if (!workspace || workspace_bytes < need) return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
+  const int nch = (int)(smax / kCH);
+  AttnArgs a{qkv, qkv_ld, k_cache, v_cache, smax, pos, reinterpret_cast<float*>(workspace), out, out_ld,
+             dev_status, (int)B, (int)HQ, (int)HKV, nch, scale};
+  hipStream_t st = as_stream(stream);
+  const int64_t nwg = HKV * nch * (HQ / HKV / kHPW);
+  if (nwg > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
+  hipLaunchKernelGGL(k_attn_part, dim3((unsigned)nwg), dim3(kAT), 0, st, a);
+  int rc = check_launch(fn);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)(B * HQ)), dim3(kHD), 0, st, a);
+  return check_launch(fn);
+}

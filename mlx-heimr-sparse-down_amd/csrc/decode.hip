@@ -251,27 +251,31 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
 
 constexpr int kSumThreads = 64;          // one wavefront per workgroup: 42 at D = 2688
 
+// y = the parts summed in part order; with res (bf16 y only): y = bf16(res + bf16(sum)),
+// the MoE block's residual add (model.py:139).
 template <int YDT, int NP>
 __global__ __launch_bounds__(kSumThreads) void k_sum_parts(const float* __restrict__ part,
                                                    typename Elem<YDT>::T* __restrict__ y, int D,
-                                                   int nparts, int n) {
+                                                   int nparts, int n, const uint16_t* __restrict__ res) {
   const int idx = blockIdx.x * kSumThreads + threadIdx.x;
   if (idx >= n) return;
   const int b = idx / D, o = idx - b * D;
   const float* pp = part + (size_t)b * nparts * D + o;
+  float s;
   if (NP > 0) {
     float v[NP > 0 ? NP : 1];
 #pragma unroll
     for (int q = 0; q < NP; ++q) v[q] = pp[(size_t)q * D];
-    float s = v[0];
+    s = v[0];
 #pragma unroll
     for (int q = 1; q < NP; ++q) s += v[q];
-    Elem<YDT>::store(y, idx, s);
   } else {
-    float s = pp[0];
+    s = pp[0];
     for (int q = 1; q < nparts; ++q) s += pp[(size_t)q * D];
-    Elem<YDT>::store(y, idx, s);
   }
+  if (YDT == HSD_DT_BF16 && res)
+    s = bf16_bits_to_f32(res[idx]) + bf16_bits_to_f32(f32_to_bf16_bits(s));
+  Elem<YDT>::store(y, idx, s);
 }
 
 // ----------------------------------------------------------------- dense comparator
@@ -412,7 +416,8 @@ int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t
                        const uint16_t* pb, const uint32_t* spw, const uint16_t* sps,
                        const uint16_t* spb, void* y, int y_dtype, int64_t B, int64_t D,
                        int64_t F, int64_t FS, int64_t topk, int64_t E, int dense,
-                       uint64_t* live_masks, int32_t* dev_status, float* part, hipStream_t st) {
+                       uint64_t* live_masks, int32_t* dev_status, float* part, hipStream_t st,
+                       const uint16_t* res = nullptr) {
   const Geom g = make_geom(D, F, FS, topk, E);
   const int64_t nblk = B * (int64_t)g.nwg;
   if (nblk > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too many workgroups", fn);
@@ -434,10 +439,10 @@ int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t
 #define HSD_SUM(DT)                                                                                  \
   if (g.nparts == 32)                                                                                \
     hipLaunchKernelGGL((k_sum_parts<DT, 32>), rgrid, dim3(kSumThreads), 0, st, part,                         \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n);            \
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n, res);       \
   else                                                                                               \
     hipLaunchKernelGGL((k_sum_parts<DT, 0>), rgrid, dim3(kSumThreads), 0, st, part,                          \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n);
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n, res);
   switch (y_dtype) {
     case HSD_DT_BF16: HSD_SUM(HSD_DT_BF16); break;
     case HSD_DT_F16: HSD_SUM(HSD_DT_F16); break;
@@ -524,6 +529,26 @@ extern "C" int hsd_sparse_down_decode(const void* h, int h_dtype, const int32_t*
   return launch_sparse_down(fn, h, h_dtype, sel, gains, pw, ps, pb, spw, sps, spb, y, y_dtype, B, D, F, FS,
                             topk, E, dense, live_masks, dev_status, reinterpret_cast<float*>(workspace),
                             as_stream(stream));
+}
+
+extern "C" int hsd_sparse_down_residual(const void* h, int h_dtype, const int32_t* sel, const float* gains,
+                                        const uint32_t* pw, const uint16_t* ps, const uint16_t* pb,
+                                        const uint32_t* spw, const uint16_t* sps, const uint16_t* spb,
+                                        const uint16_t* x, uint16_t* y, int64_t B, int64_t D, int64_t F,
+                                        int64_t FS, int64_t topk, int64_t E, int dense, uint64_t* live_masks,
+                                        int32_t* dev_status, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  const char* fn = "hsd_sparse_down_residual";
+  if (!x) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  int rc = check_sparse_down_args(fn, h, sel, gains, pw, ps, pb, spw, sps, spb, y, B, D, F, FS, topk, E);
+  if (rc) return rc;
+  if (B == 0) return HSD_OK;
+  const size_t need = hsd_sparse_down_workspace_bytes(B, D, F, FS, topk);
+  if (!workspace || workspace_bytes < need)
+    return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
+  return launch_sparse_down(fn, h, h_dtype, sel, gains, pw, ps, pb, spw, sps, spb, y, HSD_DT_BF16, B, D, F, FS,
+                            topk, E, dense, live_masks, dev_status, reinterpret_cast<float*>(workspace),
+                            as_stream(stream), x);
 }
 
 extern "C" int hsd_sparse_down_decode_noalloc(const void* h, int h_dtype, const int32_t* sel,

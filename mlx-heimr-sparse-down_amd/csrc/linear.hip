@@ -1,0 +1,538 @@
+// The dense projections of a decode step: y = x W^T for B <= 4 token rows, with W in
+// the checkpoint's affine 4-bit group-64 layout (mlx `quantized_matmul(x, w, scales,
+// biases, transpose=True)`, the QuantizedLinear of every Mamba in/out projection,
+// attention projection and lm_head) or in bf16 (the router gate, the MTP head's eh_proj).
+//
+// Optional fused prologues on x (each workgroup recomputes them for its rows, so no
+// separate normalisation launch):
+//   HSD_X_RMS    xn = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)    (mx.fast.rms_norm)
+//   HSD_X_GATED  z = y * silu(gate); per group of 512: xn = bf16(bf16(z * rsqrt(mean(z^2)
+//                + eps)) * w)     (the Mamba-2 gated RMSNorm in front of out_proj)
+// and epilogues: bf16 or f32 output, a residual add y = bf16(res + bf16(x W^T)), or the
+// greedy argmax of the bf16-rounded outputs (per-workgroup best keys, reduced by
+// hsd_argmax_keys; lm_head + argmax without writing the logits).
+//
+// Work split: a workgroup (4 wavefronts) owns 8 consecutive output rows (4-bit: 2 per
+// wavefront) or 4 (bf16: 1 per wavefront) and loops over row blocks strided by the grid
+// (at most 2048 workgroups, so the prologue is paid once per workgroup). A row's 16-byte
+// pieces are dealt over the wavefront's 64 lanes; the next block's pieces are loaded
+// while the current one is computed. 4-bit pieces are turned into bf16 pairs (1 + q/16)
+// with a shift, a mask and an OR, and v_dot2_f32_bf16 accumulates x (1 + q/16); per
+// 32-input piece u += 16 s acc + (b - 16 s) sum(x) (the affine dequantisation folded per
+// piece). A row's 64 lane partials are summed with DPP in a fixed order.
+//
+// Every token row is computed by the same instruction sequence whatever B is: a row of a
+// B-row call is bit-identical to the same row alone (verify rows == decode rows).
+#include "hsd_common.h"
+
+#include <algorithm>
+
+namespace hsd {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kLT = 256;                 // threads per workgroup
+constexpr int kLMaxB = 4;                // token rows per launch
+constexpr int kLMaxI = 6144;             // inputs per row
+constexpr int kLMaxGrid = 2048;
+constexpr uint32_t kBfOne2 = 0x3F803F80u;
+constexpr uint32_t kNibHi = 0x00780078u;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+__device__ __forceinline__ float rne_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// Order key of a bf16 value for a max: larger values give larger keys; NaN (the
+// canonical positive 0x7FC0) beats every number. Low 32 bits: ~index, so equal values
+// prefer the smaller index.
+__device__ __forceinline__ uint64_t argmax_key(uint16_t bits, int idx) {
+  const uint32_t ord = (bits & 0x8000u) ? (uint32_t)(~bits & 0xFFFFu) : (uint32_t)(bits | 0x8000u);
+  const uint32_t o2 = ((bits & 0x7FFFu) > 0x7F80u) ? 0x1FFFFu : ord;  // NaN above +inf
+  return ((uint64_t)o2 << 32) | (uint32_t)~(uint32_t)idx;
+}
+
+template <int WF> struct WTraits;
+template <> struct WTraits<HSD_W_Q4> {
+  static constexpr int kRW = 2;                         // rows per wavefront
+  static constexpr int kIn = 32;                        // inputs per 16-byte piece
+};
+template <> struct WTraits<HSD_W_BF16> {
+  static constexpr int kRW = 1;
+  static constexpr int kIn = 8;
+};
+// pieces per lane for rows of up to I inputs
+template <int WF> constexpr int pieces_per_lane(int I) { return (WTraits<WF>::kRW * (I / WTraits<WF>::kIn) + 63) / 64; }
+
+struct LinArgs {
+  const void* x;
+  int64_t x_ld;
+  const uint16_t* gate;
+  int64_t gate_ld;
+  const uint16_t* nw;
+  float eps;
+  const void* w;
+  const uint16_t* s;
+  const uint16_t* bq;
+  void* y;
+  int64_t y_ld;
+  const uint16_t* res;
+  int64_t res_ld;
+  uint16_t* xn_out;
+  int64_t xn_ld;
+  uint64_t* keys;
+  int64_t key_ld;
+  int O, I;
+};
+
+// IMAX: the largest row length the instance serves (kIt weight pieces per lane, XIT x
+// words of 8 inputs per thread in the prologue).
+template <int WF, int NB, int XK, int YK, int IMAX>
+__global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
+  using T = WTraits<WF>;
+  constexpr int kRW = T::kRW, kIt = pieces_per_lane<WF>(IMAX);
+  constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
+  constexpr int kRows = 4 * kRW;                       // rows per block
+  extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
+  // LDS: x as bf16 pairs [NB][I/2] (4-bit: pairs (x[i], x[i+4]) in a word's nibble
+  // order; bf16: natural pairs), then the 32-input piece sums [NB][I/32] (4-bit only)
+  __shared__ float wsum[NB][4];
+  __shared__ uint64_t kbest[4][NB];
+  const int I = a.I, O = a.O, NW = I / 8;
+  uint32_t* xp = lsm;
+  float* xh = reinterpret_cast<float*>(lsm + NB * (I / 2));
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nblk = O / kRows;
+  const int NPr = I / T::kIn;                          // pieces per row
+  const int npw = kRW * NPr;                           // pieces per wavefront
+  const int nit = (npw + 63) / 64;
+
+  // ---- weight pieces of a block: piece p = lane + 64 it of the wave's kRW rows
+  uint4 q[kIt];
+  float sc[WF == HSD_W_Q4 ? kIt : 1], bi[WF == HSD_W_Q4 ? kIt : 1];
+  auto load_block = [&](int blk, uint4 (&qq)[kIt], float* ss, float* bb) {
+    const int r0 = blk * kRows + kRW * wave;
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int p = min(lane + 64 * it, npw - 1);      // past the end: re-read the last piece
+      const int pr = p / NPr, pj = p - pr * NPr;
+      if constexpr (WF == HSD_W_Q4) {
+        const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)(r0 + pr) * NW;
+        qq[it] = reinterpret_cast<const uint4*>(wr)[pj];
+        const size_t gi = (size_t)(r0 + pr) * (I / 64) + (pj >> 1);
+        ss[it] = bf16_bits_to_f32(a.s[gi]);
+        bb[it] = bf16_bits_to_f32(a.bq[gi]);
+      } else {
+        const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w) + (size_t)(r0 + pr) * I;
+        qq[it] = reinterpret_cast<const uint4*>(wr)[pj];
+      }
+    }
+  };
+  int blk = blockIdx.x;
+  load_block(blk, q, sc, bi);
+
+  // ---- prologue: this workgroup's copy of the NB input rows, normalised if asked
+  // words t = tid + 256 i hold inputs 8t .. 8t+7
+  uint4 xv[NB][XIT];
+  float4 yv0[XK == HSD_X_GATED ? NB : 1][XIT], yv1[XK == HSD_X_GATED ? NB : 1][XIT];
+  uint4 nwv[XIT];
+#pragma unroll
+  for (int i = 0; i < XIT; ++i) {
+    const int tc = min(tid + kLT * i, NW - 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if constexpr (XK == HSD_X_GATED) {
+        const float4* yr = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + b * a.x_ld);
+        yv0[b][i] = yr[2 * tc];
+        yv1[b][i] = yr[2 * tc + 1];
+        xv[b][i] = reinterpret_cast<const uint4*>(a.gate + b * a.gate_ld)[tc];
+      } else {
+        xv[b][i] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + b * a.x_ld)[tc];
+      }
+    }
+    if constexpr (XK != HSD_X_BF16) nwv[i] = reinterpret_cast<const uint4*>(a.nw)[tc];
+  }
+  // xe[b][i][n]: the prologue's output element 8t + n as bf16 bits
+  uint32_t xo[NB][XIT][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float ss = 0.0f;
+    float zf[XIT][8];
+#pragma unroll
+    for (int i = 0; i < XIT; ++i) {
+      const bool tv = tid + kLT * i < NW;
+      const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const uint32_t bits = (n & 1) ? xw[n >> 1] >> 16 : xw[n >> 1] & 0xFFFFu;
+        float v = bf16_bits_to_f32(bits);
+        if constexpr (XK == HSD_X_GATED) {
+          const float yy = n < 4 ? (&yv0[b][i].x)[n] : (&yv1[b][i].x)[n - 4];
+          v = yy * silu_f32(v);
+        }
+        zf[i][n] = tv ? v : 0.0f;
+      }
+      if constexpr (XK == HSD_X_RMS) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) ss = fmaf(zf[i][n], zf[i][n], ss);
+      }
+    }
+    if constexpr (XK == HSD_X_RMS) {
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) wsum[b][wave] = ss;
+    }
+    if constexpr (XK == HSD_X_GATED) {
+      // a wavefront's 64 words of iteration i are one 512-element group
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        float g = 0.0f;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) g = fmaf(zf[i][n], zf[i][n], g);
+        g = wave_sum_dpp(g);
+        const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
+        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float w0 = bf16_bits_to_f32(nw4[c] & 0xFFFFu), w1 = bf16_bits_to_f32(nw4[c] >> 16);
+          const uint32_t lo = f32_to_bf16_bits(rne_bf16(zf[i][2 * c] * inv) * w0);
+          const uint32_t hi = f32_to_bf16_bits(rne_bf16(zf[i][2 * c + 1] * inv) * w1);
+          xo[b][i][c] = lo | (hi << 16);
+        }
+      }
+    } else if constexpr (XK == HSD_X_BF16) {
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        xo[b][i][0] = xv[b][i].x; xo[b][i][1] = xv[b][i].y; xo[b][i][2] = xv[b][i].z; xo[b][i][3] = xv[b][i].w;
+      }
+    }
+    (void)zf;
+  }
+  if constexpr (XK == HSD_X_RMS) {
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float tot = ((wsum[b][0] + wsum[b][1]) + wsum[b][2]) + wsum[b][3];
+      const float inv = __builtin_amdgcn_rsqf(tot / (float)I + a.eps);
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float x0 = bf16_bits_to_f32(xw[c] & 0xFFFFu), x1 = bf16_bits_to_f32(xw[c] >> 16);
+          const float w0 = bf16_bits_to_f32(nw4[c] & 0xFFFFu), w1 = bf16_bits_to_f32(nw4[c] >> 16);
+          const uint32_t lo = f32_to_bf16_bits(rne_bf16(x0 * inv) * w0);
+          const uint32_t hi = f32_to_bf16_bits(rne_bf16(x1 * inv) * w1);
+          xo[b][i][c] = lo | (hi << 16);
+        }
+      }
+    }
+  }
+  // ---- into LDS (and the side output)
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int i = 0; i < XIT; ++i) {
+      const int t = tid + kLT * i;
+      const uint32_t* w = xo[b][i];
+      auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
+      if (t < NW) {
+        uint4 pr;
+        if constexpr (WF == HSD_W_Q4) {
+          pr.x = el(0) | (el(4) << 16);
+          pr.y = el(1) | (el(5) << 16);
+          pr.z = el(2) | (el(6) << 16);
+          pr.w = el(3) | (el(7) << 16);
+        } else {
+          pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
+        }
+        *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * t]) = pr;
+        if (a.xn_out && blockIdx.x == 0)
+          reinterpret_cast<uint4*>(a.xn_out + b * a.xn_ld)[t] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      if constexpr (WF == HSD_W_Q4) {
+        float s8 = 0.0f;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32(el(n));
+        s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
+        s8 += dpp_f32<0x4E>(s8);
+        if (t < NW && (t & 3) == 0) xh[b * (I / 32) + (t >> 2)] = s8;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- row blocks
+  uint64_t best[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) best[b] = 0;
+  for (; blk < nblk; blk += gridDim.x) {
+    const int nxt = blk + gridDim.x;
+    uint4 qn[kIt];
+    float scn[WF == HSD_W_Q4 ? kIt : 1], bin[WF == HSD_W_Q4 ? kIt : 1];
+    // the next block's pieces in flight (past the last block: the last one again, unused;
+    // no load sits under a branch, which would make the compiler wait for the current ones)
+    load_block(min(nxt, nblk - 1), qn, scn, bin);
+    float pr[NB][kRW];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < kRW; ++r) pr[b][r] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      if (it < nit) {                                   // uniform
+        const int p0 = lane + 64 * it;
+        const bool use = p0 < npw;
+        const int p = min(p0, npw - 1);
+        const int prow = p / NPr, j = p - prow * NPr;
+        const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
+        if constexpr (WF == HSD_W_Q4) {
+          uint32_t wc[4][4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
+            wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
+            wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
+            wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
+          }
+          const float s16 = 16.0f * sc[it], bo = fmaf(-16.0f, sc[it], bi[it]);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (4 * j + m) * 4]);
+              acc = dot2_bf16(xq.x, wc[m][0], acc);
+              acc = dot2_bf16(xq.y, wc[m][1], acc);
+              acc = dot2_bf16(xq.z, wc[m][2], acc);
+              acc = dot2_bf16(xq.w, wc[m][3], acc);
+            }
+            const float t = use ? fmaf(s16, acc, bo * xh[b * (I / 32) + j]) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < kRW; ++r) pr[b][r] += prow == r ? t : 0.0f;
+          }
+        } else {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
+            float acc = 0.0f;
+            acc = dot2_bf16(xq.x, qw[0], acc);
+            acc = dot2_bf16(xq.y, qw[1], acc);
+            acc = dot2_bf16(xq.z, qw[2], acc);
+            acc = dot2_bf16(xq.w, qw[3], acc);
+            pr[b][0] += use ? acc : 0.0f;
+          }
+        }
+      }
+    }
+    // ---- row sums and the epilogue: lane b*kRW + r writes row r of token row b
+    float outv = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < kRW; ++r) {
+        float v = pr[b][r];
+        v += dpp_f32<0xB1>(v);
+        v += dpp_f32<0x4E>(v);
+        v += dpp_f32<0x141>(v);
+        v += dpp_f32<0x140>(v);
+        const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+        const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+        const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+        const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+        const float u = ((t0 + t1) + t2) + t3;
+        outv = lane == b * kRW + r ? u : outv;
+      }
+    }
+    const int ob = lane / kRW, orr = lane - ob * kRW;
+    const int o = blk * kRows + kRW * wave + orr;
+    if constexpr (YK == HSD_Y_ARGMAX) {
+      const uint16_t lb = f32_to_bf16_bits(outv);
+      uint64_t key = lane < NB * kRW ? argmax_key(lb, o) : 0;
+      if (a.y && lane < NB * kRW) reinterpret_cast<uint16_t*>(a.y)[ob * a.y_ld + o] = lb;
+      // best per token row over the wave's rows (lanes ob*kRW .. ob*kRW + kRW-1)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        uint64_t kb = 0;
+#pragma unroll
+        for (int r = 0; r < kRW; ++r) {
+          const uint64_t kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), b * kRW + r) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, b * kRW + r);
+          kb = kr > kb ? kr : kb;
+        }
+        best[b] = kb > best[b] ? kb : best[b];
+      }
+    } else if (lane < NB * kRW) {
+      const int64_t yi = ob * a.y_ld + o;
+      if constexpr (YK == HSD_Y_F32) {
+        reinterpret_cast<float*>(a.y)[yi] = outv;
+      } else if constexpr (YK == HSD_Y_RESID) {
+        const float rv = bf16_bits_to_f32(a.res[ob * a.res_ld + o]);
+        reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(rv + rne_bf16(outv));
+      } else {
+        reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(outv);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      q[it] = qn[it];
+      if constexpr (WF == HSD_W_Q4) { sc[it] = scn[it]; bi[it] = bin[it]; }
+    }
+  }
+  if constexpr (YK == HSD_Y_ARGMAX) {
+    if (lane == 0)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) kbest[wave][b] = best[b];
+    __syncthreads();
+    if (tid < NB) {
+      uint64_t k = kbest[0][tid];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) k = kbest[w][tid] > k ? kbest[w][tid] : k;
+      a.keys[tid * a.key_ld + blockIdx.x] = k;
+    }
+  }
+}
+
+// tok[b] = the index of the best key of row b (argmax with NaN first, then the larger
+// value, then the smaller index). One workgroup per row.
+__global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict__ keys, int64_t key_ld,
+                                                      int slots, int32_t* __restrict__ tok) {
+  __shared__ uint64_t wbest[16];
+  const int b = blockIdx.x;
+  uint64_t k = 0;
+  for (int i = threadIdx.x; i < slots; i += 1024) {
+    const uint64_t v = keys[b * key_ld + i];
+    k = v > k ? v : k;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
+                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
+    k = o > k ? o : k;
+  }
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t m = wbest[0];
+    for (int w = 1; w < 16; ++w) m = wbest[w] > m ? wbest[w] : m;
+    tok[b] = (int32_t)~(uint32_t)m;
+  }
+}
+
+int linear_grid(int O, int w_kind) {
+  const int rows = w_kind == HSD_W_Q4 ? 8 : 4;
+  return std::min(O / rows, kLMaxGrid);
+}
+
+}  // namespace
+}  // namespace hsd
+
+using namespace hsd;
+
+extern "C" int64_t hsd_linear_argmax_slots(int64_t O, int w_kind) {
+  if (O <= 0 || (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16)) return 0;
+  return linear_grid((int)std::min<int64_t>(O, 1 << 30), w_kind);
+}
+
+extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
+                          const uint16_t* norm_w, float eps, const void* w, const uint16_t* scales,
+                          const uint16_t* biases, int w_kind, void* y, int64_t y_ld, int y_kind,
+                          const uint16_t* res, int64_t res_ld, uint16_t* xn_out, int64_t xn_ld,
+                          uint64_t* argmax_keys, int64_t key_ld, int64_t B, int64_t O, int64_t I,
+                          void* stream) {
+  const char* fn = "hsd_linear";
+  if (!x || !w || (y_kind != HSD_Y_ARGMAX && !y)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (w_kind == HSD_W_Q4 && (!scales || !biases)) return set_error(HSD_ERR_ARG, "%s: 4-bit weights need scales and biases", fn);
+  if (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16) return set_error(HSD_ERR_DTYPE, "%s: w_kind %d", fn, w_kind);
+  if (x_kind != HSD_X_BF16 && x_kind != HSD_X_RMS && x_kind != HSD_X_GATED)
+    return set_error(HSD_ERR_DTYPE, "%s: x_kind %d", fn, x_kind);
+  if (y_kind < HSD_Y_BF16 || y_kind > HSD_Y_ARGMAX) return set_error(HSD_ERR_DTYPE, "%s: y_kind %d", fn, y_kind);
+  if (x_kind != HSD_X_BF16 && !norm_w) return set_error(HSD_ERR_ARG, "%s: the normalisation needs norm_w", fn);
+  if (x_kind == HSD_X_GATED && !gate) return set_error(HSD_ERR_ARG, "%s: the gated norm needs the gate", fn);
+  if (y_kind == HSD_Y_RESID && !res) return set_error(HSD_ERR_ARG, "%s: the residual epilogue needs res", fn);
+  if (y_kind == HSD_Y_ARGMAX && !argmax_keys) return set_error(HSD_ERR_ARG, "%s: argmax needs the key buffer", fn);
+  const int rows = w_kind == HSD_W_Q4 ? 8 : 4;
+  if (B < 0 || B > kLMaxB) return set_error(HSD_ERR_SHAPE, "%s: B must be in [0, %d]", fn, kLMaxB);
+  if (O <= 0 || O % rows || O > (1 << 28))
+    return set_error(HSD_ERR_SHAPE, "%s: O must be a positive multiple of %d", fn, rows);
+  if (I <= 0 || I > kLMaxI || I % (w_kind == HSD_W_Q4 ? 64 : 8))
+    return set_error(HSD_ERR_SHAPE, "%s: I must be a multiple of %d and at most %d", fn,
+                     w_kind == HSD_W_Q4 ? 64 : 8, kLMaxI);
+  if (x_kind == HSD_X_GATED && I % 512) return set_error(HSD_ERR_SHAPE, "%s: the gated norm needs I %% 512 == 0", fn);
+  const int64_t xe = x_kind == HSD_X_GATED ? 4 : 2;   // x element bytes
+  if (x_ld < I || (x_ld * xe) % 16 || ((uintptr_t)x & 15u) || (norm_w && ((uintptr_t)norm_w & 15u)) ||
+      ((uintptr_t)w & 15u) || (gate && (((uintptr_t)gate & 15u) || gate_ld % 8 || gate_ld < I)) ||
+      (xn_out && (((uintptr_t)xn_out & 15u) || xn_ld % 8 || xn_ld < I)))
+    return set_error(HSD_ERR_ALIGN, "%s: x, gate, norm_w, w and xn_out must be 16-byte aligned with row "
+                     "strides of whole 16-byte pieces", fn);
+  if (y_kind != HSD_Y_ARGMAX && y_ld < O) return set_error(HSD_ERR_SHAPE, "%s: y_ld < O", fn);
+  if (y_kind == HSD_Y_RESID && res_ld < O) return set_error(HSD_ERR_SHAPE, "%s: res_ld < O", fn);
+  const int grid = linear_grid((int)O, w_kind);
+  if (y_kind == HSD_Y_ARGMAX && key_ld < grid)
+    return set_error(HSD_ERR_SHAPE, "%s: key_ld must be >= hsd_linear_argmax_slots() = %d", fn, grid);
+  if (B == 0) return HSD_OK;
+  LinArgs a{x, x_ld, gate, gate_ld, norm_w, eps, w, scales, biases, y, y_ld, res, res_ld, xn_out, xn_ld,
+            argmax_keys, key_ld, (int)O, (int)I};
+  const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
+  hipStream_t st = as_stream(stream);
+  const bool small = I <= 3072;
+  // the (x_kind, y_kind) pairs this library instantiates
+  const int pair = x_kind * 8 + y_kind;
+  constexpr int kRB = HSD_X_RMS * 8 + HSD_Y_BF16, kRA = HSD_X_RMS * 8 + HSD_Y_ARGMAX,
+                kRF = HSD_X_RMS * 8 + HSD_Y_F32, kGR = HSD_X_GATED * 8 + HSD_Y_RESID,
+                kBR = HSD_X_BF16 * 8 + HSD_Y_RESID, kBB = HSD_X_BF16 * 8 + HSD_Y_BF16;
+  const bool ok = w_kind == HSD_W_Q4 ? (pair == kRB || pair == kRA || pair == kRF || pair == kGR ||
+                                        pair == kBR || pair == kBB)
+                                     : (pair == kRB || pair == kBB);
+  if (!ok)
+    return set_error(HSD_ERR_SHAPE, "%s: unsupported combination x_kind %d, y_kind %d, w_kind %d", fn, x_kind,
+                     y_kind, w_kind);
+#define HSD_LIN(WF, NB, XK, YK, IM) hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM>), dim3(grid), dim3(kLT), lds, st, a)
+#define HSD_LIN_I(WF, NB, XK, YK)     \
+  if (small) HSD_LIN(WF, NB, XK, YK, 3072); else HSD_LIN(WF, NB, XK, YK, kLMaxI);
+#define HSD_LIN_P(WF, NB)                                                  \
+  switch (pair) {                                                          \
+    case kRB: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_BF16); break;             \
+    case kBB: HSD_LIN_I(WF, NB, HSD_X_BF16, HSD_Y_BF16); break;            \
+    default:                                                               \
+      if constexpr (WF == HSD_W_Q4) {                                      \
+        switch (pair) {                                                    \
+          case kRA: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_ARGMAX); break;      \
+          case kRF: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_F32); break;         \
+          case kGR: HSD_LIN_I(WF, NB, HSD_X_GATED, HSD_Y_RESID); break;     \
+          default: HSD_LIN_I(WF, NB, HSD_X_BF16, HSD_Y_RESID); break;      \
+        }                                                                  \
+      }                                                                    \
+  }
+#define HSD_LIN_B(WF)                        \
+  switch (B) {                               \
+    case 1: HSD_LIN_P(WF, 1); break;         \
+    case 2: HSD_LIN_P(WF, 2); break;         \
+    case 3: HSD_LIN_P(WF, 3); break;         \
+    default: HSD_LIN_P(WF, 4); break;        \
+  }
+  if (w_kind == HSD_W_Q4) {
+    HSD_LIN_B(HSD_W_Q4);
+  } else {
+    HSD_LIN_B(HSD_W_BF16);
+  }
+#undef HSD_LIN_B
+#undef HSD_LIN_P
+#undef HSD_LIN_I
+#undef HSD_LIN
+  return check_launch(fn);
+}
+
+extern "C" int hsd_argmax_keys(const uint64_t* keys, int64_t key_ld, int64_t slots, int64_t B, int32_t* tok,
+                               void* stream) {
+  if (!keys || !tok) return set_error(HSD_ERR_ARG, "hsd_argmax_keys: null pointer");
+  if (B < 0 || B > 65535 || slots <= 0 || slots > key_ld || slots > (1 << 30))
+    return set_error(HSD_ERR_SHAPE, "hsd_argmax_keys: bad B/slots");
+  if (B == 0) return HSD_OK;
+  hipLaunchKernelGGL(k_argmax_keys, dim3((unsigned)B), dim3(1024), 0, as_stream(stream), keys, key_ld, (int)slots,
+                     tok);
+  return check_launch("hsd_argmax_keys");
+}

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     const float* __restrict__ A_log, const float* __restrict__ dt_bias,
     const float* __restrict__ Dp, float* __restrict__ ssm, uint16_t* __restrict__ convs,
     const int32_t* __restrict__ cur_ptr, int nslab, float* __restrict__ y_pre, int L, int H,
-    int P, int G, float dt_lo, float dt_hi) {
+    int P, int G, float dt_lo, float dt_hi, int32_t* __restrict__ status) {
   __shared__ float xs[kLMax][kPB];
   __shared__ __attribute__((aligned(16))) float Bs[kLMax][kN];
   __shared__ __attribute__((aligned(16))) float Cs[kLMax][kN];
@@ -84,8 +84,16 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   const uint16_t b1 = conv_b[ch1], b2 = conv_b[ch2];
   const int rd = min(max(tid - 64, 0), L - 1);  // wave 1's first L lanes: dt and dA
   const uint16_t dtr = dt_raw[(size_t)rd * dt_ld + hh];
-  const float Alog = A_log[hh], dtb = dt_bias[hh], Dh = Dp[hh];
-  if ((unsigned)cur >= (unsigned)nslab) return;  // a corrupt ring index: touch nothing
+  // D enters the recurrence rounded to bf16, as the reference passes m.D.astype(x.dtype)
+  // to ssm_update (mamba.py:38)
+  const float Alog = A_log[hh], dtb = dt_bias[hh], Dh = bf16_bits_to_f32(f32_to_bf16_bits(Dp[hh]));
+  if ((unsigned)cur >= (unsigned)nslab) {
+    // a corrupt ring index: no state is read or written; the rows' outputs become NaN and
+    // the status word says why
+    if (tid < kPB * L) y_pre[(size_t)(tid / kPB) * (H * P) + (size_t)hh * P + pblk * kPB + tid % kPB] = __int_as_float(0x7FC00000);
+    if (tid == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_STATE);
+    return;
+  }
 
   // the state rows: wave w owns rows 4w .. 4w+3 of the block, lane = 16 i + c holds
   // elements 8c .. 8c+7 of row 4w + i
@@ -239,12 +247,17 @@ __global__ __launch_bounds__(kMT) void k_gated_norm(const float* __restrict__ y_
   }
 }
 
+// cur += n_keep (mod nslab) for 0 <= n_keep <= L (the rows of the last verify); anything
+// else leaves cur unchanged and sets HSD_STATUS_BAD_STATE.
 __global__ void k_select_row(int32_t* cur, const int32_t* n_keep_dev, int n_keep_host,
-                             int nslab) {
+                             int nslab, int L, int32_t* status) {
   if (threadIdx.x == 0) {
     const int nk = n_keep_dev ? *n_keep_dev : n_keep_host;
     const int c = *cur;
-    if (nk >= 0 && nk < nslab && c >= 0 && c < nslab) *cur = (c + nk) % nslab;
+    if (nk >= 0 && nk <= L && nk < nslab && c >= 0 && c < nslab)
+      *cur = (c + nk) % nslab;
+    else if (status)
+      atomicOr(status, (int32_t)HSD_STATUS_BAD_STATE);
   }
 }
 
@@ -319,7 +332,8 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
                                 const int32_t* cur, int64_t nslab, void* y, int y_dtype,
                                 int64_t L, int64_t H, int64_t P, int64_t N, int64_t G,
                                 int64_t norm_group, float eps, float dt_lo, float dt_hi,
-                                void* workspace, size_t workspace_bytes, void* stream) {
+                                int32_t* dev_status, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   const char* fn = "hsd_mamba_verify";
   if (!conv_in || !dt_raw || !gate || !conv_w || !conv_b || !A_log || !dt_bias || !Dp ||
       !norm_w || !ssm_slabs || !conv_slabs || !cur || !y)
@@ -345,7 +359,7 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
   hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, st, conv_in,
                      conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias, Dp, ssm_slabs,
                      conv_slabs, cur, (int)nslab, y_pre, (int)L, (int)H, (int)P, (int)G, dt_lo,
-                     dt_hi);
+                     dt_hi, dev_status);
   int rc = check_launch(fn);
   if (rc) return rc;
   const unsigned ngrid = (unsigned)(L * (DI / norm_group));
@@ -372,14 +386,41 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
 }
 
 extern "C" int hsd_mamba_select_row(int32_t* cur, const int32_t* n_keep_dev, int64_t n_keep_host,
-                                    int64_t nslab, void* stream) {
+                                    int64_t L, int64_t nslab, int32_t* dev_status, void* stream) {
   if (!cur) return set_error(HSD_ERR_ARG, "hsd_mamba_select_row: null cur");
   if (nslab < 2 || nslab > kLMax + 1) return set_error(HSD_ERR_SHAPE, "hsd_mamba_select_row: bad nslab");
-  if (!n_keep_dev && (n_keep_host < 0 || n_keep_host >= nslab))
-    return set_error(HSD_ERR_ARG, "hsd_mamba_select_row: n_keep %lld outside [0, nslab)", (long long)n_keep_host);
+  if (L < 0 || L >= nslab) return set_error(HSD_ERR_SHAPE, "hsd_mamba_select_row: L must be in [0, nslab)");
+  if (!n_keep_dev && (n_keep_host < 0 || n_keep_host > L))
+    return set_error(HSD_ERR_ARG, "hsd_mamba_select_row: n_keep %lld outside [0, L = %lld]", (long long)n_keep_host,
+                     (long long)L);
   hipLaunchKernelGGL(k_select_row, dim3(1), dim3(64), 0, as_stream(stream), cur, n_keep_dev,
-                     (int)n_keep_host, (int)nslab);
+                     (int)n_keep_host, (int)nslab, (int)L, dev_status);
   return check_launch("hsd_mamba_select_row");
+}
+
+extern "C" int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
+                             const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log,
+                             const float* dt_bias, const float* Dp, float* ssm_slabs, uint16_t* conv_slabs,
+                             const int32_t* cur, int64_t nslab, float* y, int64_t L, int64_t H, int64_t P,
+                             int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream) {
+  const char* fn = "hsd_mamba_ssm";
+  if (!conv_in || !dt_raw || !conv_w || !conv_b || !A_log || !dt_bias || !Dp || !ssm_slabs || !conv_slabs ||
+      !cur || !y)
+    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (N != kN) return set_error(HSD_ERR_SHAPE, "%s: state size N must be %d (got %lld)", fn, kN, (long long)N);
+  if (L < 1 || L > kLMax || nslab < L + 1 || nslab > kLMax + 1)
+    return set_error(HSD_ERR_SHAPE, "%s: need 1 <= L <= nslab-1 <= %d (L=%lld nslab=%lld)", fn, kLMax,
+                     (long long)L, (long long)nslab);
+  if (H <= 0 || P <= 0 || P % kPB || G <= 0 || H % G)
+    return set_error(HSD_ERR_SHAPE, "%s: need P %% %d == 0 and H %% G == 0", fn, kPB);
+  const int64_t DI = H * P, CD = DI + 2 * G * N;
+  if (conv_in_ld < CD || dt_ld < H) return set_error(HSD_ERR_SHAPE, "%s: row strides smaller than the rows", fn);
+  if ((uintptr_t)ssm_slabs & 15u) return set_error(HSD_ERR_ALIGN, "%s: ssm_slabs must be 16-byte aligned", fn);
+  if (H * (P / kPB) > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
+  hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, as_stream(stream), conv_in,
+                     conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias, Dp, ssm_slabs, conv_slabs, cur,
+                     (int)nslab, y, (int)L, (int)H, (int)P, (int)G, dt_lo, dt_hi, dev_status);
+  return check_launch(fn);
 }
 
 extern "C" int hsd_greedy_accept(const void* logits, int dtype, int64_t k, int64_t V,

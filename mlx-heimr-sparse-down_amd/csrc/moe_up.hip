@@ -49,12 +49,75 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          false);
 }
 
+// The router's top-k (the gate of mlx-lm's NemotronH MoE, model.py:115; restated from the
+// model family's published gate): score = sigmoid(logit) in fp32, choice = score + bias;
+// the topk largest choices in descending order (equal choices: the smaller expert id);
+// gain_k = score_k / (sum of the selected scores + 1e-20) * scale (norm_topk), else
+// score_k * scale. Every lane ends with the same sel[] and gain[]. E <= 256.
+struct Router {
+  const uint16_t* logits;   // [B, E] bf16
+  const float* bias;        // [E] f32 (nullable)
+  int32_t* sel_out;         // [B, topk]
+  float* gains_out;         // [B, topk + 1]
+  float scale;
+  int norm_topk;
+};
+constexpr int kMaxTopk = 8;
+
+__device__ __forceinline__ uint32_t f32_order(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ void route_topk(const Router& rt, int b, int E, int topk, int lane, int (&sel)[kMaxTopk],
+                           float (&gain)[kMaxTopk]) {
+  uint64_t kk[4];
+  float sg[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int e = lane + 64 * v;
+    const bool valid = e < E;
+    const int ec = valid ? e : 0;
+    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + ec]);
+    const float bi = rt.bias ? rt.bias[ec] : 0.0f;
+    sg[v] = 1.0f / (1.0f + expf(-x));
+    const float c = sg[v] + bi;
+    kk[v] = valid ? ((uint64_t)f32_order(c) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e) : 0;
+  }
+  float ssum = 0.0f;
+  float sc[kMaxTopk];
+  for (int k = 0; k < topk; ++k) {
+    uint64_t m = kk[0];
+#pragma unroll
+    for (int v = 1; v < 4; ++v) m = kk[v] > m ? kk[v] : m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(m >> 32), off, 64) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)m, off, 64);
+      m = o > m ? o : m;
+    }
+    const int e = (int)(0xFFFFFFFFu - (uint32_t)m);
+    const int v = e >> 6;
+    float mine = sg[0];
+#pragma unroll
+    for (int vv = 1; vv < 4; ++vv) mine = v == vv ? sg[vv] : mine;
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) kk[vv] = kk[vv] == m ? 0 : kk[vv];
+    sel[k] = e;
+    sc[k] = s;
+    ssum += s;
+  }
+  for (int k = 0; k < topk; ++k) gain[k] = rt.norm_topk ? sc[k] / (ssum + 1e-20f) * rt.scale : sc[k] * rt.scale;
+}
+
+template <bool ROUTE>
 __global__ __launch_bounds__(kUpThreads) void k_moe_up(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ sel, const uint32_t* __restrict__ w1,
     const uint16_t* __restrict__ s1, const uint16_t* __restrict__ b1, const uint32_t* __restrict__ sw1,
     const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
     uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
-    int E) {
+    int E, Router rt) {
   // x pairs: piece j, word m, pair n at xp[(4 j + m) 4 + n] = (x[32 j + 8 m + n], x[.. + 4])
   __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
@@ -70,12 +133,33 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   const int f0 = routed ? r0 - k * F : r0 - topk * F;
 
   // ---- round trip: x, the expert id, the rows' pieces and their scales (no load under a
-  // branch: indices past the end are clamped and the values dropped)
-  const int e = routed ? sel[b * topk + k] : 0;
+  // branch: indices past the end are clamped and the values dropped); with the router,
+  // the expert id is the top-k of the gate's logits, computed by every wavefront while x
+  // is in flight
   uint4 xv[kUpXIt];
 #pragma unroll
   for (int i = 0; i < kUpXIt; ++i)
     xv[i] = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid + kUpThreads * i, NW - 1)];
+  int e;
+  if constexpr (ROUTE) {
+    int rsel[kMaxTopk];
+    float rgain[kMaxTopk];
+    route_topk(rt, b, E, topk, lane, rsel, rgain);
+    e = 0;
+    for (int i = 0; i < topk; ++i) e = (routed && i == k) ? rsel[i] : e;
+    if (blk == 0 && tid <= topk) {                     // one writer per token row
+      float gv = 1.0f;
+      int sv = 0;
+      for (int i = 0; i < topk; ++i) {
+        gv = i == tid ? rgain[i] : gv;
+        sv = i == tid ? rsel[i] : sv;
+      }
+      if (tid < topk) rt.sel_out[b * topk + tid] = sv;
+      rt.gains_out[b * (topk + 1) + tid] = gv;
+    }
+  } else {
+    e = routed ? sel[b * topk + k] : 0;
+  }
   const bool ok = !routed || (unsigned)e < (unsigned)E;
   const size_t row0 = routed ? (size_t)(ok ? e : 0) * F + f0 : (size_t)f0;
   const uint32_t* wb = routed ? w1 : sw1;
@@ -224,9 +308,38 @@ extern "C" int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, 
     return set_error(HSD_ERR_ALIGN, "%s: x, the weights, scales and biases must be 16-byte aligned", fn);
   if (B == 0) return HSD_OK;
   const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
-  hipLaunchKernelGGL(k_moe_up, grid, dim3(kUpThreads), 0, as_stream(stream),
+  hipLaunchKernelGGL(k_moe_up<false>, grid, dim3(kUpThreads), 0, as_stream(stream),
                      reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,
                      reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F,
-                     (int)FS, (int)topk, (int)E);
+                     (int)FS, (int)topk, (int)E, Router{});
+  return check_launch(fn);
+}
+
+extern "C" int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t* logits, const float* e_bias,
+                                      float routed_scale, int norm_topk, int32_t* sel, float* gains,
+                                      const uint32_t* w1, const uint16_t* s1, const uint16_t* b1,
+                                      const uint32_t* sw1, const uint16_t* ss1, const uint16_t* sb1, void* hcat,
+                                      int64_t B, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
+                                      uint64_t* live_masks, void* stream) {
+  const char* fn = "hsd_moe_route_up_relu2";
+  if (!x || !logits || !sel || !gains || !w1 || !s1 || !b1 || !sw1 || !ss1 || !sb1 || !hcat)
+    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (x_dtype != HSD_DT_BF16) return set_error(HSD_ERR_DTYPE, "%s: x must be bf16", fn);
+  if (B < 0 || topk <= 0 || topk > kMaxTopk || E < topk || E > 256 || D <= 0 || D % 64 || D > kUpMaxD || F <= 0 ||
+      F % 64 || FS <= 0 || FS % 64)
+    return set_error(HSD_ERR_SHAPE, "%s: need topk <= %d <= E <= 256, D %% 64 == 0, D <= %d, F and FS %% 64 == 0", fn,
+                     kMaxTopk, kUpMaxD);
+  if (B > 65535 || E * F * (D / 8) >= ((int64_t)1 << 40)) return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)w1 | (uintptr_t)sw1 | (uintptr_t)s1 | (uintptr_t)b1 |
+                       (uintptr_t)ss1 | (uintptr_t)sb1;
+  if (al & 15u)
+    return set_error(HSD_ERR_ALIGN, "%s: x, the weights, scales and biases must be 16-byte aligned", fn);
+  if (B == 0) return HSD_OK;
+  const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
+  Router rt{logits, e_bias, sel, gains, routed_scale, norm_topk};
+  hipLaunchKernelGGL(k_moe_up<true>, grid, dim3(kUpThreads), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(x), nullptr, w1, s1, b1, sw1, ss1, sb1,
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, (int)D, (int)F, (int)FS, (int)topk,
+                     (int)E, rt);
   return check_launch(fn);
 }

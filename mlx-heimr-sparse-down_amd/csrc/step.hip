@@ -1,0 +1,290 @@
+// The small kernels that tie a decode / verify step together on the device, so a whole
+// step is one captured graph with no host round trip (hsd/model.py:281-323 `step` /
+// `generate`, 333-356 `verify_step` / `rollback`, 366-443 `generate_mtp`):
+//   k_embed_q4       the quantised token embedding (mlx QuantizedEmbedding, model.py:223)
+//   k_pair_norm      concat(rms_norm(e, enorm), rms_norm(h, hnorm)): the MTP head's input
+//                    (mtp.py:81-83)
+//   k_decode_advance argmax of the last row + the sequence state after a plain step
+//   k_spec_accept    greedy acceptance of a verify step + the rollback of every cache
+//   k_mtp_chain      the inputs of the MTP head's chained call (mtp.py, model.py:408-414)
+//   k_draft          the verify ids [tok, drafts], optionally with scripted acceptance
+//
+// The sequence state is a device int32 array (HSD_SEQ_* indices in hsd.h): the attention
+// caches' length, the Mamba ring index, the count of emitted tokens, the last token, the
+// MTP head's cache length and pending-row count, ...
+#include "hsd_common.h"
+
+namespace hsd {
+namespace {
+
+// ---------------------------------------------------------------- embedding
+// out[b, i] = bf16(s[t, i/64] * q[t, i] + b[t, i/64]), t = tok[b] (one workgroup per row;
+// thread = 8 outputs = one word). A token outside [0, V) gives a zero row and the status
+// bit HSD_STATUS_BAD_TOKEN.
+__global__ __launch_bounds__(256) void k_embed_q4(const int32_t* __restrict__ tok, const uint32_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ s, const uint16_t* __restrict__ bq,
+                                                  int V, int D, uint16_t* __restrict__ out, int64_t out_ld,
+                                                  int32_t* __restrict__ status) {
+  const int b = blockIdx.x;
+  const int t = tok[b];
+  const bool ok = (unsigned)t < (unsigned)V;
+  const size_t row = ok ? (size_t)t : 0;
+  for (int wi = threadIdx.x; wi < D / 8; wi += blockDim.x) {
+    const uint32_t q = w[row * (D / 8) + wi];
+    const float sc = bf16_bits_to_f32(s[row * (D / 64) + wi / 8]);
+    const float bi = bf16_bits_to_f32(bq[row * (D / 64) + wi / 8]);
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c)) & 0xFu), bi)) : 0u;
+      const uint32_t hi = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c + 4)) & 0xFu), bi)) : 0u;
+      o[c] = lo | (hi << 16);
+    }
+    reinterpret_cast<uint4*>(out + (size_t)b * out_ld)[wi] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (!ok && threadIdx.x == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_TOKEN);
+}
+
+// ---------------------------------------------------------------- pair norm
+// out[b, :D] = rms_norm(e[b], w_e), out[b, D:] = rms_norm(h[b], w_h), each
+// bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w). One workgroup (256 threads) per row and half.
+__global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ e, int64_t e_ld,
+                                                   const uint16_t* __restrict__ h, int64_t h_ld,
+                                                   const uint16_t* __restrict__ we, const uint16_t* __restrict__ wh,
+                                                   float eps, int D, uint16_t* __restrict__ out, int64_t out_ld) {
+  __shared__ float wsum[4];
+  const int b = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const uint16_t* x = half ? h + (size_t)b * h_ld : e + (size_t)b * e_ld;
+  const uint16_t* w = half ? wh : we;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < D; i += 256) {
+    const float v = bf16_bits_to_f32(x[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum_dpp(ss);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  const float inv = __builtin_amdgcn_rsqf(tot / (float)D + eps);
+  uint16_t* o = out + (size_t)b * out_ld + half * D;
+  for (int i = threadIdx.x; i < D; i += 256) {
+    const float t = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(x[i]) * inv));
+    o[i] = f32_to_bf16_bits(t * bf16_bits_to_f32(w[i]));
+  }
+}
+
+// ---------------------------------------------------------------- argmax of keys
+// The best key of row b over `slots` per-workgroup keys (hsd_linear's HSD_Y_ARGMAX), by
+// one wavefront: the index (low 32 bits inverted) of the largest key.
+__device__ int wave_argmax_keys(const uint64_t* keys, int slots, int lane) {
+  uint64_t k = 0;
+  for (int i = lane; i < slots; i += 64) {
+    const uint64_t v = keys[i];
+    k = v > k ? v : k;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
+                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
+    k = o > k ? o : k;
+  }
+  return (int)~(uint32_t)k;
+}
+
+// A plain decode step's end: tok = argmax; out_tokens[n] = tok (if n < cap); n += 1;
+// pos += 1; cur = (cur + 1) % nslab. One wavefront.
+__global__ __launch_bounds__(64) void k_decode_advance(const uint64_t* __restrict__ keys, int slots,
+                                                       int32_t* __restrict__ seq, int32_t* __restrict__ out_tokens,
+                                                       int cap, int nslab) {
+  const int tok = wave_argmax_keys(keys, slots, threadIdx.x);
+  if (threadIdx.x == 0) {
+    const int n = seq[HSD_SEQ_N];
+    if (n < cap) out_tokens[n] = tok;
+    seq[HSD_SEQ_N] = n + 1;
+    seq[HSD_SEQ_TOK] = tok;
+    seq[HSD_SEQ_POS] += 1;
+    if (nslab > 0) seq[HSD_SEQ_CUR] = (seq[HSD_SEQ_CUR] + 1) % nslab;
+    seq[HSD_SEQ_STEPS] += 1;
+  }
+}
+
+// A verify step's end: tgt[r] = argmax of row r (r <= k); a = first i < k with
+// draft[i] != tgt[i], else k; the emitted tokens draft[:a] + [tgt[a]] go to out_tokens
+// at n (up to cap) and to pend[0..a] (the MTP head's next rows); n, pos and cur advance
+// by a + 1 (the rollback of the attention caches and of the Mamba rings); the head's
+// cache keeps the rows of its last first call (head_pos += R) and R = a + 1.
+// One workgroup of (k+1) wavefronts.
+__global__ __launch_bounds__(256) void k_spec_accept(const uint64_t* __restrict__ keys, int64_t key_ld, int slots,
+                                                     int k, const int32_t* __restrict__ ids,
+                                                     int32_t* __restrict__ seq, int32_t* __restrict__ out_tokens,
+                                                     int cap, int nslab, int32_t* __restrict__ pend,
+                                                     int32_t* __restrict__ tgt_out) {
+  __shared__ int tgt[8];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (w <= k) {
+    const int t = wave_argmax_keys(keys + (size_t)w * key_ld, slots, lane);
+    if (lane == 0) tgt[w] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int a = k;
+    for (int i = 0; i < k; ++i)
+      if (ids[1 + i] != tgt[i]) { a = i; break; }
+    const int n = seq[HSD_SEQ_N];
+    for (int i = 0; i <= a; ++i) {
+      const int tk = i < a ? ids[1 + i] : tgt[a];
+      if (n + i < cap) out_tokens[n + i] = tk;
+      if (pend) pend[i] = tk;
+    }
+    if (tgt_out)
+      for (int i = 0; i <= k; ++i) tgt_out[i] = tgt[i];
+    seq[HSD_SEQ_N] = n + a + 1;
+    seq[HSD_SEQ_TOK] = tgt[a];
+    seq[HSD_SEQ_POS] += a + 1;
+    if (nslab > 0) seq[HSD_SEQ_CUR] = (seq[HSD_SEQ_CUR] + a + 1) % nslab;
+    seq[HSD_SEQ_HEAD_POS] += seq[HSD_SEQ_R];
+    seq[HSD_SEQ_R] = a + 1;
+    seq[HSD_SEQ_ACCEPT] = a;
+    seq[HSD_SEQ_STEPS] += 1;
+    seq[HSD_SEQ_ACC_SUM] += a;
+  }
+}
+
+// The chained call's inputs: row R-1 of the first call (its prediction and its normed
+// hidden state), and that row's cache position head_pos + R.
+__global__ __launch_bounds__(256) void k_mtp_chain(const uint64_t* __restrict__ keys, int64_t key_ld, int slots,
+                                                   const uint16_t* __restrict__ hn, int64_t hn_ld, int D,
+                                                   int32_t* __restrict__ seq, int32_t* __restrict__ d1,
+                                                   uint16_t* __restrict__ h2) {
+  const int R = seq[HSD_SEQ_R];
+  const int r = min(max(R, 1), 3) - 1;
+  if (threadIdx.x < 64) {
+    const int t = wave_argmax_keys(keys + (size_t)r * key_ld, slots, threadIdx.x);
+    if (threadIdx.x == 0) {
+      d1[0] = t;
+      seq[HSD_SEQ_HEAD_POS2] = seq[HSD_SEQ_HEAD_POS] + r + 1;
+    }
+  }
+  for (int i = threadIdx.x; i < D; i += 256) h2[i] = hn[(size_t)r * hn_ld + i];
+}
+
+// The verify ids [tok, d_0 .. d_{k-1}]: d_0 = the chained call's input prediction, d_1
+// = the chained call's argmax (k = 2). With `script` (true tokens, indexed by the count
+// of emitted tokens) and `accepts` (one accepted-draft count per step), the drafts are
+// forced: d_i = true[n + i] for i < a_t, a guaranteed-wrong token at i = a_t.
+__global__ __launch_bounds__(64) void k_draft(const int32_t* __restrict__ d1, const uint64_t* __restrict__ keys2,
+                                              int slots, int k, int32_t* __restrict__ seq,
+                                              const int32_t* __restrict__ script, int script_len,
+                                              const int32_t* __restrict__ accepts, int n_accepts, int V,
+                                              int32_t* __restrict__ ids) {
+  int d2 = 0;
+  if (k >= 2 && keys2) d2 = wave_argmax_keys(keys2, slots, threadIdx.x);
+  if (threadIdx.x == 0) {
+    ids[0] = seq[HSD_SEQ_TOK];
+    int d[8];
+    d[0] = d1 ? d1[0] : 0;
+    if (k >= 2) d[1] = d2;
+    for (int i = 2; i < k; ++i) d[i] = 0;
+    if (script) {
+      const int n = seq[HSD_SEQ_N];
+      const int st = seq[HSD_SEQ_STEPS];
+      const int at = accepts ? accepts[min(st, n_accepts - 1)] : k;
+      for (int i = 0; i < k; ++i) {
+        const int tt = script[min(n + i, script_len - 1)];
+        d[i] = i < at ? tt : (i == at ? (tt + 1) % V : tt);
+      }
+    }
+    for (int i = 0; i < k; ++i) ids[1 + i] = d[i];
+  }
+}
+
+// seq[idx] += delta (host-known adjustments outside a graph, e.g. the head's prefill rows)
+__global__ void k_seq_add(int32_t* seq, int idx, int delta) {
+  if (threadIdx.x == 0) seq[idx] += delta;
+}
+
+}  // namespace
+}  // namespace hsd
+
+using namespace hsd;
+
+extern "C" int hsd_embed_q4(const int32_t* tok, int64_t B, const uint32_t* w, const uint16_t* scales,
+                            const uint16_t* biases, int64_t V, int64_t D, uint16_t* out, int64_t out_ld,
+                            int32_t* dev_status, void* stream) {
+  const char* fn = "hsd_embed_q4";
+  if (!tok || !w || !scales || !biases || !out) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (B < 0 || B > 65535 || V <= 0 || V > 0x7FFFFFFF || D <= 0 || D % 64 || out_ld < D || out_ld % 8)
+    return set_error(HSD_ERR_SHAPE, "%s: need D %% 64 == 0 and out_ld >= D, a multiple of 8", fn);
+  if ((uintptr_t)out & 15u) return set_error(HSD_ERR_ALIGN, "%s: out must be 16-byte aligned", fn);
+  if (B == 0) return HSD_OK;
+  hipLaunchKernelGGL(k_embed_q4, dim3((unsigned)B), dim3(256), 0, as_stream(stream), tok, w, scales, biases, (int)V,
+                     (int)D, out, out_ld, dev_status);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_pair_norm(const uint16_t* e, int64_t e_ld, const uint16_t* h, int64_t h_ld, const uint16_t* we,
+                             const uint16_t* wh, float eps, int64_t B, int64_t D, uint16_t* out, int64_t out_ld,
+                             void* stream) {
+  const char* fn = "hsd_pair_norm";
+  if (!e || !h || !we || !wh || !out) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (B < 0 || B > 65535 || D <= 0 || e_ld < D || h_ld < D || out_ld < 2 * D)
+    return set_error(HSD_ERR_SHAPE, "%s: row strides", fn);
+  if (B == 0) return HSD_OK;
+  hipLaunchKernelGGL(k_pair_norm, dim3((unsigned)(2 * B)), dim3(256), 0, as_stream(stream), e, e_ld, h, h_ld, we, wh,
+                     eps, (int)D, out, out_ld);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_decode_advance(const uint64_t* argmax_keys, int64_t slots, int32_t* seq, int32_t* out_tokens,
+                                  int64_t cap, int64_t nslab, void* stream) {
+  const char* fn = "hsd_decode_advance";
+  if (!argmax_keys || !seq || (cap > 0 && !out_tokens)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (slots <= 0 || slots > (1 << 30) || cap < 0 || cap > 0x7FFFFFFF || nslab < 0 || nslab > 64)
+    return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  hipLaunchKernelGGL(k_decode_advance, dim3(1), dim3(64), 0, as_stream(stream), argmax_keys, (int)slots, seq,
+                     out_tokens, (int)cap, (int)nslab);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_spec_accept(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, int64_t k,
+                               const int32_t* ids, int32_t* seq, int32_t* out_tokens, int64_t cap, int64_t nslab,
+                               int32_t* pend, int32_t* tgt, void* stream) {
+  const char* fn = "hsd_spec_accept";
+  if (!argmax_keys || !ids || !seq || (cap > 0 && !out_tokens)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (k < 1 || k > 3 || slots <= 0 || slots > key_ld || cap < 0 || cap > 0x7FFFFFFF || nslab < 0 || nslab > 64 ||
+      (nslab > 0 && nslab < k + 2))
+    return set_error(HSD_ERR_SHAPE, "%s: need 1 <= k <= 3, slots <= key_ld, nslab 0 or >= k + 2", fn);
+  hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(256), 0, as_stream(stream), argmax_keys, key_ld, (int)slots, (int)k,
+                     ids, seq, out_tokens, (int)cap, (int)nslab, pend, tgt);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_mtp_chain(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, const uint16_t* hn,
+                             int64_t hn_ld, int64_t D, int32_t* seq, int32_t* d1, uint16_t* h2, void* stream) {
+  const char* fn = "hsd_mtp_chain";
+  if (!argmax_keys || !hn || !seq || !d1 || !h2) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (slots <= 0 || slots > key_ld || D <= 0 || hn_ld < D) return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  hipLaunchKernelGGL(k_mtp_chain, dim3(1), dim3(256), 0, as_stream(stream), argmax_keys, key_ld, (int)slots, hn,
+                     hn_ld, (int)D, seq, d1, h2);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_draft_ids(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots, int64_t k, int32_t* seq,
+                             const int32_t* script, int64_t script_len, const int32_t* accepts, int64_t n_accepts,
+                             int64_t V, int32_t* ids, void* stream) {
+  const char* fn = "hsd_draft_ids";
+  if (!seq || !ids || (k >= 2 && !script && !argmax_keys2)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (k < 1 || k > 7 || V <= 0 || (script && script_len <= 0) || (accepts && n_accepts <= 0) ||
+      (argmax_keys2 && slots <= 0))
+    return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  hipLaunchKernelGGL(k_draft, dim3(1), dim3(64), 0, as_stream(stream), d1, argmax_keys2, (int)slots, (int)k, seq,
+                     script, (int)script_len, accepts, (int)n_accepts, (int)V, ids);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_seq_add(int32_t* seq, int64_t idx, int64_t delta, void* stream) {
+  if (!seq) return set_error(HSD_ERR_ARG, "hsd_seq_add: null pointer");
+  if (idx < 0 || idx >= HSD_SEQ_LEN) return set_error(HSD_ERR_SHAPE, "hsd_seq_add: bad index");
+  hipLaunchKernelGGL(k_seq_add, dim3(1), dim3(64), 0, as_stream(stream), seq, (int)idx, (int)delta);
+  return check_launch("hsd_seq_add");
+}

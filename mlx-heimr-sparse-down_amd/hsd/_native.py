@@ -16,7 +16,13 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("HSD_LIB") or os.path.join(_PKG_ROOT, "libhsd.so")
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
-STATUS_BAD_EXPERT = 1
+STATUS_BAD_EXPERT, STATUS_BAD_STATE, STATUS_BAD_TOKEN = 1, 2, 4
+X_BF16, X_RMS, X_GATED = 0, 1, 2
+W_Q4, W_BF16 = 0, 1
+Y_BF16, Y_F32, Y_RESID, Y_ARGMAX = 0, 1, 2, 3
+# sequence state indices (include/hsd.h HSD_SEQ_*)
+SEQ_POS, SEQ_CUR, SEQ_N, SEQ_TOK, SEQ_HEAD_POS, SEQ_R, SEQ_HEAD_POS2, SEQ_ACCEPT, SEQ_STEPS, SEQ_ACC_SUM = range(10)
+SEQ_LEN = 16
 
 _c_int, _c_i64, _c_size, _c_float, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p
 
@@ -43,11 +49,31 @@ _SIGS = {
     "hsd_prefill_gemm": (_c_int, [_vp] * 14 + [_c_int] + [_c_i64] * 9 + [_vp, _c_size, _vp]),
     "hsd_mamba_workspace_bytes": (_c_size, [_c_i64] * 3),
     "hsd_mamba_verify": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64] + [_vp] * 9 + [_c_i64, _vp, _c_int]
-                         + [_c_i64] * 6 + [_c_float] * 3 + [_vp, _c_size, _vp]),
-    "hsd_mamba_select_row": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+                         + [_c_i64] * 6 + [_c_float] * 3 + [_vp, _vp, _c_size, _vp]),
+    "hsd_mamba_ssm": (_c_int, [_vp, _c_i64, _vp, _c_i64] + [_vp] * 8 + [_c_i64, _vp] + [_c_i64] * 5
+                      + [_c_float] * 2 + [_vp, _vp]),
+    "hsd_mamba_select_row": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "hsd_greedy_accept": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
     "hsd_moe_up_relu2": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
                          + [_c_i64] * 6 + [_vp, _vp, _vp]),
+    "hsd_moe_route_up_relu2": (_c_int, [_vp, _c_int, _vp, _vp, _c_float, _c_int, _vp, _vp] + [_vp] * 7
+                               + [_c_i64] * 6 + [_vp, _vp]),
+    "hsd_sparse_down_residual": (_c_int, [_vp, _c_int] + [_vp] * 10 + [_c_i64] * 6 + [_c_int, _vp, _vp, _vp,
+                                                                                      _c_size, _vp]),
+    "hsd_linear_argmax_slots": (_c_i64, [_c_i64, _c_int]),
+    "hsd_linear": (_c_int, [_vp, _c_i64, _c_int, _vp, _c_i64, _vp, _c_float, _vp, _vp, _vp, _c_int, _vp, _c_i64,
+                            _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
+    "hsd_argmax_keys": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
+    "hsd_attn_workspace_bytes": (_c_size, [_c_i64] * 3),
+    "hsd_attn_decode": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_float, _vp, _vp, _c_size, _vp]),
+    "hsd_embed_q4": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
+    "hsd_pair_norm": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_float, _c_i64, _c_i64, _vp, _c_i64, _vp]),
+    "hsd_decode_advance": (_c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp]),
+    "hsd_spec_accept": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "hsd_mtp_chain": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+    "hsd_draft_ids": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp]),
+    "hsd_seq_add": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
 }
 
 EXPORTS = tuple(_SIGS)

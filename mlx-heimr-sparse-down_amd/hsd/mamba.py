@@ -81,10 +81,12 @@ class MambaCache:
         return self.conv[c], self.ssm[c]
 
 
-def verify_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out_dtype=torch.bfloat16, workspace=None):
+def verify_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out_dtype=torch.bfloat16, workspace=None,
+                status=None):
     """The fused conv + SSM + gated-norm update of L rows from the in_proj output
     proj [L, 2*H*P + 2*G*N + H] (gate | conv input | dt, mamba.py:27), writing the per-row
-    checkpoints. -> y [L, H*P] (the gated RMSNorm output that out_proj consumes)."""
+    checkpoints. -> y [L, H*P] (the gated RMSNorm output that out_proj consumes).
+    status: optional int32 [1], ORed with 2 when the ring index is corrupt (y is then NaN)."""
     if proj.dtype != torch.bfloat16:
         raise N.HSDError("the Mamba-2 verify takes the bf16 in_proj output")
     proj = N.contig(proj)
@@ -108,7 +110,32 @@ def verify_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out_dtype=torch.bfl
            N.ptr(N.contig(mixer.dt_bias)), N.ptr(N.contig(mixer.D)), N.ptr(N.contig(mixer.norm_w)),
            N.ptr(cache.ssm), N.ptr(cache.conv), N.ptr(cache.cur), cache.nslab, N.ptr(y),
            N.dtype_tag(out_dtype), L, H, P, Nst, G, mixer.norm_group, float(mixer.eps), float(lo),
-           float(hi), N.ptr(ws), ws.numel(), N.stream(proj.device))
+           float(hi), N.ptr(status), N.ptr(ws), ws.numel(), N.stream(proj.device))
+    return y
+
+
+def ssm_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out=None, status=None):
+    """The conv + SSM update of L rows from the in_proj output proj [L, 2*H*P + 2*G*N + H]
+    (gate | conv input | dt) with the per-row checkpoints written, without the gated norm:
+    -> y [L, H*P] f32 (sum_n S C + D x), which out_proj consumes through nn.linear's gated
+    norm prologue (with the gate columns of proj)."""
+    if proj.dtype != torch.bfloat16:
+        raise N.HSDError("the Mamba-2 update takes the bf16 in_proj output")
+    L = proj.shape[0]
+    H, P, Nst, G = mixer.num_heads, mixer.head_dim, mixer.ssm_state_size, mixer.n_groups
+    DI, CD = mixer.intermediate_size, mixer.conv_dim
+    if proj.shape[1] < DI + CD + H or proj.stride(1) != 1:
+        raise N.HSDError(f"proj needs {DI + CD + H} unit-stride columns")
+    y = out if out is not None else torch.empty((L, DI), dtype=torch.float32, device=proj.device)
+    es = proj.element_size()
+    import ctypes
+    conv_p = ctypes.c_void_p(proj.data_ptr() + DI * es)
+    dt_p = ctypes.c_void_p(proj.data_ptr() + (DI + CD) * es)
+    lo, hi = mixer.time_step_limit
+    N.call("hsd_mamba_ssm", conv_p, proj.stride(0), dt_p, proj.stride(0), N.ptr(N.contig(mixer.conv_w)),
+           N.ptr(N.contig(mixer.conv_b)), N.ptr(N.contig(mixer.A_log)), N.ptr(N.contig(mixer.dt_bias)),
+           N.ptr(N.contig(mixer.D)), N.ptr(cache.ssm), N.ptr(cache.conv), N.ptr(cache.cur), cache.nslab, N.ptr(y), L,
+           H, P, Nst, G, float(lo), float(hi), N.ptr(status), N.stream(proj.device))
     return y
 
 
@@ -128,11 +155,12 @@ def mamba_verify(block, x3, cache, records):
     return y[None]
 
 
-def mamba_rollback(records, n_keep, n_keep_dev=None):
+def mamba_rollback(records, n_keep, n_keep_dev=None, status=None):
     """hsd/mamba.py:47-56. After mamba_verify on L rows, put every cache in `records` at
     the state after its first n_keep rows: cur += n_keep on the device. A `cur` shared by
     several caches is moved once. n_keep_dev (a device int32 [1], e.g. from
-    hsd.mtp.greedy_accept) overrides the host n_keep."""
+    hsd.mtp.greedy_accept) overrides the host n_keep; a device value outside [0, L] leaves
+    the caches where they are and ORs 2 into `status` (optional int32 [1])."""
     seen = set()
     for cache, L in records:
         if id(cache.cur) in seen:
@@ -141,4 +169,5 @@ def mamba_rollback(records, n_keep, n_keep_dev=None):
         if n_keep_dev is None and not 0 <= n_keep <= L:
             raise N.HSDError(f"n_keep {n_keep} outside [0, {L}]")
         N.call("hsd_mamba_select_row", N.ptr(cache.cur), N.ptr(n_keep_dev),
-               0 if n_keep_dev is not None else int(n_keep), cache.nslab, N.stream(cache.cur.device))
+               0 if n_keep_dev is not None else int(n_keep), L, cache.nslab, N.ptr(status),
+               N.stream(cache.cur.device))

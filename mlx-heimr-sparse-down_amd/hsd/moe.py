@@ -150,6 +150,31 @@ def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, statu
     return hcat
 
 
+def route_up_relu2(x, logits, e_bias, w1, s1, b1, sw1, ss1, sb1, *, topk, routed_scale=1.0, norm_topk=True,
+                   live_masks=None, out=None):
+    """The MoE front end WITH the router (model.py:110-121 from `mix.gate` on): from the
+    gate's logits [B, E] bf16 (nn.linear of the normed token with the bf16 gate weight)
+    the top-k experts (sigmoid scores plus the selection bias e_bias [E] f32, descending,
+    equal choices by expert id), their gains (normalised and scaled), then hcat as
+    up_relu2. -> (hcat [B, topk*F + FS] bf16, sel [B, topk] int32, gains [B, topk+1] f32)."""
+    if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
+        raise N.HSDError("route_up_relu2 takes bf16 activations and logits")
+    x = N.contig(x)
+    logits = N.contig(logits)
+    B, D = x.shape
+    E, F = w1.shape[0], w1.shape[1]
+    FS = sw1.shape[0]
+    NR = topk * F + FS
+    hcat = out if out is not None else torch.empty((B, NR), dtype=torch.bfloat16, device=x.device)
+    sel = torch.empty((B, topk), dtype=torch.int32, device=x.device)
+    gains = torch.empty((B, topk + 1), dtype=torch.float32, device=x.device)
+    N.call("hsd_moe_route_up_relu2", N.ptr(x), N.DT_BF16, N.ptr(logits), N.ptr(e_bias), float(routed_scale),
+           1 if norm_topk else 0, N.ptr(sel), N.ptr(gains), N.ptr(N.as_words(N.contig(w1))), N.ptr(N.contig(s1)),
+           N.ptr(N.contig(b1)), N.ptr(N.as_words(N.contig(sw1))), N.ptr(N.contig(ss1)), N.ptr(N.contig(sb1)),
+           N.ptr(hcat), B, D, F, FS, topk, E, N.ptr(live_masks), N.stream(x.device))
+    return hcat, sel, gains
+
+
 def build_layouts(blocks, single_layout=True):
     """NemotronModel.set_mode("sparse") (model.py:233-247): every block's neuron-major
     layout, one layer at a time, so the permutation's transient stays one layer's size

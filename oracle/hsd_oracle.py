@@ -340,7 +340,7 @@ def mamba_verify(conv_in, dt_raw, gate, conv_w, conv_b, A_log, dt_bias, Dp, norm
       co = silu(sum_j conv_w[:, j] * window_r[j] + conv_b)                  (mamba.py:32)
       x, B, C = split(co, [H*P, H*P + G*N])                                 (mamba.py:33-37)
       dt = clip(softplus(dt_raw + dt_bias), lo, hi); dA = exp(-exp(A_log) * dt)
-      S <- dA * S + (x * dt) B^T ;  y = S C + D x                           (mamba.py:38-41)
+      S <- dA * S + (x * dt) B^T ;  y = S C + bf16(D) x                     (mamba.py:38-41)
       out = rmsnorm_{groups of 512}(y * silu(gate)) * norm_w                (mamba.py:43)
     Inputs are float arrays (bf16 values); returns dict with y [L, H*P] (normed, f32),
     y_pre [L, H*P] (before the gate/norm), conv_states [L, 3, CD] (after each row) and
@@ -356,6 +356,9 @@ def mamba_verify(conv_in, dt_raw, gate, conv_w, conv_b, A_log, dt_bias, Dp, norm
     W = np.asarray(conv_w, dtype=np.float64)
     S = np.asarray(ssm_state, dtype=np.float64).copy()
     A = -np.exp(np.asarray(A_log, dtype=np.float64))
+    # D enters ssm_update rounded to the activations' dtype, bf16 (m.D.astype(hs4.dtype),
+    # mamba.py:38)
+    Dr = round_bf16(np.asarray(Dp, dtype=np.float32)).astype(np.float64)
     out = dict(y=np.zeros((L, DI), np.float32), y_pre=np.zeros((L, DI), np.float32),
                conv_states=np.zeros((L, 3, CD), np.float32),
                ssm_states=np.zeros((L, H, P, Nst), np.float32))
@@ -370,7 +373,7 @@ def mamba_verify(conv_in, dt_raw, gate, conv_w, conv_b, A_log, dt_bias, Dp, norm
         Bh = np.repeat(Bm, hpg, axis=0)                                # [H, N]
         Ch = np.repeat(Cm, hpg, axis=0)
         S = dA[:, None, None] * S + (x * dt[:, None])[:, :, None] * Bh[:, None, :]
-        y = np.einsum("hpn,hn->hp", S, Ch) + np.asarray(Dp, dtype=np.float64)[:, None] * x
+        y = np.einsum("hpn,hn->hp", S, Ch) + Dr[:, None] * x
         z = y.reshape(-1) * silu(np.asarray(gate[r], dtype=np.float64))
         zg = z.reshape(-1, norm_group)
         zn = zg / np.sqrt((zg * zg).mean(axis=1, keepdims=True) + eps)
@@ -405,6 +408,110 @@ def greedy_accept(draft, tgt):
     return a, [int(t) for t in draft[:a]] + [int(tgt[a])], a + 1
 
 
+# ------------------------------------------- the rest of a decode step (end to end)
+def rms_norm_bf16(x, w, eps=1e-5):
+    """mx.fast.rms_norm(x, w, eps) on bf16 (the block pre-norms, model.py:114, mamba.py:25;
+    the MTP head's norms, mtp.py:81-86): t = bf16(x / sqrt(mean(x^2) + eps)), out =
+    bf16(t * w). x, w bf16 values (float arrays) over the last axis -> bf16 bits."""
+    x = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    t = round_bf16((x * inv).astype(np.float32)).astype(np.float64)
+    return f32_to_bf16((t * np.asarray(w, dtype=np.float64)).astype(np.float32))
+
+
+def gated_rms_norm_bf16(y, gate, w, eps=1e-5, group=512):
+    """The Mamba-2 gated RMSNorm in front of out_proj (mamba.py:43, mlx-lm's
+    MambaRMSNormGated): z = y * silu(gate); per group of `group` elements t = bf16(z /
+    sqrt(mean(z^2) + eps)); out = bf16(t * w). -> bf16 bits."""
+    z = np.asarray(y, dtype=np.float64) * silu(np.asarray(gate, dtype=np.float64))
+    shp = z.shape
+    zg = z.reshape(*shp[:-1], shp[-1] // group, group)
+    inv = 1.0 / np.sqrt((zg * zg).mean(axis=-1, keepdims=True) + eps)
+    t = round_bf16((zg * inv).reshape(shp).astype(np.float32)).astype(np.float64)
+    return f32_to_bf16((t * np.asarray(w, dtype=np.float64)).astype(np.float32))
+
+
+def linear_q4(x, w, s, b):
+    """mlx quantized_matmul(x, w, s, b, transpose=True) in float64: x [B, I] values, w
+    [O, I/8] u32, s/b [O, I/64] bf16 bits -> [B, O]."""
+    return up_proj_f64(x, w, s, b)
+
+
+def linear_bf16(x, w_bits):
+    """x @ W.T with W [O, I] bf16 bits, float64."""
+    return np.asarray(x, dtype=np.float64) @ bf16_to_f32(w_bits).astype(np.float64).T
+
+
+def argmax_bf16(y):
+    """mx.argmax of bf16 outputs (lm_head then argmax, model.py:302, 419): the first index
+    of the largest bf16-rounded value; NaN beats every number."""
+    v = round_bf16(np.asarray(y, dtype=np.float32))
+    v = np.atleast_2d(v)
+    out = np.empty(v.shape[0], dtype=np.int32)
+    for r in range(v.shape[0]):
+        nan = np.flatnonzero(np.isnan(v[r]))
+        out[r] = nan[0] if nan.size else int(np.argmax(v[r]))
+    return out
+
+
+def embed_q4(tok, w, s, b):
+    """The quantised embedding (model.py:223-224): row tok of W = s q + b, the exact value
+    rounded to fp32 then to bf16. -> [B, D] bf16 bits; a token outside [0, V) gives 0."""
+    V = w.shape[0]
+    D = w.shape[1] * 8
+    out = np.zeros((len(tok), D), dtype=np.uint16)
+    for i, t in enumerate(tok):
+        if 0 <= int(t) < V:
+            out[i] = f32_to_bf16(dequantize(w[int(t)], s[int(t)], b[int(t)]).astype(np.float32))
+    return out
+
+
+def attention(q, k, v, scale):
+    """Scaled dot-product attention of one query row over its visible keys, per query
+    head (float64): q [HQ, HD], k/v [HKV, S, HD] -> [HQ, HD]; query head h uses kv head
+    h // (HQ // HKV). The reference's block calls mx.fast.scaled_dot_product_attention
+    (mlx-lm NemotronH attention, model.py:287, 343)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    HQ, HKV = q.shape[0], k.shape[0]
+    out = np.zeros_like(q)
+    for h in range(HQ):
+        g = h // (HQ // HKV)
+        sc = (k[g] @ q[h]) * scale
+        p = np.exp(sc - sc.max())
+        out[h] = (p / p.sum()) @ v[g]
+    return out
+
+
+def sigmoid_f32(x):
+    """1 / (1 + exp(-x)) in float32 arithmetic."""
+    x = np.asarray(x, dtype=np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x, dtype=np.float32))).astype(np.float32)
+
+
+def router_topk(logits, bias, topk, scale=1.0, norm_topk=True):
+    """The MoE router of the Nemotron-H family as mlx-lm runs it after `x @ gate.T`
+    (model.py:115; restated from the family's published gate: sigmoid scores, a selection
+    bias, top-k, normalised and scaled weights): score = sigmoid(logit) (fp32), choice =
+    score + bias; sel = the topk largest choices in descending order, equal choices by
+    the smaller expert id (mlx's argpartition leaves the order open: parity unpinned);
+    gain = score / (sum of the selected scores + 1e-20) * scale (norm_topk) or score *
+    scale. logits [B, E] float (bf16 values) -> (sel [B, topk] int32, gains [B, topk])."""
+    lg = np.atleast_2d(np.asarray(logits, dtype=np.float32))
+    B, E = lg.shape
+    sc = sigmoid_f32(lg)
+    ch = (sc + (np.zeros(E, np.float32) if bias is None else np.asarray(bias, np.float32))).astype(np.float32)
+    sel = np.zeros((B, topk), dtype=np.int32)
+    gains = np.zeros((B, topk), dtype=np.float64)
+    for r in range(B):
+        order = sorted(range(E), key=lambda e: (-float(ch[r, e]), e))[:topk]
+        sel[r] = order
+        sv = sc[r, order].astype(np.float64)
+        gains[r] = sv / (sv.sum() + 1e-20) * scale if norm_topk else sv * scale
+    return sel, gains
+
+
 PINNING = {
     "up_proj_f64": "brute force on tiny shapes (scalar loops over words and nibbles); the nibble order "
                    "is unpack_nibbles', pinned with the layout",
@@ -426,4 +533,16 @@ PINNING = {
                     "mlx-lm ssm_update's time_step_limit default and intermediate precisions: "
                     "parity unpinned (mlx-lm is not available here)",
     "greedy_accept": "brute force over all draft/target combinations",
+    "rms_norm_bf16": "closed forms: a constant-magnitude row normalises to +-w exactly; scale invariance "
+                     "under powers of two (eps = 0); a hand-computed known answer",
+    "gated_rms_norm_bf16": "closed form: a group of constant |y| and constant gate gives +-w whatever "
+                           "silu's value; groups are independent",
+    "linear_q4": "brute force on tiny shapes (scalar loops over words and nibbles)",
+    "argmax_bf16": "ties to the first index, NaN first, bf16 rounding ties; brute force",
+    "embed_q4": "closed form: one dequantised row, exactly representable values round trip",
+    "attention": "closed forms: one visible key returns its value row; equal keys average the value "
+                 "rows; a dominant key selects its value row; GQA head grouping",
+    "router_topk": "brute force over every subset of size topk on small E; normalised gains sum to the "
+                   "scale; order and tie rule by construction. The gate's exact form in mlx-lm 0.31.3 "
+                   "(nemotron_h) is not in the container: parity unpinned against it",
 }

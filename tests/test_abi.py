@@ -66,8 +66,9 @@ def test_argument_errors_are_reported():
         assert lib.hsd_moe_up_relu2(dummy, 0, dummy, dummy, sc[0], sc[1], dummy, sc[2], sc[3], dummy,
                                     1, 2688, 1856, 3712, 6, 128, None, None, None) == -4
     assert lib.hsd_mamba_verify(*([dummy, 10304] * 3), *([dummy] * 9), 4, dummy, 0,
-                                3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, dummy, 1 << 20, None) == -2  # N != 128
-    assert lib.hsd_mamba_select_row(dummy, None, 4, 4, None) == -1                 # n_keep >= nslab
+                                3, 64, 64, 64, 8, 512, 1e-5, 0.0, 1e30, None, dummy, 1 << 20, None) == -2  # N != 128
+    assert lib.hsd_mamba_select_row(dummy, None, 4, 3, 4, None, None) == -1       # n_keep > L
+    assert lib.hsd_mamba_select_row(dummy, None, 1, 4, 4, None, None) == -2       # L >= nslab
     assert lib.hsd_prefill_gemm(*([dummy] * 14), 0, 512, 2688, 1856, 3712, 6, 128, 48, 240, 3712,
                                 dummy, 1 << 30, None) == -2                          # tt = 48
     assert lib.hsd_prefill_gemm(*([dummy] * 14), 0, 512, 2688, 1856, 4096, 6, 128, 32, 240, 4096,

@@ -1,0 +1,172 @@
+"""GPU parity of hsd_linear -- the projections of a decode step (mlx quantized_matmul with
+transpose=True: Mamba in/out_proj, attention q/k/v/o, lm_head; bf16 router gate and MTP
+eh_proj) with the fused rms_norm / gated-norm prologues and the residual / argmax
+epilogues.
+
+Bars:
+* the fused norms (xn_out) equal the oracle's bf16 within one bf16 ulp, and at least
+  99 % of the elements are bit-identical;
+* y against the float64 oracle applied to the kernel's own xn: max|y - ref| <= 1e-4 *
+  max|ref| (fp32 accumulation over up to 6144 inputs); bf16 outputs within the north-star
+  bound |y - ref| <= 2e-2 + 1e-2 |ref|;
+* bit-exact: every row of a B-row call equals that row alone; the bf16, residual and
+  argmax epilogues equal bf16(f32 output), bf16(res + bf16(y)) and the first argmax of
+  the bf16 outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from hsd import nn, synth as S
+from oracle import hsd_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def q4_weight(seed, O_, I, dev, scale=None):
+    rng = np.random.default_rng(seed)
+    w, s, b = S.down_proj_np(rng, (), O_, I)
+    if scale is not None:
+        s = O.f32_to_bf16(O.bf16_to_f32(s) * scale)
+        b = O.f32_to_bf16(O.bf16_to_f32(b) * scale)
+    return (w, s, b), nn.QWeight(S.to_device(w, dev), S.to_device(s, dev), S.to_device(b, dev))
+
+
+def bf16_rows(rng, B, I, dev, scale=1.0):
+    x = O.f32_to_bf16(rng.standard_normal((B, I)).astype(np.float32) * scale)
+    return x, S.to_device(x, dev)
+
+
+def ulp_close(a_bits, b_bits):
+    """Element-wise |a - b| <= 1 bf16 ulp, and the fraction of bit-identical elements."""
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    sa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+    sb = np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    return np.all(np.abs(sa - sb) <= 1), float(np.mean(a == b))
+
+
+@pytest.mark.parametrize("I,O_", [(2688, 2688), (4096, 1024), (2688, 10304)])
+def test_rms_linear_matches_oracle(dev, I, O_):
+    (w, s, b), W = q4_weight(10 + I, O_, I, dev)
+    rng = np.random.default_rng(20)
+    nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))
+    x, xd = bf16_rows(rng, 3, I, dev, 2.0)
+    xn = torch.empty((3, I), dtype=torch.bfloat16, device=dev)
+    y = nn.linear(xd, W, norm=S.to_device(nw, dev), eps=1e-5, out_dtype=torch.float32, xn_out=xn)
+    xn_h = S.to_host(xn)
+    ok, same = ulp_close(xn_h, O.rms_norm_bf16(O.bf16_to_f32(x), O.bf16_to_f32(nw), 1e-5))
+    print(f"I={I} O={O_}: xn within 1 ulp {ok}, identical {same:.4f}")
+    assert ok and same >= 0.99
+    ref = O.linear_q4(O.bf16_to_f32(xn_h), w, s, b)
+    yh = y.cpu().numpy()
+    scale = np.abs(ref).max()
+    print(f"  max rel err {np.abs(yh - ref).max() / scale:.2e}")
+    assert np.abs(yh - ref).max() <= 1e-4 * scale
+
+
+def test_rows_are_independent_and_epilogues_agree(dev):
+    I, O_ = 2688, 4608
+    (w, s, b), W = q4_weight(31, O_, I, dev)
+    rng = np.random.default_rng(32)
+    nw = S.to_device(O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32)), dev)
+    _, xd = bf16_rows(rng, 4, I, dev)
+    y4 = nn.linear(xd, W, norm=nw, out_dtype=torch.float32)
+    for r in range(4):
+        y1 = nn.linear(xd[r:r + 1], W, norm=nw, out_dtype=torch.float32)
+        assert torch.equal(y1.view(torch.int32), y4[r:r + 1].view(torch.int32)), f"row {r}"
+    y3 = nn.linear(xd[:3], W, norm=nw, out_dtype=torch.float32)
+    assert torch.equal(y3.view(torch.int32), y4[:3].view(torch.int32))
+    yb = nn.linear(xd, W, norm=nw)                                      # bf16 epilogue
+    assert torch.equal(yb.view(torch.int16), y4.to(torch.bfloat16).view(torch.int16))
+    # argmax epilogue: the first index of the largest bf16 output, per row
+    slots = nn.argmax_slots(O_)
+    keys = torch.empty((4, slots), dtype=torch.int64, device=dev)
+    logits = torch.empty((4, O_), dtype=torch.bfloat16, device=dev)
+    nn.linear(xd, W, norm=nw, argmax_keys=keys, out=logits)
+    tok = nn.argmax(keys).cpu().numpy()
+    assert torch.equal(logits.view(torch.int16), yb.view(torch.int16))
+    assert tok.tolist() == O.argmax_bf16(yb.float().cpu().numpy()).tolist()
+
+
+def test_residual_epilogue(dev):
+    I, O_ = 4096, 2688
+    (w, s, b), W = q4_weight(41, O_, I, dev)
+    rng = np.random.default_rng(42)
+    x, xd = bf16_rows(rng, 3, I, dev)
+    res = S.to_device(O.f32_to_bf16(rng.standard_normal((3, O_)).astype(np.float32) * 4), dev)
+    y = nn.linear(xd, W)                                                 # plain bf16 x, bf16 y
+    ref = O.linear_q4(O.bf16_to_f32(x), w, s, b)
+    assert np.all(np.abs(y.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+    out = res.clone()
+    nn.linear(xd, W, residual=out, out=out)                              # in place, as the model does
+    want = (res.float() + y.float()).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_gated_norm_prologue(dev):
+    I, O_ = 4096, 2688
+    (w, s, b), W = q4_weight(51, O_, I, dev)
+    rng = np.random.default_rng(52)
+    y_pre = rng.standard_normal((2, I)).astype(np.float32) * 3
+    gate = O.f32_to_bf16(rng.standard_normal((2, I)).astype(np.float32))
+    gate_buf = torch.zeros((2, I + 64), dtype=torch.bfloat16, device=dev)  # a strided gate, as in_proj's
+    gate_buf[:, 64:] = S.to_device(gate, dev)
+    nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))
+    res = torch.zeros((2, O_), dtype=torch.bfloat16, device=dev)
+    xn = torch.empty((2, I), dtype=torch.bfloat16, device=dev)
+    # the gated norm is instantiated with the residual epilogue only (out_proj)
+    out = nn.linear(torch.from_numpy(y_pre).to(dev), W, norm=S.to_device(nw, dev), gate=gate_buf[:, 64:],
+                    residual=res, xn_out=xn)
+    xn_h = S.to_host(xn)
+    ok, same = ulp_close(xn_h, O.gated_rms_norm_bf16(y_pre, O.bf16_to_f32(gate), O.bf16_to_f32(nw), 1e-5))
+    print(f"gated norm: within 1 ulp {ok}, identical {same:.4f}")
+    assert ok and same >= 0.99
+    ref = O.linear_q4(O.bf16_to_f32(xn_h), w, s, b)
+    assert np.all(np.abs(out.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+
+
+@pytest.mark.parametrize("I,O_,B", [(2688, 128, 1), (2688, 128, 3), (5376, 2688, 3)])
+def test_bf16_weights(dev, I, O_, B):
+    rng = np.random.default_rng(60 + I + B)
+    wb = O.f32_to_bf16((rng.standard_normal((O_, I)) * 0.02).astype(np.float32))
+    W = nn.QWeight(S.to_device(wb, dev))
+    x, xd = bf16_rows(rng, B, I, dev)
+    y = nn.linear(xd, W)
+    ref = O.linear_bf16(O.bf16_to_f32(x), wb)
+    assert np.all(np.abs(y.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+    if I == 2688:                                                        # the router: rms prologue
+        nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))
+        xn = torch.empty((B, I), dtype=torch.bfloat16, device=dev)
+        y = nn.linear(xd, W, norm=S.to_device(nw, dev), xn_out=xn)
+        ref = O.linear_bf16(O.bf16_to_f32(S.to_host(xn)), wb)
+        assert np.all(np.abs(y.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+        for r in range(B):
+            assert torch.equal(nn.linear(xd[r:r + 1], W, norm=S.to_device(nw, dev)).view(torch.int16),
+                               y[r:r + 1].view(torch.int16))
+
+
+def test_embed_rows(dev):
+    rng = np.random.default_rng(70)
+    V, D = 1000, 2688
+    w, s, b = S.down_proj_np(rng, (), V, D)
+    W = nn.QWeight(S.to_device(w, dev), S.to_device(s, dev), S.to_device(b, dev))
+    tok = np.array([0, 999, 17, 1000], dtype=np.int32)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = nn.embed(torch.from_numpy(tok).to(dev), W, status=status)
+    assert np.array_equal(S.to_host(out), O.embed_q4(tok, w, s, b))
+    assert int(status.item()) == 4                                       # token 1000 is outside [0, V)
+
+
+def test_pair_norm(dev):
+    rng = np.random.default_rng(80)
+    D = 2688
+    e, ed = bf16_rows(rng, 3, D, dev)
+    h, hd = bf16_rows(rng, 3, D, dev, 5.0)
+    we = O.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    wh = O.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    out = S.to_host(nn.pair_norm(ed, hd, S.to_device(we, dev), S.to_device(wh, dev)))
+    ref = np.concatenate([O.rms_norm_bf16(O.bf16_to_f32(e), O.bf16_to_f32(we)),
+                          O.rms_norm_bf16(O.bf16_to_f32(h), O.bf16_to_f32(wh))], axis=1)
+    ok, same = ulp_close(out, ref)
+    assert ok and same >= 0.99

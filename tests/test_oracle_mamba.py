@@ -41,8 +41,9 @@ def test_conv_orientation_by_impulse():
             Bm = co[DI:DI + G * N].reshape(G, N)
             Cm = co[DI + G * N:].reshape(G, N)
             hpg = H // G
+            Dbf = O.round_bf16(np.float32(p["Dp"]))        # m.D.astype(bf16), mamba.py:38
             y = np.array([[dt[h] * x.reshape(H, P)[h, q] * (Bm[h // hpg] @ Cm[h // hpg]) +
-                           p["Dp"][h] * x.reshape(H, P)[h, q] for q in range(P)] for h in range(H)])
+                           Dbf[h] * x.reshape(H, P)[h, q] for q in range(P)] for h in range(H)])
             assert np.allclose(out["y_pre"][0], y.reshape(-1), rtol=1e-5, atol=1e-6)
     # conv state after each row = the last 3 rows of the padded input
     padded = np.concatenate([np.zeros((3, CD)), conv_in])
