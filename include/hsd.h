@@ -282,6 +282,22 @@ int hsd_draft_ids(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots
                   int32_t* seq, const int32_t* script, int64_t script_len, const int32_t* accepts,
                   int64_t n_accepts, int64_t V, int32_t* ids, void* stream);
 
+/* dst[i] = src[clamp(POS + offset + i, 0, n-1)] for i < count: the next rows of a prompt
+ * held on the device, so a prefill step (model.py:259-279, here in steps of a few rows)
+ * replays as one graph. */
+int hsd_gather_tokens(const int32_t* src, int64_t n, const int32_t* seq, int64_t offset, int64_t count,
+                      int32_t* dst, void* stream);
+
+/* The sequence state after a prefill step of B rows of a T-token prompt at POS (the
+ * chunk loop of model.py:265-279 and the MTP head's prefill hook, model.py:385-391):
+ * POS and CUR advance by min(B, T - POS); HEAD_POS by min(B, T - 1 - POS) (>= 0). */
+int hsd_prefill_advance(int32_t* seq, int64_t T, int64_t B, int64_t nslab, void* stream);
+
+/* Replaces NemotronModel.rollback (model.py:348-356) after a verify that advanced the
+ * state by B rows: POS -= n_drop (KVCache.trim) and CUR -= n_drop mod nslab (the
+ * checkpoint ring still holds the kept rows' state). n_drop = B - n_keep < nslab. */
+int hsd_seq_rollback(int32_t* seq, int64_t n_drop, int64_t nslab, void* stream);
+
 /* seq[idx] += delta on the stream (host-known adjustments, e.g. the head's prefill rows). */
 int hsd_seq_add(int32_t* seq, int64_t idx, int64_t delta, void* stream);
 

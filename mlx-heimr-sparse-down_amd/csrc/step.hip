@@ -198,6 +198,37 @@ __global__ __launch_bounds__(64) void k_draft(const int32_t* __restrict__ d1, co
   }
 }
 
+// dst[i] = src[clamp(POS + offset + i, 0, n - 1)]: the next rows' tokens of a prompt held
+// on the device (a prefill step replays as one graph).
+__global__ void k_gather_tokens(const int32_t* __restrict__ src, int n, const int32_t* __restrict__ seq,
+                                int offset, int count, int32_t* __restrict__ dst) {
+  const int i = threadIdx.x;
+  if (i < count) dst[i] = src[min(max(seq[HSD_SEQ_POS] + offset + i, 0), n - 1)];
+}
+
+// The state after a prefill step of B rows at POS of a T-token prompt: the rows up to the
+// prompt's end are kept (POS and CUR advance by min(B, T - POS)); the MTP head keeps the
+// rows whose next token is a prompt token (HEAD_POS += min(B, T - 1 - POS), >= 0).
+__global__ void k_prefill_advance(int32_t* seq, int T, int B, int nslab) {
+  if (threadIdx.x == 0) {
+    const int p = seq[HSD_SEQ_POS];
+    const int valid = min(max(T - p, 0), B);
+    const int head = min(max(T - 1 - p, 0), B);
+    seq[HSD_SEQ_POS] = p + valid;
+    if (nslab > 0) seq[HSD_SEQ_CUR] = (seq[HSD_SEQ_CUR] + valid) % nslab;
+    seq[HSD_SEQ_HEAD_POS] += head;
+  }
+}
+
+// POS -= n_drop and CUR -= n_drop (mod nslab): the rollback of a verify step's last
+// n_drop rows (KVCache.trim, model.py:355; the checkpoint ring still holds the state).
+__global__ void k_seq_rollback(int32_t* seq, int n_drop, int nslab) {
+  if (threadIdx.x == 0) {
+    seq[HSD_SEQ_POS] -= n_drop;
+    if (nslab > 0) seq[HSD_SEQ_CUR] = ((seq[HSD_SEQ_CUR] - n_drop) % nslab + nslab) % nslab;
+  }
+}
+
 // seq[idx] += delta (host-known adjustments outside a graph, e.g. the head's prefill rows)
 __global__ void k_seq_add(int32_t* seq, int idx, int delta) {
   if (threadIdx.x == 0) seq[idx] += delta;
@@ -287,4 +318,31 @@ extern "C" int hsd_seq_add(int32_t* seq, int64_t idx, int64_t delta, void* strea
   if (idx < 0 || idx >= HSD_SEQ_LEN) return set_error(HSD_ERR_SHAPE, "hsd_seq_add: bad index");
   hipLaunchKernelGGL(k_seq_add, dim3(1), dim3(64), 0, as_stream(stream), seq, (int)idx, (int)delta);
   return check_launch("hsd_seq_add");
+}
+
+extern "C" int hsd_gather_tokens(const int32_t* src, int64_t n, const int32_t* seq, int64_t offset, int64_t count,
+                                 int32_t* dst, void* stream) {
+  if (!src || !seq || !dst) return set_error(HSD_ERR_ARG, "hsd_gather_tokens: null pointer");
+  if (n <= 0 || n > 0x7FFFFFFF || count < 0 || count > 64 || offset < -65536 || offset > 65536)
+    return set_error(HSD_ERR_SHAPE, "hsd_gather_tokens: bad sizes");
+  if (count == 0) return HSD_OK;
+  hipLaunchKernelGGL(k_gather_tokens, dim3(1), dim3(64), 0, as_stream(stream), src, (int)n, seq, (int)offset,
+                     (int)count, dst);
+  return check_launch("hsd_gather_tokens");
+}
+
+extern "C" int hsd_prefill_advance(int32_t* seq, int64_t T, int64_t B, int64_t nslab, void* stream) {
+  if (!seq) return set_error(HSD_ERR_ARG, "hsd_prefill_advance: null pointer");
+  if (T < 0 || T > 0x7FFFFFFF || B < 1 || B > 64 || nslab < 0 || nslab > 64)
+    return set_error(HSD_ERR_SHAPE, "hsd_prefill_advance: bad sizes");
+  hipLaunchKernelGGL(k_prefill_advance, dim3(1), dim3(64), 0, as_stream(stream), seq, (int)T, (int)B, (int)nslab);
+  return check_launch("hsd_prefill_advance");
+}
+
+extern "C" int hsd_seq_rollback(int32_t* seq, int64_t n_drop, int64_t nslab, void* stream) {
+  if (!seq) return set_error(HSD_ERR_ARG, "hsd_seq_rollback: null pointer");
+  if (n_drop < 0 || n_drop > 64 || nslab < 0 || nslab > 64 || (nslab > 0 && n_drop >= nslab))
+    return set_error(HSD_ERR_SHAPE, "hsd_seq_rollback: need 0 <= n_drop < nslab");
+  hipLaunchKernelGGL(k_seq_rollback, dim3(1), dim3(64), 0, as_stream(stream), seq, (int)n_drop, (int)nslab);
+  return check_launch("hsd_seq_rollback");
 }

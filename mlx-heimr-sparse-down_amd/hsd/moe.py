@@ -151,7 +151,7 @@ def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, statu
 
 
 def route_up_relu2(x, logits, e_bias, w1, s1, b1, sw1, ss1, sb1, *, topk, routed_scale=1.0, norm_topk=True,
-                   live_masks=None, out=None):
+                   live_masks=None, out=None, sel=None, gains=None):
     """The MoE front end WITH the router (model.py:110-121 from `mix.gate` on): from the
     gate's logits [B, E] bf16 (nn.linear of the normed token with the bf16 gate weight)
     the top-k experts (sigmoid scores plus the selection bias e_bias [E] f32, descending,
@@ -166,8 +166,8 @@ def route_up_relu2(x, logits, e_bias, w1, s1, b1, sw1, ss1, sb1, *, topk, routed
     FS = sw1.shape[0]
     NR = topk * F + FS
     hcat = out if out is not None else torch.empty((B, NR), dtype=torch.bfloat16, device=x.device)
-    sel = torch.empty((B, topk), dtype=torch.int32, device=x.device)
-    gains = torch.empty((B, topk + 1), dtype=torch.float32, device=x.device)
+    sel = sel if sel is not None else torch.empty((B, topk), dtype=torch.int32, device=x.device)
+    gains = gains if gains is not None else torch.empty((B, topk + 1), dtype=torch.float32, device=x.device)
     N.call("hsd_moe_route_up_relu2", N.ptr(x), N.DT_BF16, N.ptr(logits), N.ptr(e_bias), float(routed_scale),
            1 if norm_topk else 0, N.ptr(sel), N.ptr(gains), N.ptr(N.as_words(N.contig(w1))), N.ptr(N.contig(s1)),
            N.ptr(N.contig(b1)), N.ptr(N.as_words(N.contig(sw1))), N.ptr(N.contig(ss1)), N.ptr(N.contig(sb1)),
