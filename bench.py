@@ -1,20 +1,22 @@
 """Benchmark of the hsd hot path on one MI355X.
 
-Default workload (python bench.py [--steps K --warmup W]): the 23-layer batch-1 decode
-sweep at the Nemotron-3.5-Lightning-30B-A3B MoE shape -- 128 experts, top-6 uniform
-routing per layer and token, routed D=2688 x F=1856 and shared D x 3712 down
-projections in affine 4-bit g64 (8.39 GB of neuron-major weights resident), ReLU^2
-activations with 90 % exact zeros. A step = one token through the 23 sparse down
-projections (captured once per token as a HIP graph and replayed). `value` is GB/s over
-the bytes actually touched (live rows x D/2 + live 64-groups x 4D + I/O) for the whole
-timed region; inputs are resident in HBM.
+Default (python bench.py [--steps K --warmup W]): one JSON line whose headline is the
+end-to-end workload -- batch-1 greedy decode of a random-init Nemotron-H hybrid at the
+Nemotron-3.5-Lightning-30B-A3B shape (52 layers: 23 Mamba-2, 23 MoE with 128 experts top-6
+and the 4-bit neuron-major down projection, 6 GQA attention; vocab 131072; 4-bit g64; the
+one-layer MTP head), a 2048-token seeded random prompt, then 256 tokens: `value` is the
+decode tok/s of sparse down + MTP-2 with scripted acceptance at a mean of 1.26 accepted
+drafts; dense down, sparse down and the 1.68 acceptance are reported beside it, with the
+check that all four produce the same greedy tokens. A step is one speculative step
+(the head's two drafts, the 3-row verify through the 52 layers, the acceptance and the
+rollback), replayed from one captured graph; inputs and weights are resident in HBM.
 
-Other workloads, each printing one JSON line of its own:
-  --workload prefill   2048-token prompt in chunks of 512, Zipf(1.1) routing, 23 layers
-  --workload mtp       MTP-2 verify (3 rows) + rollback over 23 Mamba-2 layers
-  --workload up        the MoE front end after the router: 4-bit up projections of the 6
-                       selected and the shared expert + ReLU^2 into hcat, 23 layers,
-                       batch 1; also the front end followed by the sparse down projection
+`roofline` is the sparse down projection's (the hot path of the metric), from the 23-layer
+decode sweep; `workloads` holds the decode sweep, the prefill grouped GEMM, the MTP
+verify + rollback over 23 Mamba-2 layers and the MoE front end, each with its roofline and
+its CPU baseline (the NumPy oracle on the host cores, a bounded sample).
+
+--workload e2e|decode|prefill|mtp|up prints one of them alone.
 """
 from __future__ import annotations
 
@@ -31,10 +33,11 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-heimr-sparse-down_amd"))
 import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
-from hsd import decode, layout, mamba as M, moe, mtp, prefill, synth as S  # noqa: E402
+from hsd import decode, layout, mamba as M, model as Mdl, moe, mtp, prefill, synth as S  # noqa: E402
 from hsd import _native as N  # noqa: E402
 
 METRIC = "batch-1 decode tok/s (sparse+MTP2); sparse-down HBM GB/s vs peak"
+DECODE_METRIC = "sparse down projection, 23 MoE layers, batch 1: HBM GB/s on touched bytes"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.txt")
@@ -226,6 +229,38 @@ def cpu_baseline_decode(layers, h, sel, gains, budget_s=15.0):
                 ms_per_token_layer=round(1e3 * cpu_s / n, 3), **{k: v for k, v in info.items()})
 
 
+def cpu_baseline_decode_formula(layers, h, sel, gains, budget_s=8.0):
+    """The reference's own formula on host cores (test_layout_decode.py:128-142): the 7
+    selected stock-layout matrices dequantised in full, then the mat-vecs (the oracle's
+    float64 dense_reference), over token-layers in order until ~budget_s."""
+    sys.path.insert(0, ROOT)
+    from oracle import hsd_oracle as O
+    cpu_s, n, done_bytes = 0.0, 0, 0
+    t = 0
+    while cpu_s < budget_s and t < h.shape[0]:
+        for l in range(NL):
+            st = layers[l]["stock"]
+            s_h = sel[t, l].cpu().numpy()
+            w = np.stack([S.to_host(st["w"][int(e)]).view(np.uint32) for e in s_h])
+            sc = np.stack([S.to_host(st["s"][int(e)]) for e in s_h])
+            bi = np.stack([S.to_host(st["b"][int(e)]) for e in s_h])
+            sw, ss, sb = S.to_host(st["sw"]).view(np.uint32), S.to_host(st["ss"]), S.to_host(st["sb"])
+            hv = h[t, l].float().cpu().numpy()[None]
+            g = gains[t, l].cpu().numpy()[None]
+            idx = np.arange(K, dtype=np.int32)[None]
+            t0 = time.perf_counter()
+            O.dense_reference(hv, idx, g, w, sc, bi, sw, ss, sb, F=F, FS=FS, D=D, topk=K)
+            cpu_s += time.perf_counter() - t0
+            done_bytes += int(touched_bytes_dev(h[t, l]).item())
+            n += 1
+            if cpu_s >= budget_s:
+                break
+        t += 1
+    return dict(value=round(done_bytes / cpu_s / 1e9, 4), unit="GB/s (touched bytes)",
+                ms_per_token_layer=round(1e3 * cpu_s / n, 3),
+                sample=f"{n} token-layers: full dequantisation of the 7 selected matrices + mat-vec (float64)")
+
+
 def bench_decode(args):
     dev = torch.device("cuda:0")
     log(f"[decode] building {NL} MoE layers (stock 4-bit, permuting to neuron-major on device)")
@@ -283,8 +318,10 @@ def bench_decode(args):
         log(f"[decode] cold: {1e3 * ms_c / ncold:.1f} us/token, {bc / (ms_c * 1e-3) / 1e9:.0f} GB/s")
         del flush
     cpu = cpu_baseline_decode(layers, h, sel, gains, budget_s=args.cpu_budget) if args.cpu_budget > 0 else None
+    if cpu is not None and not args.no_dense:
+        cpu["reference_formula"] = cpu_baseline_decode_formula(layers, h, sel, gains, budget_s=args.cpu_budget / 2)
     achieved = per_launch_bytes / (per_launch_us * 1e-6) / 1e9
-    rec = dict(metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=steps, warmup=warm,
+    rec = dict(metric=DECODE_METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=steps, warmup=warm,
                ms_per_step=round(ms_step, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
                dtype="f32 (4-bit weights, bf16 scales/activations)", data="synthetic",
                config=dict(workload="decode sweep: 23 MoE layers, batch 1, sparse 4-bit down projection",
@@ -302,6 +339,39 @@ def bench_decode(args):
 
 
 # ------------------------------------------------------------------ prefill
+def cpu_baseline_prefill(layers, chunks, args, tokens=32):
+    """The oracle's grouped matmul (sparse_down_prefill: per tile, the union rows
+    dequantised, float64) on host cores for the first `tokens` tokens of the first chunk of
+    layer 0 (the same tile order and unions), as algorithmic TFLOP/s."""
+    sys.path.insert(0, ROOT)
+    from oracle import hsd_oracle as O
+    l, h, sel, gains = chunks[0]
+    hh = S.to_host(h[:tokens])
+    ss, gg = sel[:tokens].cpu().numpy(), gains[:tokens].cpu().numpy()
+    nm = layers[l]["nm"]
+    used = sorted(set(int(e) for e in ss.reshape(-1)))
+    pw = np.zeros((E, F, D // 8), np.uint32)
+    ps = np.zeros((E, F // 64, D), np.uint16)
+    pb = np.zeros((E, F // 64, D), np.uint16)
+    for e in used:
+        pw[e] = S.to_host(nm[0][e]).view(np.uint32)
+        ps[e] = S.to_host(nm[1][e])
+        pb[e] = S.to_host(nm[2][e])
+    spw, sps, spb = S.to_host(nm[3]).view(np.uint32), S.to_host(nm[4]), S.to_host(nm[5])
+    te, ts = O.build_tiles(ss, E, args.tt)
+    ul, uc = O.build_union(O.bf16_to_f32(hh), te, ts, F=F, FS=FS, topk=K, E=E, tt=args.tt)
+    nvalid = (ts.reshape(-1, args.tt) >= 0).sum(1)
+    flops = int((2 * D * nvalid.astype(np.int64) * uc.astype(np.int64)).sum())
+    t0 = time.perf_counter()
+    O.sparse_down_prefill(O.bf16_to_f32(hh), ss, gg, pw, ps, pb, spw, sps, spb, F=F, FS=FS, D=D, topk=K, E=E,
+                          tt=args.tt, tiles=(te, ts), union=(ul, uc))
+    sec = time.perf_counter() - t0
+    info = cpu_info()
+    return dict(value=round(flops / sec / 1e12, 6), unit="TFLOP/s", cores=info["affinity"], kind="port",
+                sample=f"{tokens} tokens of one 512-token chunk of one layer (NumPy oracle grouped matmul over the "
+                       f"union rows, float64)", seconds=round(sec, 3), **info)
+
+
 def bench_prefill(args):
     dev = torch.device("cuda:0")
     nl = args.layers
@@ -361,6 +431,7 @@ def bench_prefill(args):
     wbytes = nl * 364.8e6 * (T // chunk)
     log(f"[prefill] grouped GEMM {ms_gemm:.2f} ms per prompt ({tflops:.1f} TFLOP/s algorithmic); with tiles+union "
         f"{ms_all:.2f} ms -> {T / (ms_all * 1e-3):.0f} tok/s")
+    cpu = cpu_baseline_prefill(layers, chunks, args) if args.cpu_budget > 0 else None
     return dict(metric="prefill down-projection TFLOP/s (bf16 MFMA, algorithmic union FLOPs)",
                 value=round(tflops, 2), unit="TFLOP/s", n_gpus=1, steps=args.steps, warmup=1,
                 ms_per_step=round(ms_all, 4), higher_is_better=True, scaling="weak", vs_baseline=None,
@@ -370,10 +441,34 @@ def bench_prefill(args):
                 roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
                               frac=round(tflops / BF16_PEAK_TFLOPS, 4), traffic=pmc_traffic("prefill"),
                               hbm_frac_dense_weights=round(wbytes / (ms_gemm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
+                cpu_baseline=cpu,
                 prefill_tok_s=round(T / (ms_all * 1e-3), 1), gflop_per_prompt=round(flops / 1e9, 2))
 
 
 # ------------------------------------------------------------------ MTP verify
+def cpu_baseline_mtp(args, per_layer, layers=4):
+    """The oracle's sequential Mamba-2 recurrence (mamba_verify: conv, SSM over 3 rows with
+    every row's state kept, gated norm; float64) on host cores for `layers` layer-steps, as
+    GB/s over the same byte model."""
+    sys.path.insert(0, ROOT)
+    from oracle import hsd_oracle as O
+    rng = np.random.default_rng(args.seed)
+    DI, CD = 4096, 6144
+    sec = 0.0
+    for l in range(layers):
+        p = S.mamba_params_np(args.seed + l)
+        r = O.bf16_to_f32(S.mamba_rows_np(rng, 3))
+        t0 = time.perf_counter()
+        O.mamba_verify(r[:, DI:DI + CD], r[:, DI + CD:], r[:, :DI], O.bf16_to_f32(p["conv_w"]),
+                       O.bf16_to_f32(p["conv_b"]), p["A_log"], p["dt_bias"], p["D"], O.bf16_to_f32(p["norm_w"]),
+                       O.bf16_to_f32(p["conv_state"]), p["ssm_state"])
+        sec += time.perf_counter() - t0
+    info = cpu_info()
+    return dict(value=round(per_layer * layers / sec / 1e9, 4), unit="GB/s", cores=info["affinity"], kind="port",
+                sample=f"{layers} layer-steps of 3 rows (NumPy oracle recurrence, float64)",
+                ms_per_layer_step=round(1e3 * sec / layers, 2), **info)
+
+
 def bench_mtp(args):
     dev = torch.device("cuda:0")
     nl = NL
@@ -416,6 +511,7 @@ def bench_mtp(args):
     per_layer = 2097152 + 3 * 2097152 + 3 * 6144 * 2 + 3 * 3 * 6144 * 2 + 3 * 10304 * 2 + 3 * 4096 * 2
     gbs = per_layer * nl * args.steps / (ms * 1e-3) / 1e9
     log(f"[mtp] verify(3)+rollback, 23 Mamba-2 layers: {1e3 * ms / args.steps:.1f} us/step, {gbs:.0f} GB/s")
+    cpu = cpu_baseline_mtp(args, per_layer) if args.cpu_budget > 0 else None
     return dict(metric="MTP-2 verify + rollback, 23 Mamba-2 layers: HBM GB/s", value=round(gbs, 2), unit="GB/s",
                 n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=round(ms / args.steps, 5),
                 higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32 state, bf16 I/O",
@@ -423,10 +519,34 @@ def bench_mtp(args):
                 config=dict(workload="MTP verify + rollback: 23 Mamba-2 layers, 3 rows, P(0,1,2)=(.15,.35,.5)"),
                 roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                               frac=round(gbs / HBM_PEAK_GBS, 4), traffic=pmc_traffic("mtp"),
-                              bytes_per_layer_step=per_layer))
+                              bytes_per_layer_step=per_layer),
+                cpu_baseline=cpu)
 
 
 # ------------------------------------------------------------------ MoE front end
+def cpu_baseline_up(ups, x, sel, per_call, calls=3):
+    """The oracle's front end (up_relu2: the 7 up projections dequantised, float64, then
+    ReLU^2 in bf16) on host cores for `calls` token-layers, as GB/s over the same bytes."""
+    sys.path.insert(0, ROOT)
+    from oracle import hsd_oracle as O
+    sec = 0.0
+    for c in range(calls):
+        u = ups[c]
+        s_h = sel[c, c].cpu().numpy()
+        w1 = np.stack([S.to_host(u["w1"][int(e)]).view(np.uint32) for e in s_h])
+        s1 = np.stack([S.to_host(u["s1"][int(e)]) for e in s_h])
+        b1 = np.stack([S.to_host(u["b1"][int(e)]) for e in s_h])
+        sw1, ss1, sb1 = S.to_host(u["sw1"]).view(np.uint32), S.to_host(u["ss1"]), S.to_host(u["sb1"])
+        xb = S.to_host(x[c, c:c + 1])
+        t0 = time.perf_counter()
+        O.up_relu2(xb, np.arange(K, dtype=np.int32)[None], w1, s1, b1, sw1, ss1, sb1, F=F, FS=FS, topk=K)
+        sec += time.perf_counter() - t0
+    info = cpu_info()
+    return dict(value=round(per_call * calls / sec / 1e9, 4), unit="GB/s", cores=info["affinity"], kind="port",
+                sample=f"{calls} token-layers (NumPy oracle up projections + ReLU^2, float64)",
+                ms_per_token_layer=round(1e3 * sec / calls, 2), **info)
+
+
 def bench_up(args):
     dev = torch.device("cuda:0")
     nl = args.layers
@@ -466,6 +586,7 @@ def bench_up(args):
     log(f"[up] front end (up projections + ReLU^2), 23 layers: {1e3 * ms / args.steps:.1f} us/token, "
         f"{gbs:.0f} GB/s over {per_call / 1e6:.2f} MB/layer")
     log(f"[up] front end + sparse down, 23 layers: {1e3 * cms / args.steps:.1f} us/token")
+    cpu = cpu_baseline_up(ups, x, sel, per_call) if args.cpu_budget > 0 else None
     return dict(metric="MoE front end (4-bit up projections + ReLU^2), batch 1, 23 layers: HBM GB/s",
                 value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
                 ms_per_step=round(ms / args.steps, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
@@ -477,15 +598,193 @@ def bench_up(args):
                               frac=round(gbs / HBM_PEAK_GBS, 4), traffic=pmc_traffic("up"),
                               kernel="k_moe_up", bytes_per_launch=per_call,
                               us_per_launch=round(1e3 * ms / args.steps / nl, 3)),
+                cpu_baseline=cpu,
                 front_plus_down_us_per_token=round(1e3 * cms / args.steps, 2))
+
+
+# ------------------------------------------------------------------ end to end
+def _host_block_weights(model, l):
+    """Block l's weights as host arrays in the oracle's conventions."""
+    u32 = lambda t: S.to_host(t).view(np.uint32)
+    t, blk = model.cfg.pattern[l], model.blocks[l]
+    if t == "M":
+        m = blk.mixer
+        return dict(norm_w=S.to_host(blk.norm_w), in_w=u32(blk.in_proj.w), in_s=S.to_host(blk.in_proj.scales),
+                    in_b=S.to_host(blk.in_proj.biases), out_w=u32(blk.out_proj.w), out_s=S.to_host(blk.out_proj.scales),
+                    out_b=S.to_host(blk.out_proj.biases), conv_w=m.conv_w.float().cpu().numpy(),
+                    conv_b=m.conv_b.float().cpu().numpy(), A_log=m.A_log.cpu().numpy(),
+                    dt_bias=m.dt_bias.cpu().numpy(), D=m.D.cpu().numpy(), gnorm_w=S.to_host(m.norm_w))
+    if t == "*":
+        return dict(norm_w=S.to_host(blk.norm_w), qkv_w=u32(blk.qkv.w), qkv_s=S.to_host(blk.qkv.scales),
+                    qkv_b=S.to_host(blk.qkv.biases), o_w=u32(blk.o_proj.w), o_s=S.to_host(blk.o_proj.scales),
+                    o_b=S.to_host(blk.o_proj.biases))
+    return dict(norm_w=S.to_host(blk.norm_w), gate=S.to_host(blk.gate.w), e_bias=blk.e_bias.cpu().numpy(),
+                w1=u32(blk.w1), s1=S.to_host(blk.s1), b1=S.to_host(blk.b1), sw1=u32(blk.sw1), ss1=S.to_host(blk.ss1),
+                sb1=S.to_host(blk.sb1), pw=u32(blk.pw), ps=S.to_host(blk.ps), pb=S.to_host(blk.pb), spw=u32(blk.spw),
+                sps=S.to_host(blk.sps), spb=S.to_host(blk.spb))
+
+
+def cpu_baseline_e2e(model, sess, lm_rows=8192):
+    """The oracle's decode step on host cores, sampled: one decode row through one Mamba-2,
+    one MoE and one attention block (the attention over the session's cached keys) and
+    lm_head over `lm_rows` of its rows, each timed, then scaled to the 52-layer step
+    (23 / 23 / 6 blocks, the whole vocabulary) -> tok/s."""
+    sys.path.insert(0, ROOT)
+    from oracle import hsd_oracle as O
+    c = model.cfg
+    pat = c.pattern
+    seq = sess.state()
+    P, cur = seq[N.SEQ_POS], seq[N.SEQ_CUR]
+    E_ = model.embedding
+    x = O.embed_q4(np.array([seq[N.SEQ_TOK]]), S.to_host(E_.w).view(np.uint32), S.to_host(E_.scales),
+                   S.to_host(E_.biases))[0]
+    t = {}
+    for kind in "ME*":
+        l = pat.index(kind)
+        w = _host_block_weights(model, l)
+        lc = sess.cache.layers[l]
+        t0 = time.perf_counter()
+        if kind == "M":
+            O.mamba_block_step(x, w, lc.conv[cur].float().cpu().numpy(), lc.ssm[cur].cpu().numpy(),
+                               n_groups=c.n_groups, eps=c.eps)
+        elif kind == "*":
+            k = lc.k[:, :P].float().cpu().numpy()
+            v = lc.v[:, :P].float().cpu().numpy()
+            t0 = time.perf_counter()
+            O.attn_block_step(x, w, k, v, n_heads=c.attn_heads, n_kv_heads=c.kv_heads, eps=c.eps)
+        else:
+            O.moe_block_step(x, w, topk=c.topk, routed_scale=c.routed_scale, eps=c.eps)
+        t[kind] = time.perf_counter() - t0
+        del w
+    lw = S.to_host(model.lm_head.w[:lm_rows]).view(np.uint32)
+    t0 = time.perf_counter()
+    O.lm_head_logits(x, S.to_host(model.norm_f), lw, S.to_host(model.lm_head.scales[:lm_rows]),
+                     S.to_host(model.lm_head.biases[:lm_rows]), c.eps)
+    t_lm = (time.perf_counter() - t0) * c.vocab / lm_rows
+    per_tok = pat.count("M") * t["M"] + pat.count("E") * t["E"] + pat.count("*") * t["*"] + t_lm
+    info = cpu_info()
+    return dict(value=round(1.0 / per_tok, 5), unit="tok/s", cores=info["affinity"], kind="port",
+                sample=f"one decode row through one Mamba-2, one MoE and one attention block (keys 0..{P}) and "
+                       f"{lm_rows} lm_head rows with the NumPy oracle (float64), scaled to the 52-layer step",
+                seconds_per_token=round(per_tok, 3),
+                block_seconds=dict(mamba=round(t["M"], 4), moe=round(t["E"], 4), attention=round(t["*"], 4),
+                                   lm_head=round(t_lm, 4)), **info)
+
+
+def bench_e2e(args):
+    dev = torch.device("cuda:0")
+    cfg = Mdl.ModelConfig()
+    t0 = time.time()
+    model = Mdl.NemotronModel(cfg, mode="sparse", seed=args.seed)
+    torch.cuda.synchronize()
+    init_s = time.time() - t0
+    log(f"[e2e] model: {len(cfg.pattern)} layers + MTP head, {model.nbytes() / 1e9:.2f} GB, built and calibrated "
+        f"in {init_s:.1f} s; MoE zero fractions {min(model.zero_frac_measured):.3f}..{max(model.zero_frac_measured):.3f}")
+    prompt = np.random.default_rng(args.seed + 11).integers(0, cfg.vocab, args.prompt).astype(np.int32)
+    G, W = args.gen, max(args.warmup, 0)
+    runs = {}
+
+    def plain(mode):
+        model.set_mode(mode)
+        s = model.session(prompt, cap=G + 8)
+        s.step(W)
+        n0 = s.emitted()
+        k = max(G + 4 - n0, 1)
+        sec = s.step(k)
+        n1 = s.emitted()
+        toks = s.tokens(G + 4)
+        r = dict(tok_s=round((n1 - n0) / sec, 2), ms_per_token=round(1e3 * sec / k, 4), steps=k, warmup=W,
+                 prompt_tok_s=round(len(prompt) / s.prompt_s, 1))
+        log(f"[e2e] {mode}: {r['tok_s']:.1f} tok/s decode ({r['ms_per_token']:.3f} ms/token), prefill "
+            f"{r['prompt_tok_s']:.0f} tok/s")
+        return r, toks, s
+
+    runs["dense"], dense_toks, _ = plain("dense")
+    runs["sparse"], sparse_toks, sess_sparse = plain("sparse")
+    runs["sparse"]["tokens_equal_dense"] = sparse_toks[:G] == dense_toks[:G]
+    cpu = cpu_baseline_e2e(model, sess_sparse) if args.cpu_budget > 0 else None
+    del sess_sparse
+    model.set_mode("sparse")
+    for name, probs in (("mtp2_prose", (0.2, 0.34, 0.46)), ("mtp2_code", (0.06, 0.2, 0.74))):
+        acc = mtp.scripted_accepts(8192, probs, seed=args.seed + 5)
+        s = model.session(prompt, mtp=True, cap=G + 8, script=dense_toks, accepts=acc)
+        s.step(W)
+        n0, st0 = s.emitted(), s.state()
+        if args.steps > 0:
+            k = args.steps
+        else:                                    # the steps that bring the generation to G tokens
+            k, n = 0, n0
+            while n < G:
+                n += int(acc[W + k]) + 1
+                k += 1
+        sec = s.step(k)
+        st1 = s.state()
+        n1 = s.emitted()
+        toks = s.tokens(G)
+        acc_mean = (st1[N.SEQ_ACC_SUM] - st0[N.SEQ_ACC_SUM]) / k
+        runs[name] = dict(tok_s=round((n1 - n0) / sec, 2), ms_per_step=round(1e3 * sec / k, 4), steps=k, warmup=W,
+                          accepted_mean=round(acc_mean, 4), tokens_per_step=round((n1 - n0) / k, 4),
+                          scripted_probs=list(probs), tokens_equal_dense=toks == dense_toks[:G],
+                          prompt_tok_s=round(len(prompt) / s.prompt_s, 1))
+        log(f"[e2e] sparse + MTP-2 ({name}, mean accepted {acc_mean:.2f}): {runs[name]['tok_s']:.1f} tok/s, "
+            f"{runs[name]['ms_per_step']:.3f} ms/step, tokens equal dense: {runs[name]['tokens_equal_dense']}")
+        del s
+    head = runs["mtp2_prose"]
+    rec = dict(metric=METRIC, value=head["tok_s"], unit="tok/s", n_gpus=1, steps=head["steps"], warmup=W,
+               ms_per_step=head["ms_per_step"], higher_is_better=True, scaling="weak", vs_baseline=None,
+               dtype="f32 accumulate (4-bit weights, bf16 activations)", data="synthetic",
+               config=dict(workload="end to end: random-init Nemotron-H hybrid, 52 layers (23 Mamba-2, 23 MoE "
+                                    "128x top-6, 6 GQA 32/2) + 1-layer MTP head, 4-bit g64, vocab 131072; "
+                                    "2048-token random prompt, 256 greedy tokens; sparse down + MTP-2, scripted "
+                                    "acceptance at mean 1.26/2",
+                           prompt_tokens=len(prompt), gen_tokens=G, layers=len(cfg.pattern), hidden=cfg.hidden,
+                           vocab=cfg.vocab, experts=cfg.n_experts, topk=cfg.topk,
+                           weights_gb=round(model.nbytes() / 1e9, 2),
+                           moe_zero_frac=round(float(np.mean(model.zero_frac_measured)), 4)),
+               roofline=None, cpu_baseline=cpu, e2e=runs,
+               all_tokens_equal=all(r.get("tokens_equal_dense", True) for r in runs.values()),
+               reference_published={"sparse+MTP2 tok/s, Apple M5 Pro, real checkpoint and text (README.md:19)": 153})
+    del model
+    torch.cuda.empty_cache()
+    return rec
+
+
+def _sub(rec):
+    """A workload's record inside the combined line (the fields the run record repeats dropped)."""
+    drop = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "data")
+    return {k: v for k, v in rec.items() if k not in drop}
+
+
+def bench_all(args):
+    import copy
+    rec = bench_e2e(args)
+    torch.cuda.empty_cache()
+    sub = {}
+    for name, fn, steps, warm in (("decode_sparse_down", bench_decode, 200, 20), ("prefill", bench_prefill, 3, 1),
+                                  ("mtp_verify_rollback", bench_mtp, 200, 20), ("moe_front_end", bench_up, 200, 20)):
+        a = copy.copy(args)
+        a.steps, a.warmup = steps, warm
+        if name == "decode_sparse_down":
+            a.cold = True
+        sub[name] = _sub(fn(a))
+        torch.cuda.empty_cache()
+    dec = sub["decode_sparse_down"]
+    rec["roofline"] = dict(dec["roofline"], workload="decode_sparse_down",
+                           note="the sparse down projection (the metric's 'sparse-down HBM GB/s vs peak'), from the "
+                                "23-layer decode sweep at 90 % zeros, warm; the cold figure is in workloads")
+    rec["workloads"] = sub
+    return rec
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "mtp", "up"))
+    ap.add_argument("--steps", type=int, default=0,
+                    help="timed steps (0: the workload's default; end to end: the steps that make 256 tokens)")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="all", choices=("all", "e2e", "decode", "prefill", "mtp", "up"))
+    ap.add_argument("--prompt", type=int, default=2048, help="end to end: prompt tokens")
+    ap.add_argument("--gen", type=int, default=256, help="end to end: generated tokens")
     ap.add_argument("--zero-frac", type=float, default=0.9)
     ap.add_argument("--hot", action="store_true", help="hot-neuron activation variant")
     ap.add_argument("--ntok", type=int, default=32, help="distinct tokens rotated (one graph each)")
@@ -503,7 +802,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    fn = dict(decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp, up=bench_up)[args.workload]
+    if args.workload not in ("all", "e2e"):
+        defaults = dict(decode=(200, 20), prefill=(3, 1), mtp=(200, 20), up=(200, 20))[args.workload]
+        if args.steps <= 0:
+            args.steps, args.warmup = defaults
+    fn = dict(all=bench_all, e2e=bench_e2e, decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp,
+              up=bench_up)[args.workload]
     rec = fn(args)
     rec["device"] = torch.cuda.get_device_name(0)
     rec["torch"] = torch.__version__

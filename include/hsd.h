@@ -168,6 +168,11 @@ int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t* logits, c
                            int64_t B, int64_t D, int64_t F, int64_t FS, int64_t topk, int64_t E,
                            uint64_t* live_masks, void* stream);
 
+/* The router half of hsd_moe_route_up_relu2 on its own: sel [B, topk] and gains
+ * [B, topk+1] from the gate's logits, by the same rule (one workgroup per token row). */
+int hsd_router_topk(const uint16_t* logits, const float* e_bias, float routed_scale, int norm_topk,
+                    int32_t* sel, float* gains, int64_t B, int64_t E, int64_t topk, void* stream);
+
 /* The dense 4-bit down projection on the STOCK layout -- the comparator that
  * mlx-lm's gather_qmm + quantized_matmul compute in dense mode (model.py:132-133;
  * test_layout_decode.py:145-151). w [E, D, F/8], s/b [E, D, F/64]; sw [D, FS/8],
@@ -229,7 +234,7 @@ int hsd_argmax_keys(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, 
  *   out [B, HQ * HD] bf16: softmax(scale q k^T over keys 0 .. P+r) v per query head;
  *   query head h reads kv head h / (HQ / HKV).
  * P + B > smax: the call writes zeros and sets HSD_STATUS_BAD_STATE. Requirements:
- * HD == 128, (HQ / HKV) % 8 == 0, smax % 64 == 0. A row's arithmetic does not depend on
+ * HD == 128, (HQ / HKV) % 8 == 0, smax % 64 == 0, smax <= 16384. A row's arithmetic does not depend on
  * B. workspace: hsd_attn_workspace_bytes(B, HQ, smax). */
 size_t hsd_attn_workspace_bytes(int64_t B, int64_t HQ, int64_t smax);
 int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, uint16_t* k_cache,

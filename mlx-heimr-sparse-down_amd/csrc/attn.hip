@@ -164,6 +164,7 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
     for (int r = 0; r < kAMaxB; ++r)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
+#pragma unroll 8
     for (int jl = 0; jl < kCH; ++jl) {
       const uint2 vv = *reinterpret_cast<const uint2*>(&vs[jl][d0 / 2]);
       const float v0 = bf16_bits_to_f32(vv.x & 0xFFFFu), v1 = bf16_bits_to_f32(vv.x >> 16);
@@ -203,7 +204,12 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
   }
 }
 
+constexpr int kMaxCh = 256;      // chunks per row the combine stages in LDS (smax <= 16384)
+
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
+  __shared__ float mw[kMaxCh];    // the chunks' maxima, then their weights e^(m - M)
+  __shared__ float lw[kMaxCh];
+  __shared__ float red[2];
   const int r = blockIdx.x / a.HQ, h = blockIdx.x - r * a.HQ;
   const int d = threadIdx.x;
   const int P = *a.pos;
@@ -214,14 +220,40 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   }
   const int nc = (P + r) / kCH + 1;
   const float* src = a.part + ((size_t)r * a.HQ + h) * a.nch * kRec;
-  float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, src[(size_t)c * kRec]);
+  // (m, l) of every chunk in one round trip, into LDS
+  for (int c = d; c < nc; c += kHD) {
+    mw[c] = src[(size_t)c * kRec];
+    lw[c] = src[(size_t)c * kRec + 1];
+  }
+  __syncthreads();
+  if (d < 64) {
+    float M = -INFINITY;
+    for (int c = d; c < nc; c += 64) M = fmaxf(M, mw[c]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if (d == 0) red[0] = M;
+  }
+  __syncthreads();
+  const float M = red[0];
+  for (int c = d; c < nc; c += kHD) mw[c] = __expf(mw[c] - M);
+  __syncthreads();
+  // L and this dimension's sum over the chunks in chunk order; the loads are issued in
+  // batches of 8 so that their latencies overlap
   float L = 0.0f, acc = 0.0f;
-  for (int c = 0; c < nc; ++c) {
-    const float* pc = src + (size_t)c * kRec;
-    const float e = __expf(pc[0] - M);
-    L = fmaf(pc[1], e, L);
-    acc = fmaf(pc[4 + d], e, acc);
+  int c = 0;
+  for (; c + 8 <= nc; c += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(c + u) * kRec + 4 + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      L = fmaf(lw[c + u], mw[c + u], L);
+      acc = fmaf(v[u], mw[c + u], acc);
+    }
+  }
+  for (; c < nc; ++c) {
+    L = fmaf(lw[c], mw[c], L);
+    acc = fmaf(src[(size_t)c * kRec + 4 + d], mw[c], acc);
   }
   o[d] = f32_to_bf16_bits(acc / L);
 }
@@ -247,8 +279,9 @@ extern "C" int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, u
   if (B < 1 || B > kAMaxB) return set_error(HSD_ERR_SHAPE, "%s: B must be in [1, %d]", fn, kAMaxB);
   if (HKV <= 0 || HQ <= 0 || HQ % HKV || (HQ / HKV) % kHPW)
     return set_error(HSD_ERR_SHAPE, "%s: query heads per kv head must be a multiple of %d", fn, kHPW);
-  if (smax <= 0 || smax % kCH || smax > (1 << 24))
-    return set_error(HSD_ERR_SHAPE, "%s: the cache length must be a multiple of %d", fn, kCH);
+  if (smax <= 0 || smax % kCH || smax > kCH * kMaxCh)
+    return set_error(HSD_ERR_SHAPE, "%s: the cache length must be a multiple of %d and at most %d", fn, kCH,
+                     kCH * kMaxCh);
   if (qkv_ld < (HQ + 2 * HKV) * kHD || qkv_ld % 8 || out_ld < HQ * kHD)
     return set_error(HSD_ERR_SHAPE, "%s: row strides", fn);
   if (((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u)

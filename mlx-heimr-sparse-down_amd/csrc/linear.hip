@@ -88,6 +88,15 @@ struct LinArgs {
   int O, I;
 };
 
+// Two floats to packed bf16 (round to nearest even; v_cvt_pk_bf16_f32 on gfx950). Used for
+// the normalised activations, which are finite.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+__device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
 // IMAX: the largest row length the instance serves (kIt weight pieces per lane, XIT x
 // words of 8 inputs per thread in the prologue).
 template <int WF, int NB, int XK, int YK, int IMAX>
@@ -96,6 +105,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   constexpr int kRW = T::kRW, kIt = pieces_per_lane<WF>(IMAX);
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   constexpr int kRows = 4 * kRW;                       // rows per block
+  constexpr int kSc = WF == HSD_W_Q4 ? kIt : 1;
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
   // LDS: x as bf16 pairs [NB][I/2] (4-bit: pairs (x[i], x[i+4]) in a word's nibble
   // order; bf16: natural pairs), then the 32-input piece sums [NB][I/32] (4-bit only)
@@ -111,9 +121,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   const int nit = (npw + 63) / 64;
 
   // ---- weight pieces of a block: piece p = lane + 64 it of the wave's kRW rows
-  uint4 q[kIt];
-  float sc[WF == HSD_W_Q4 ? kIt : 1], bi[WF == HSD_W_Q4 ? kIt : 1];
-  auto load_block = [&](int blk, uint4 (&qq)[kIt], float* ss, float* bb) {
+  auto load_block = [&](int blk, uint4 (&qq)[kIt], float (&ss)[kSc], float (&bb)[kSc]) {
     const int r0 = blk * kRows + kRW * wave;
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
@@ -131,6 +139,8 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
       }
     }
   };
+  uint4 q[kIt];
+  float sc[kSc], bi[kSc];
   int blk = blockIdx.x;
   load_block(blk, q, sc, bi);
 
@@ -155,63 +165,34 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
     }
     if constexpr (XK != HSD_X_BF16) nwv[i] = reinterpret_cast<const uint4*>(a.nw)[tc];
   }
-  // xe[b][i][n]: the prologue's output element 8t + n as bf16 bits
+  // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
   uint32_t xo[NB][XIT][4];
+  if constexpr (XK == HSD_X_BF16) {
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    float ss = 0.0f;
-    float zf[XIT][8];
-#pragma unroll
-    for (int i = 0; i < XIT; ++i) {
-      const bool tv = tid + kLT * i < NW;
-      const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const uint32_t bits = (n & 1) ? xw[n >> 1] >> 16 : xw[n >> 1] & 0xFFFFu;
-        float v = bf16_bits_to_f32(bits);
-        if constexpr (XK == HSD_X_GATED) {
-          const float yy = n < 4 ? (&yv0[b][i].x)[n] : (&yv1[b][i].x)[n - 4];
-          v = yy * silu_f32(v);
-        }
-        zf[i][n] = tv ? v : 0.0f;
-      }
-      if constexpr (XK == HSD_X_RMS) {
-#pragma unroll
-        for (int n = 0; n < 8; ++n) ss = fmaf(zf[i][n], zf[i][n], ss);
-      }
-    }
-    if constexpr (XK == HSD_X_RMS) {
-      ss = wave_sum_dpp(ss);
-      if (lane == 0) wsum[b][wave] = ss;
-    }
-    if constexpr (XK == HSD_X_GATED) {
-      // a wavefront's 64 words of iteration i are one 512-element group
-#pragma unroll
-      for (int i = 0; i < XIT; ++i) {
-        float g = 0.0f;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) g = fmaf(zf[i][n], zf[i][n], g);
-        g = wave_sum_dpp(g);
-        const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
-        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float w0 = bf16_bits_to_f32(nw4[c] & 0xFFFFu), w1 = bf16_bits_to_f32(nw4[c] >> 16);
-          const uint32_t lo = f32_to_bf16_bits(rne_bf16(zf[i][2 * c] * inv) * w0);
-          const uint32_t hi = f32_to_bf16_bits(rne_bf16(zf[i][2 * c + 1] * inv) * w1);
-          xo[b][i][c] = lo | (hi << 16);
-        }
-      }
-    } else if constexpr (XK == HSD_X_BF16) {
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < XIT; ++i) {
         xo[b][i][0] = xv[b][i].x; xo[b][i][1] = xv[b][i].y; xo[b][i][2] = xv[b][i].z; xo[b][i][3] = xv[b][i].w;
       }
+  } else if constexpr (XK == HSD_X_RMS) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        const bool tv = tid + kLT * i < NW;
+        const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float v0 = tv ? lo_f(xw[c]) : 0.0f, v1 = tv ? hi_f(xw[c]) : 0.0f;
+          ss = fmaf(v0, v0, ss);
+          ss = fmaf(v1, v1, ss);
+        }
+      }
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) wsum[b][wave] = ss;
     }
-    (void)zf;
-  }
-  if constexpr (XK == HSD_X_RMS) {
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float tot = ((wsum[b][0] + wsum[b][1]) + wsum[b][2]) + wsum[b][3];
@@ -222,11 +203,36 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float x0 = bf16_bits_to_f32(xw[c] & 0xFFFFu), x1 = bf16_bits_to_f32(xw[c] >> 16);
-          const float w0 = bf16_bits_to_f32(nw4[c] & 0xFFFFu), w1 = bf16_bits_to_f32(nw4[c] >> 16);
-          const uint32_t lo = f32_to_bf16_bits(rne_bf16(x0 * inv) * w0);
-          const uint32_t hi = f32_to_bf16_bits(rne_bf16(x1 * inv) * w1);
-          xo[b][i][c] = lo | (hi << 16);
+          const uint32_t t = pack_bf16x2(lo_f(xw[c]) * inv, hi_f(xw[c]) * inv);
+          xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
+        }
+      }
+    }
+  } else {  // HSD_X_GATED: a wavefront's 64 words of iteration i are one 512-element group
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        const bool tv = tid + kLT * i < NW;
+        const uint32_t gw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+        const float yy[8] = {yv0[b][i].x, yv0[b][i].y, yv0[b][i].z, yv0[b][i].w,
+                             yv1[b][i].x, yv1[b][i].y, yv1[b][i].z, yv1[b][i].w};
+        float z[8];
+        float g = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          z[2 * c] = tv ? yy[2 * c] * silu_f32(lo_f(gw[c])) : 0.0f;
+          z[2 * c + 1] = tv ? yy[2 * c + 1] * silu_f32(hi_f(gw[c])) : 0.0f;
+          g = fmaf(z[2 * c], z[2 * c], g);
+          g = fmaf(z[2 * c + 1], z[2 * c + 1], g);
+        }
+        g = wave_sum_dpp(g);
+        const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
+        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t t = pack_bf16x2(z[2 * c] * inv, z[2 * c + 1] * inv);
+          xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
         }
       }
     }
@@ -238,14 +244,14 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
     for (int i = 0; i < XIT; ++i) {
       const int t = tid + kLT * i;
       const uint32_t* w = xo[b][i];
-      auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
       if (t < NW) {
         uint4 pr;
         if constexpr (WF == HSD_W_Q4) {
-          pr.x = el(0) | (el(4) << 16);
-          pr.y = el(1) | (el(5) << 16);
-          pr.z = el(2) | (el(6) << 16);
-          pr.w = el(3) | (el(7) << 16);
+          // pairs (x[8t + n], x[8t + n + 4]): element n of the word is half (n & 1) of w[n / 2]
+          pr.x = (w[0] & 0xFFFFu) | (w[2] << 16);
+          pr.y = (w[0] >> 16) | (w[2] & 0xFFFF0000u);
+          pr.z = (w[1] & 0xFFFFu) | (w[3] << 16);
+          pr.w = (w[1] >> 16) | (w[3] & 0xFFFF0000u);
         } else {
           pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
         }
@@ -256,7 +262,10 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
       if constexpr (WF == HSD_W_Q4) {
         float s8 = 0.0f;
 #pragma unroll
-        for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32(el(n));
+        for (int c = 0; c < 4; ++c) {
+          s8 += lo_f(w[c]);
+          s8 += hi_f(w[c]);
+        }
         s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
         s8 += dpp_f32<0x4E>(s8);
         if (t < NW && (t & 3) == 0) xh[b * (I / 32) + (t >> 2)] = s8;
@@ -265,17 +274,11 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   }
   __syncthreads();
 
-  // ---- row blocks
+  // ---- one block: the lane's pieces into per-row partials, the 64-lane sums, the epilogue
   uint64_t best[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
-  for (; blk < nblk; blk += gridDim.x) {
-    const int nxt = blk + gridDim.x;
-    uint4 qn[kIt];
-    float scn[WF == HSD_W_Q4 ? kIt : 1], bin[WF == HSD_W_Q4 ? kIt : 1];
-    // the next block's pieces in flight (past the last block: the last one again, unused;
-    // no load sits under a branch, which would make the compiler wait for the current ones)
-    load_block(min(nxt, nblk - 1), qn, scn, bin);
+  auto do_block = [&](int blk_, const uint4 (&qq)[kIt], const float (&ss)[kSc], const float (&bb)[kSc]) {
     float pr[NB][kRW];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         const bool use = p0 < npw;
         const int p = min(p0, npw - 1);
         const int prow = p / NPr, j = p - prow * NPr;
-        const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
+        const uint32_t qw[4] = {qq[it].x, qq[it].y, qq[it].z, qq[it].w};
         if constexpr (WF == HSD_W_Q4) {
           uint32_t wc[4][4];
 #pragma unroll
@@ -298,7 +301,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
             wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
             wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
           }
-          const float s16 = 16.0f * sc[it], bo = fmaf(-16.0f, sc[it], bi[it]);
+          const float s16 = 16.0f * ss[it], bo = fmaf(-16.0f, ss[it], bb[it]);
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
             float acc = 0.0f;
@@ -328,7 +331,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         }
       }
     }
-    // ---- row sums and the epilogue: lane b*kRW + r writes row r of token row b
+    // row sums: lane b*kRW + r ends with row r of token row b
     float outv = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -348,12 +351,11 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
       }
     }
     const int ob = lane / kRW, orr = lane - ob * kRW;
-    const int o = blk * kRows + kRW * wave + orr;
+    const int o = blk_ * kRows + kRW * wave + orr;
     if constexpr (YK == HSD_Y_ARGMAX) {
       const uint16_t lb = f32_to_bf16_bits(outv);
-      uint64_t key = lane < NB * kRW ? argmax_key(lb, o) : 0;
+      const uint64_t key = lane < NB * kRW ? argmax_key(lb, o) : 0;
       if (a.y && lane < NB * kRW) reinterpret_cast<uint16_t*>(a.y)[ob * a.y_ld + o] = lb;
-      // best per token row over the wave's rows (lanes ob*kRW .. ob*kRW + kRW-1)
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         uint64_t kb = 0;
@@ -376,10 +378,27 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(outv);
       }
     }
+  };
+
+  if ((int)gridDim.x >= nblk) {
+    do_block(blk, q, sc, bi);                          // one block per workgroup
+  } else {
+    // several blocks: the next block's pieces are in flight while one is computed; the
+    // load is unconditional (the last block re-reads its own lines), so the compiler's
+    // wait before the arithmetic counts only the current block's loads
+    for (;;) {
+      const int nxt = blk + (int)gridDim.x;
+      uint4 qn[kIt];
+      float scn[kSc], bin[kSc];
+      load_block(nxt < nblk ? nxt : blk, qn, scn, bin);
+      do_block(blk, q, sc, bi);
+      if (nxt >= nblk) break;
+      blk = nxt;
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      q[it] = qn[it];
-      if constexpr (WF == HSD_W_Q4) { sc[it] = scn[it]; bi[it] = bin[it]; }
+      for (int it = 0; it < kIt; ++it) {
+        q[it] = qn[it];
+        if constexpr (WF == HSD_W_Q4) { sc[it] = scn[it]; bi[it] = bin[it]; }
+      }
     }
   }
   if constexpr (YK == HSD_Y_ARGMAX) {

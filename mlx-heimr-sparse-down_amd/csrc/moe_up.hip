@@ -50,10 +50,13 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 // The router's top-k (the gate of mlx-lm's NemotronH MoE, model.py:115; restated from the
-// model family's published gate): score = sigmoid(logit) in fp32, choice = score + bias;
-// the topk largest choices in descending order (equal choices: the smaller expert id);
-// gain_k = score_k / (sum of the selected scores + 1e-20) * scale (norm_topk), else
-// score_k * scale. Every lane ends with the same sel[] and gain[]. E <= 256.
+// model family's published gate): score = sigmoid(logit) in fp32, choice = score + bias
+// (a NaN choice ranks below every number); the topk largest choices in descending order
+// (equal choices: the smaller expert id); gain_k = score_k / (sum of the selected scores +
+// 1e-20) * scale (norm_topk), else score_k * scale. E <= 256.
+// Each workgroup ranks the E choices itself (a choice's rank = the number of choices
+// before it in that order; thread e counts over the E choices in LDS), so no wavefront
+// reduction chain sits in front of the weight loads.
 struct Router {
   const uint16_t* logits;   // [B, E] bf16
   const float* bias;        // [E] f32 (nullable)
@@ -63,52 +66,39 @@ struct Router {
   int norm_topk;
 };
 constexpr int kMaxTopk = 8;
+constexpr int kMaxE = 256;
 
-__device__ __forceinline__ uint32_t f32_order(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ void route_topk(const Router& rt, int b, int E, int topk, int lane, int (&sel)[kMaxTopk],
-                           float (&gain)[kMaxTopk]) {
-  uint64_t kk[4];
-  float sg[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int e = lane + 64 * v;
-    const bool valid = e < E;
-    const int ec = valid ? e : 0;
-    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + ec]);
-    const float bi = rt.bias ? rt.bias[ec] : 0.0f;
-    sg[v] = 1.0f / (1.0f + expf(-x));
-    const float c = sg[v] + bi;
-    kk[v] = valid ? ((uint64_t)f32_order(c) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e) : 0;
+// sel[0..topk) and gain[0..topk) of token b into LDS (every thread of the workgroup calls it)
+__device__ __forceinline__ void route_topk(const Router& rt, int b, int E, int topk, int tid, float* chs, float* scs,
+                                           int* tsel, float* tgain) {
+  if (tid < E) {
+    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + tid]);
+    const float sg = 1.0f / (1.0f + expf(-x));
+    const float c = sg + (rt.bias ? rt.bias[tid] : 0.0f);
+    chs[tid] = c != c ? -INFINITY : c;
+    scs[tid] = sg;
   }
-  float ssum = 0.0f;
-  float sc[kMaxTopk];
-  for (int k = 0; k < topk; ++k) {
-    uint64_t m = kk[0];
-#pragma unroll
-    for (int v = 1; v < 4; ++v) m = kk[v] > m ? kk[v] : m;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(m >> 32), off, 64) << 32) |
-                         (uint32_t)__shfl_xor((int)(uint32_t)m, off, 64);
-      m = o > m ? o : m;
+  lds_barrier();
+  if (tid < E) {
+    const float v = chs[tid];
+    int r = 0;
+    for (int e = 0; e < E; e += 4) {                 // E % 4 == 0
+      const float4 c4 = *reinterpret_cast<const float4*>(&chs[e]);
+      r += (c4.x > v || (c4.x == v && e < tid)) ? 1 : 0;
+      r += (c4.y > v || (c4.y == v && e + 1 < tid)) ? 1 : 0;
+      r += (c4.z > v || (c4.z == v && e + 2 < tid)) ? 1 : 0;
+      r += (c4.w > v || (c4.w == v && e + 3 < tid)) ? 1 : 0;
     }
-    const int e = (int)(0xFFFFFFFFu - (uint32_t)m);
-    const int v = e >> 6;
-    float mine = sg[0];
-#pragma unroll
-    for (int vv = 1; vv < 4; ++vv) mine = v == vv ? sg[vv] : mine;
-    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
-#pragma unroll
-    for (int vv = 0; vv < 4; ++vv) kk[vv] = kk[vv] == m ? 0 : kk[vv];
-    sel[k] = e;
-    sc[k] = s;
-    ssum += s;
+    if (r < topk) tsel[r] = tid;
   }
-  for (int k = 0; k < topk; ++k) gain[k] = rt.norm_topk ? sc[k] / (ssum + 1e-20f) * rt.scale : sc[k] * rt.scale;
+  lds_barrier();
+  if (tid < topk) {
+    float ssum = 0.0f;
+    for (int k = 0; k < topk; ++k) ssum += scs[tsel[k]];
+    const float s = scs[tsel[tid]];
+    tgain[tid] = rt.norm_topk ? s / (ssum + 1e-20f) * rt.scale : s * rt.scale;
+  }
+  lds_barrier();
 }
 
 template <bool ROUTE>
@@ -142,20 +132,15 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
     xv[i] = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid + kUpThreads * i, NW - 1)];
   int e;
   if constexpr (ROUTE) {
-    int rsel[kMaxTopk];
-    float rgain[kMaxTopk];
-    route_topk(rt, b, E, topk, lane, rsel, rgain);
-    e = 0;
-    for (int i = 0; i < topk; ++i) e = (routed && i == k) ? rsel[i] : e;
+    __shared__ __attribute__((aligned(16))) float chs[kMaxE];
+    __shared__ float scs[kMaxE];
+    __shared__ int tsel[kMaxTopk];
+    __shared__ float tgain[kMaxTopk];
+    route_topk(rt, b, E, topk, tid, chs, scs, tsel, tgain);
+    e = routed ? tsel[k] : 0;
     if (blk == 0 && tid <= topk) {                     // one writer per token row
-      float gv = 1.0f;
-      int sv = 0;
-      for (int i = 0; i < topk; ++i) {
-        gv = i == tid ? rgain[i] : gv;
-        sv = i == tid ? rsel[i] : sv;
-      }
-      if (tid < topk) rt.sel_out[b * topk + tid] = sv;
-      rt.gains_out[b * (topk + 1) + tid] = gv;
+      if (tid < topk) rt.sel_out[b * topk + tid] = tsel[tid];
+      rt.gains_out[b * (topk + 1) + tid] = tid < topk ? tgain[tid] : 1.0f;
     }
   } else {
     e = routed ? sel[b * topk + k] : 0;
@@ -282,6 +267,21 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   if (!ok && tid == 0 && f0 == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
 }
 
+// The router's top-k alone: one workgroup per token row writes sel and gains (the shared
+// expert's gain 1.0 last).
+__global__ __launch_bounds__(kUpThreads) void k_router_topk(Router rt, int E, int topk) {
+  __shared__ __attribute__((aligned(16))) float chs[kMaxE];
+  __shared__ float scs[kMaxE];
+  __shared__ int tsel[kMaxTopk];
+  __shared__ float tgain[kMaxTopk];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  route_topk(rt, b, E, topk, tid, chs, scs, tsel, tgain);
+  if (tid <= topk) {
+    if (tid < topk) rt.sel_out[b * topk + tid] = tsel[tid];
+    rt.gains_out[b * (topk + 1) + tid] = tid < topk ? tgain[tid] : 1.0f;
+  }
+}
+
 }  // namespace
 }  // namespace hsd
 
@@ -325,10 +325,11 @@ extern "C" int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t
   if (!x || !logits || !sel || !gains || !w1 || !s1 || !b1 || !sw1 || !ss1 || !sb1 || !hcat)
     return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (x_dtype != HSD_DT_BF16) return set_error(HSD_ERR_DTYPE, "%s: x must be bf16", fn);
-  if (B < 0 || topk <= 0 || topk > kMaxTopk || E < topk || E > 256 || D <= 0 || D % 64 || D > kUpMaxD || F <= 0 ||
-      F % 64 || FS <= 0 || FS % 64)
-    return set_error(HSD_ERR_SHAPE, "%s: need topk <= %d <= E <= 256, D %% 64 == 0, D <= %d, F and FS %% 64 == 0", fn,
-                     kMaxTopk, kUpMaxD);
+  if (B < 0 || topk <= 0 || topk > kMaxTopk || E < topk || E > kMaxE || E % 4 || D <= 0 || D % 64 || D > kUpMaxD ||
+      F <= 0 || F % 64 || FS <= 0 || FS % 64)
+    return set_error(HSD_ERR_SHAPE,
+                     "%s: need topk <= %d, topk <= E <= %d, E %% 4 == 0, D %% 64 == 0, D <= %d, F and FS %% 64 == 0", fn,
+                     kMaxTopk, kMaxE, kUpMaxD);
   if (B > 65535 || E * F * (D / 8) >= ((int64_t)1 << 40)) return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
   const uintptr_t al = (uintptr_t)x | (uintptr_t)w1 | (uintptr_t)sw1 | (uintptr_t)s1 | (uintptr_t)b1 |
                        (uintptr_t)ss1 | (uintptr_t)sb1;
@@ -341,5 +342,17 @@ extern "C" int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t
                      reinterpret_cast<const uint16_t*>(x), nullptr, w1, s1, b1, sw1, ss1, sb1,
                      reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, (int)D, (int)F, (int)FS, (int)topk,
                      (int)E, rt);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_router_topk(const uint16_t* logits, const float* e_bias, float routed_scale, int norm_topk,
+                               int32_t* sel, float* gains, int64_t B, int64_t E, int64_t topk, void* stream) {
+  const char* fn = "hsd_router_topk";
+  if (!logits || !sel || !gains) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (B < 0 || B > 65535 || topk <= 0 || topk > kMaxTopk || E < topk || E > kMaxE || E % 4)
+    return set_error(HSD_ERR_SHAPE, "%s: need topk <= %d, topk <= E <= %d, E %% 4 == 0", fn, kMaxTopk, kMaxE);
+  if (B == 0) return HSD_OK;
+  Router rt{logits, e_bias, sel, gains, routed_scale, norm_topk};
+  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)B), dim3(kUpThreads), 0, as_stream(stream), rt, (int)E, (int)topk);
   return check_launch(fn);
 }

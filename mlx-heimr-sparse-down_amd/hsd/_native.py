@@ -58,6 +58,7 @@ _SIGS = {
                          + [_c_i64] * 6 + [_vp, _vp, _vp]),
     "hsd_moe_route_up_relu2": (_c_int, [_vp, _c_int, _vp, _vp, _c_float, _c_int, _vp, _vp] + [_vp] * 7
                                + [_c_i64] * 6 + [_vp, _vp]),
+    "hsd_router_topk": (_c_int, [_vp, _vp, _c_float, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "hsd_sparse_down_residual": (_c_int, [_vp, _c_int] + [_vp] * 10 + [_c_i64] * 6 + [_c_int, _vp, _vp, _vp,
                                                                                       _c_size, _vp]),
     "hsd_linear_argmax_slots": (_c_i64, [_c_i64, _c_int]),

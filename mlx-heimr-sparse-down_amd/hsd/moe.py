@@ -124,7 +124,7 @@ class MoEDown:
         return x + y.to(x.dtype)
 
 
-def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, status=None):
+def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, status=None, out=None):
     """The front end after the router (model.py:110-121) in pack's layout: x [B, D] bf16
     (the normed token), inds [B, topk] -> hcat [B, topk*F + FS] bf16 = square(relu(x W^T))
     of each selected expert's up projection (w1 [E, F, D/8] u32, s1/b1 [E, F, D/64] bf16,
@@ -139,11 +139,12 @@ def up_relu2(x, inds, w1, s1, b1, sw1, ss1, sb1, *, topk, live_masks=None, statu
     E, F = w1.shape[0], w1.shape[1]
     FS = sw1.shape[0]
     NR = topk * F + FS
-    hcat = torch.empty((B, NR), dtype=torch.bfloat16, device=x.device)
+    hcat = out if out is not None else torch.empty((B, NR), dtype=torch.bfloat16, device=x.device)
     if live_masks is not None and (live_masks.dtype != torch.int64 or not live_masks.is_contiguous()
                                    or live_masks.numel() < B * (NR // 64)):
         raise N.HSDError("live_masks must be a contiguous int64 tensor of B*(topk*F + FS)/64 entries")
-    N.call("hsd_moe_up_relu2", N.ptr(x), N.dtype_tag(x.dtype), N.ptr(N.contig(inds.to(torch.int32))),
+    inds = inds if inds.dtype == torch.int32 and inds.is_contiguous() else N.contig(inds.to(torch.int32))
+    N.call("hsd_moe_up_relu2", N.ptr(x), N.dtype_tag(x.dtype), N.ptr(inds),
            N.ptr(N.as_words(N.contig(w1))), N.ptr(N.contig(s1)), N.ptr(N.contig(b1)),
            N.ptr(N.as_words(N.contig(sw1))), N.ptr(N.contig(ss1)), N.ptr(N.contig(sb1)), N.ptr(hcat),
            B, D, F, FS, topk, E, N.ptr(live_masks), N.ptr(status), N.stream(x.device))
@@ -173,6 +174,18 @@ def route_up_relu2(x, logits, e_bias, w1, s1, b1, sw1, ss1, sb1, *, topk, routed
            N.ptr(N.contig(b1)), N.ptr(N.as_words(N.contig(sw1))), N.ptr(N.contig(ss1)), N.ptr(N.contig(sb1)),
            N.ptr(hcat), B, D, F, FS, topk, E, N.ptr(live_masks), N.stream(x.device))
     return hcat, sel, gains
+
+
+def router_topk(logits, e_bias, *, topk, routed_scale=1.0, norm_topk=True, sel=None, gains=None):
+    """The router's selection from the gate's logits [B, E] bf16 (model.py:115): -> (sel
+    [B, topk] int32, gains [B, topk+1] f32), by route_up_relu2's rule."""
+    logits = N.contig(logits)
+    B, E = logits.shape
+    sel = sel if sel is not None else torch.empty((B, topk), dtype=torch.int32, device=logits.device)
+    gains = gains if gains is not None else torch.empty((B, topk + 1), dtype=torch.float32, device=logits.device)
+    N.call("hsd_router_topk", N.ptr(logits), N.ptr(e_bias), float(routed_scale), 1 if norm_topk else 0, N.ptr(sel),
+           N.ptr(gains), B, E, topk, N.stream(logits.device))
+    return sel, gains
 
 
 def build_layouts(blocks, single_layout=True):

@@ -502,6 +502,7 @@ def router_topk(logits, bias, topk, scale=1.0, norm_topk=True):
     B, E = lg.shape
     sc = sigmoid_f32(lg)
     ch = (sc + (np.zeros(E, np.float32) if bias is None else np.asarray(bias, np.float32))).astype(np.float32)
+    ch = np.where(np.isnan(ch), np.float32(-np.inf), ch)          # a NaN choice ranks last
     sel = np.zeros((B, topk), dtype=np.int32)
     gains = np.zeros((B, topk), dtype=np.float64)
     for r in range(B):
@@ -510,6 +511,74 @@ def router_topk(logits, bias, topk, scale=1.0, norm_topk=True):
         sv = sc[r, order].astype(np.float64)
         gains[r] = sv / (sv.sum() + 1e-20) * scale if norm_topk else sv * scale
     return sel, gains
+
+
+# ------------------------------------- one decode row through the hybrid's blocks
+def _vals(bits):
+    return bf16_to_f32(np.asarray(bits, dtype=np.uint16)).astype(np.float64)
+
+
+def residual_add_bf16(x_bits, y):
+    """x + mixer(x) in bf16 (model.py:139, mamba.py:44): bf16(x + bf16(y)) -> bits."""
+    return f32_to_bf16((_vals(x_bits) + round_bf16(np.asarray(y, np.float32)).astype(np.float64)).astype(np.float32))
+
+
+def mamba_block_step(x_bits, w, conv_state, ssm_state, *, n_groups=8, eps=1e-5):
+    """One decode row through a Mamba-2 block (mamba.py:19-44 with L = 1): rms_norm,
+    in_proj (4-bit), split gate | conv input | dt, the conv + SSM step (mamba_verify), the
+    gated RMSNorm, out_proj (4-bit), the residual add. w: norm_w, in_w/in_s/in_b, out_w/
+    out_s/out_b, conv_w, conv_b (bf16 values), A_log, dt_bias, D, gnorm_w. -> (x bits,
+    conv_state, ssm_state)."""
+    xn = rms_norm_bf16(_vals(x_bits), _vals(w["norm_w"]), eps)
+    proj = round_bf16(linear_q4(_vals(xn)[None], w["in_w"], w["in_s"], w["in_b"]).astype(np.float32))[0]
+    H = np.asarray(w["A_log"]).shape[0]
+    DI = np.asarray(w["gnorm_w"]).shape[0]
+    CD = np.asarray(w["conv_b"]).shape[0]
+    gate, cin, dt = proj[:DI], proj[DI:DI + CD], proj[DI + CD:DI + CD + H]
+    out = mamba_verify(cin[None], dt[None], gate[None], w["conv_w"], w["conv_b"], w["A_log"], w["dt_bias"], w["D"],
+                       np.ones(DI), conv_state, ssm_state, n_groups=n_groups, eps=eps)
+    g = gated_rms_norm_bf16(out["y_pre"], gate[None], _vals(w["gnorm_w"]), eps, DI // n_groups)
+    y = linear_q4(_vals(g), w["out_w"], w["out_s"], w["out_b"])[0]
+    return residual_add_bf16(x_bits, y), out["conv_states"][0], out["ssm_states"][0]
+
+
+def attn_block_step(x_bits, w, k_cache, v_cache, *, n_heads, n_kv_heads, head_dim=128, eps=1e-5):
+    """One decode row through the attention block at position P = k_cache.shape[1]
+    (model.py:287): rms_norm, the q|k|v projection (4-bit), the new key/value appended,
+    scaled dot-product attention over keys 0..P (bf16 output), o_proj (4-bit), residual.
+    k_cache/v_cache [HKV, P, HD] values. -> (x bits, k_cache, v_cache) with P + 1 rows."""
+    xn = rms_norm_bf16(_vals(x_bits), _vals(w["norm_w"]), eps)
+    qkv = round_bf16(linear_q4(_vals(xn)[None], w["qkv_w"], w["qkv_s"], w["qkv_b"]).astype(np.float32))[0]
+    QD, KD = n_heads * head_dim, n_kv_heads * head_dim
+    q = qkv[:QD].reshape(n_heads, head_dim)
+    k = np.concatenate([k_cache, qkv[QD:QD + KD].reshape(n_kv_heads, 1, head_dim)], axis=1)
+    v = np.concatenate([v_cache, qkv[QD + KD:QD + 2 * KD].reshape(n_kv_heads, 1, head_dim)], axis=1)
+    o = round_bf16(attention(q, k, v, 1.0 / np.sqrt(head_dim)).reshape(-1).astype(np.float32))
+    y = linear_q4(o[None], w["o_w"], w["o_s"], w["o_b"])[0]
+    return residual_add_bf16(x_bits, y), k, v
+
+
+def moe_block_step(x_bits, w, *, topk, routed_scale, norm_topk=True, eps=1e-5):
+    """One decode row through the MoE block (model.py:110-139): rms_norm, the bf16 gate
+    and the router (router_topk), the selected and shared 4-bit up projections with
+    ReLU^2 (up_relu2), the sparse down projection on the neuron-major layout
+    (sparse_down), the residual add. -> x bits."""
+    xn = rms_norm_bf16(_vals(x_bits), _vals(w["norm_w"]), eps)
+    logits = round_bf16(linear_bf16(_vals(xn)[None], w["gate"]).astype(np.float32))
+    sel, g = router_topk(logits, w["e_bias"], topk, routed_scale, norm_topk)
+    gains = np.concatenate([g.astype(np.float32), np.ones((1, 1), np.float32)], axis=1)
+    F, FS = w["w1"].shape[1], w["sw1"].shape[0]
+    hcat = up_relu2(xn[None], sel, w["w1"], w["s1"], w["b1"], w["sw1"], w["ss1"], w["sb1"], F=F, FS=FS, topk=topk)
+    D = w["pw"].shape[2] * 8
+    y = sparse_down(bf16_to_f32(hcat), sel, gains, w["pw"], w["ps"], w["pb"], w["spw"], w["sps"], w["spb"], F=F,
+                    FS=FS, D=D, topk=topk)[0]
+    return residual_add_bf16(x_bits, y)
+
+
+def lm_head_logits(x_bits, norm_f, w, s, b, eps=1e-5):
+    """lm_head(norm_f(x)) (model.py:229-230) in float64 from the bf16 normed row."""
+    xn = rms_norm_bf16(_vals(x_bits), _vals(norm_f), eps)
+    return linear_q4(_vals(xn)[None], w, s, b)[0]
 
 
 PINNING = {
@@ -542,6 +611,9 @@ PINNING = {
     "embed_q4": "closed form: one dequantised row, exactly representable values round trip",
     "attention": "closed forms: one visible key returns its value row; equal keys average the value "
                  "rows; a dominant key selects its value row; GQA head grouping",
+    "mamba_block_step / attn_block_step / moe_block_step / lm_head_logits": "compositions of the pinned "
+                                                                              "functions above in the blocks' "
+                                                                              "order (model.py, mamba.py)",
     "router_topk": "brute force over every subset of size topk on small E; normalised gains sum to the "
                    "scale; order and tie rule by construction. The gate's exact form in mlx-lm 0.31.3 "
                    "(nemotron_h) is not in the container: parity unpinned against it",

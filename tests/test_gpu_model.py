@@ -127,3 +127,79 @@ def test_verify_rollback_equals_single_steps(model):
         assert len(sa) == len(sb)
         for u, v in zip(sa, sb):
             assert torch.equal(u.view(torch.uint8), v.view(torch.uint8))
+
+
+def host_weights(model):
+    """The reduced model's weights as host arrays in the oracle's conventions."""
+    from hsd import synth as S
+    u32 = lambda t: S.to_host(t).view(np.uint32)
+    out = []
+    for t, blk in zip(model.cfg.pattern, model.blocks):
+        if t == "M":
+            m = blk.mixer
+            out.append(dict(norm_w=S.to_host(blk.norm_w), in_w=u32(blk.in_proj.w), in_s=S.to_host(blk.in_proj.scales),
+                            in_b=S.to_host(blk.in_proj.biases), out_w=u32(blk.out_proj.w),
+                            out_s=S.to_host(blk.out_proj.scales), out_b=S.to_host(blk.out_proj.biases),
+                            conv_w=m.conv_w.float().cpu().numpy(), conv_b=m.conv_b.float().cpu().numpy(),
+                            A_log=m.A_log.cpu().numpy(), dt_bias=m.dt_bias.cpu().numpy(), D=m.D.cpu().numpy(),
+                            gnorm_w=S.to_host(m.norm_w)))
+        elif t == "*":
+            out.append(dict(norm_w=S.to_host(blk.norm_w), qkv_w=u32(blk.qkv.w), qkv_s=S.to_host(blk.qkv.scales),
+                            qkv_b=S.to_host(blk.qkv.biases), o_w=u32(blk.o_proj.w), o_s=S.to_host(blk.o_proj.scales),
+                            o_b=S.to_host(blk.o_proj.biases)))
+        else:
+            out.append(dict(norm_w=S.to_host(blk.norm_w), gate=S.to_host(blk.gate.w), e_bias=blk.e_bias.cpu().numpy(),
+                            w1=u32(blk.w1), s1=S.to_host(blk.s1), b1=S.to_host(blk.b1), sw1=u32(blk.sw1),
+                            ss1=S.to_host(blk.ss1), sb1=S.to_host(blk.sb1), pw=u32(blk.pw), ps=S.to_host(blk.ps),
+                            pb=S.to_host(blk.pb), spw=u32(blk.spw), sps=S.to_host(blk.sps), spb=S.to_host(blk.spb)))
+    return out
+
+
+def test_decode_step_matches_oracle(model):
+    """One decode step of the whole reduced model against the oracle's composition of the
+    blocks (float64 sums, bf16 activations between ops), from the GPU's caches after the
+    prompt: the final hidden row and the logits within 3e-2 of their scale, and the same
+    greedy token unless the top two logits are closer than that."""
+    from hsd import synth as S
+    from oracle import hsd_oracle as O
+    c = model.cfg
+    model.set_mode("sparse")
+    cache = model.make_cache(cap=8)
+    x_last = model.prefill(PROMPT, cache, with_head=False, graph=False)
+    model._first_token(x_last, cache)
+    torch.cuda.synchronize()
+    seq = cache.state()
+    tok0, P, cur = seq[N.SEQ_TOK], seq[N.SEQ_POS], seq[N.SEQ_CUR]
+    states = []
+    for t, lc in zip(c.pattern, cache.layers):
+        if t == "M":
+            states.append((lc.conv[cur].float().cpu().numpy(), lc.ssm[cur].cpu().numpy()))
+        elif t == "*":
+            states.append((lc.k[:, :P].float().cpu().numpy(), lc.v[:, :P].float().cpu().numpy()))
+        else:
+            states.append(None)
+    model._decode_step(cache)
+    buf = model._bufs[1]
+    x_gpu = buf["x"].float().cpu().numpy()[0]
+    logits_gpu = model.logits(buf["x"]).float().cpu().numpy()[0]
+    torch.cuda.synchronize()
+    # the oracle from the same token and states
+    E = model.embedding
+    x = O.embed_q4(np.array([tok0]), S.to_host(E.w).view(np.uint32), S.to_host(E.scales), S.to_host(E.biases))[0]
+    for t, w, st in zip(c.pattern, host_weights(model), states):
+        if t == "M":
+            x, _, _ = O.mamba_block_step(x, w, st[0], st[1], n_groups=c.n_groups, eps=c.eps)
+        elif t == "*":
+            x, _, _ = O.attn_block_step(x, w, st[0], st[1], n_heads=c.attn_heads, n_kv_heads=c.kv_heads, eps=c.eps)
+        else:
+            x = O.moe_block_step(x, w, topk=c.topk, routed_scale=c.routed_scale, eps=c.eps)
+    x_ref = O.bf16_to_f32(x)
+    lg = O.lm_head_logits(x, S.to_host(model.norm_f), S.to_host(model.lm_head.w).view(np.uint32),
+                          S.to_host(model.lm_head.scales), S.to_host(model.lm_head.biases), c.eps)
+    ex = np.abs(x_gpu - x_ref).max() / np.abs(x_ref).max()
+    el = np.abs(logits_gpu - lg).max() / np.abs(lg).max()
+    print(f"decode step vs oracle: hidden max rel err {ex:.2e}, logits {el:.2e}")
+    assert ex <= 3e-2 and el <= 3e-2
+    top = np.sort(lg)[::-1]
+    if top[0] - top[1] > 6e-2 * np.abs(lg).max():
+        assert int(np.argmax(logits_gpu)) == int(np.argmax(lg))

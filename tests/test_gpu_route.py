@@ -47,6 +47,9 @@ def test_router_topk_and_front_end(dev, up, B):
         assert sel_h[r].tolist() == rsel[r].tolist()
         assert np.allclose(g_h[r, :K], rg[r], rtol=1e-6, atol=0)
         assert g_h[r, K] == 1.0
+    # the router alone gives the same selection and gains
+    s2, g2 = moe.router_topk(S.to_device(logits, dev), torch.from_numpy(bias).to(dev), topk=K, routed_scale=2.5)
+    assert torch.equal(s2, sel) and torch.equal(g2.view(torch.int32), gains.view(torch.int32))
     # the up projection with those experts is hsd_moe_up_relu2's, bit for bit
     h2 = moe.up_relu2(xd, sel, ud["w1"], ud["s1"], ud["b1"], ud["sw1"], ud["ss1"], ud["sb1"], topk=K)
     assert torch.equal(hcat.view(torch.int16), h2.view(torch.int16))
