@@ -26,6 +26,9 @@
 #include "hsd_common.h"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace hsd {
 namespace {
@@ -57,15 +60,13 @@ __device__ __forceinline__ uint64_t argmax_key(uint16_t bits, int idx) {
 
 template <int WF> struct WTraits;
 template <> struct WTraits<HSD_W_Q4> {
-  static constexpr int kRW = 2;                         // rows per wavefront
   static constexpr int kIn = 32;                        // inputs per 16-byte piece
 };
 template <> struct WTraits<HSD_W_BF16> {
-  static constexpr int kRW = 1;
   static constexpr int kIn = 8;
 };
-// pieces per lane for rows of up to I inputs
-template <int WF> constexpr int pieces_per_lane(int I) { return (WTraits<WF>::kRW * (I / WTraits<WF>::kIn) + 63) / 64; }
+// pieces per lane for RW rows of up to I inputs per wavefront
+template <int WF> constexpr int pieces_per_lane(int RW, int I) { return (RW * (I / WTraits<WF>::kIn) + 63) / 64; }
 
 struct LinArgs {
   const void* x;
@@ -85,6 +86,7 @@ struct LinArgs {
   int64_t xn_ld;
   uint64_t* keys;
   int64_t key_ld;
+  int key_slots;
   int O, I;
 };
 
@@ -99,16 +101,18 @@ __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0
 
 // IMAX: the largest row length the instance serves (kIt weight pieces per lane, XIT x
 // words of 8 inputs per thread in the prologue).
-template <int WF, int NB, int XK, int YK, int IMAX>
+// RW: output rows per wavefront (a block = 4 RW rows).
+template <int WF, int NB, int XK, int YK, int IMAX, int RW>
 __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   using T = WTraits<WF>;
-  constexpr int kRW = T::kRW, kIt = pieces_per_lane<WF>(IMAX);
+  constexpr int kRW = RW, kIt = pieces_per_lane<WF>(RW, IMAX);
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   constexpr int kRows = 4 * kRW;                       // rows per block
   constexpr int kSc = WF == HSD_W_Q4 ? kIt : 1;
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
   // LDS: x as bf16 pairs [NB][I/2] (4-bit: pairs (x[i], x[i+4]) in a word's nibble
-  // order; bf16: natural pairs), then the 32-input piece sums [NB][I/32] (4-bit only)
+  // order, word m of 32-input piece j at [m][j]; bf16: natural pairs), then the 32-input
+  // piece sums [NB][I/32] (4-bit only)
   __shared__ float wsum[NB][4];
   __shared__ uint64_t kbest[4][NB];
   const int I = a.I, O = a.O, NW = I / 8;
@@ -139,10 +143,6 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
       }
     }
   };
-  uint4 q[kIt];
-  float sc[kSc], bi[kSc];
-  int blk = blockIdx.x;
-  load_block(blk, q, sc, bi);
 
   // ---- prologue: this workgroup's copy of the NB input rows, normalised if asked
   // words t = tid + 256 i hold inputs 8t .. 8t+7
@@ -165,6 +165,12 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
     }
     if constexpr (XK != HSD_X_BF16) nwv[i] = reinterpret_cast<const uint4*>(a.nw)[tc];
   }
+  // the first block's weight pieces, issued after x: the prologue waits for x only (loads
+  // complete in issue order), while the weights are still on their way
+  uint4 q[kIt];
+  float sc[kSc], bi[kSc];
+  int blk = blockIdx.x;
+  load_block(blk, q, sc, bi);
   // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
   uint32_t xo[NB][XIT][4];
   if constexpr (XK == HSD_X_BF16) {
@@ -184,9 +190,8 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float v0 = tv ? lo_f(xw[c]) : 0.0f, v1 = tv ? hi_f(xw[c]) : 0.0f;
-          ss = fmaf(v0, v0, ss);
-          ss = fmaf(v1, v1, ss);
+          const uint32_t v = tv ? xw[c] : 0u;
+          ss = dot2_bf16(v, v, ss);
         }
       }
       ss = wave_sum_dpp(ss);
@@ -255,17 +260,17 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         } else {
           pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
         }
-        *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * t]) = pr;
+        // 4-bit: word m of piece j at [m][j] (lanes holding consecutive pieces then read
+        // consecutive 16-byte words, free of bank conflicts); bf16: word t at t
+        const int slot = WF == HSD_W_Q4 ? (t & 3) * (I / 32) + (t >> 2) : t;
+        *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * slot]) = pr;
         if (a.xn_out && blockIdx.x == 0)
           reinterpret_cast<uint4*>(a.xn_out + b * a.xn_ld)[t] = make_uint4(w[0], w[1], w[2], w[3]);
       }
       if constexpr (WF == HSD_W_Q4) {
         float s8 = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          s8 += lo_f(w[c]);
-          s8 += hi_f(w[c]);
-        }
+        for (int c = 0; c < 4; ++c) s8 = dot2_bf16(w[c], kBfOne2, s8);
         s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
         s8 += dpp_f32<0x4E>(s8);
         if (t < NW && (t & 3) == 0) xh[b * (I / 32) + (t >> 2)] = s8;
@@ -307,7 +312,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
             float acc = 0.0f;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (4 * j + m) * 4]);
+              const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
               acc = dot2_bf16(xq.x, wc[m][0], acc);
               acc = dot2_bf16(xq.y, wc[m][1], acc);
               acc = dot2_bf16(xq.z, wc[m][2], acc);
@@ -411,6 +416,8 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
 #pragma unroll
       for (int w = 1; w < 4; ++w) k = kbest[w][tid] > k ? kbest[w][tid] : k;
       a.keys[tid * a.key_ld + blockIdx.x] = k;
+      // slots past the grid (the grid follows the occupancy) read as the smallest key
+      for (int sl = blockIdx.x + gridDim.x; sl < a.key_slots; sl += gridDim.x) a.keys[tid * a.key_ld + sl] = 0;
     }
   }
 }
@@ -444,6 +451,28 @@ __global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict
 int linear_grid(int O, int w_kind) {
   const int rows = w_kind == HSD_W_Q4 ? 8 : 4;
   return std::min(O / rows, kLMaxGrid);
+}
+
+// Workgroups of `kernel` that are resident at once on the current device (occupancy x
+// CUs), looked up once per kernel, LDS size and device. A grid no larger than this has no
+// workgroup waiting for another to finish; each workgroup loops over its row blocks.
+std::mutex g_occ_mu;
+std::map<std::tuple<const void*, size_t, int>, int> g_occ;
+
+int resident_workgroups(const void* kernel, size_t lds) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return kLMaxGrid;
+  std::lock_guard<std::mutex> lock(g_occ_mu);
+  auto key = std::make_tuple(kernel, lds, dev);
+  auto it = g_occ.find(key);
+  if (it != g_occ.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  int r = kLMaxGrid;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kLT, lds) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && per_cu > 0 && cus > 0)
+    r = per_cu * cus;
+  g_occ[key] = r;
+  return r;
 }
 
 }  // namespace
@@ -489,15 +518,16 @@ extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_
                      "strides of whole 16-byte pieces", fn);
   if (y_kind != HSD_Y_ARGMAX && y_ld < O) return set_error(HSD_ERR_SHAPE, "%s: y_ld < O", fn);
   if (y_kind == HSD_Y_RESID && res_ld < O) return set_error(HSD_ERR_SHAPE, "%s: res_ld < O", fn);
-  const int grid = linear_grid((int)O, w_kind);
-  if (y_kind == HSD_Y_ARGMAX && key_ld < grid)
-    return set_error(HSD_ERR_SHAPE, "%s: key_ld must be >= hsd_linear_argmax_slots() = %d", fn, grid);
+  const int slots = linear_grid((int)O, w_kind);     // argmax key slots (an upper bound of the grid)
+  if (y_kind == HSD_Y_ARGMAX && key_ld < slots)
+    return set_error(HSD_ERR_SHAPE, "%s: key_ld must be >= hsd_linear_argmax_slots() = %d", fn, slots);
   if (B == 0) return HSD_OK;
   LinArgs a{x, x_ld, gate, gate_ld, norm_w, eps, w, scales, biases, y, y_ld, res, res_ld, xn_out, xn_ld,
-            argmax_keys, key_ld, (int)O, (int)I};
+            argmax_keys, key_ld, slots, (int)O, (int)I};
   const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
   hipStream_t st = as_stream(stream);
   const bool small = I <= 3072;
+  const int grid = slots;
   // the (x_kind, y_kind) pairs this library instantiates
   const int pair = x_kind * 8 + y_kind;
   constexpr int kRB = HSD_X_RMS * 8 + HSD_Y_BF16, kRA = HSD_X_RMS * 8 + HSD_Y_ARGMAX,
@@ -509,9 +539,15 @@ extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_
   if (!ok)
     return set_error(HSD_ERR_SHAPE, "%s: unsupported combination x_kind %d, y_kind %d, w_kind %d", fn, x_kind,
                      y_kind, w_kind);
-#define HSD_LIN(WF, NB, XK, YK, IM) hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM>), dim3(grid), dim3(kLT), lds, st, a)
+#define HSD_LIN(WF, NB, XK, YK, IM)                                                                   \
+  {                                                                                                   \
+    constexpr int RW = WF == HSD_W_Q4 ? 2 : 1;                                                        \
+    const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW>);               \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, lds)));                         \
+    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW>), dim3(g), dim3(kLT), lds, st, a);           \
+  }
 #define HSD_LIN_I(WF, NB, XK, YK)     \
-  if (small) HSD_LIN(WF, NB, XK, YK, 3072); else HSD_LIN(WF, NB, XK, YK, kLMaxI);
+  if (small) HSD_LIN(WF, NB, XK, YK, 3072) else HSD_LIN(WF, NB, XK, YK, kLMaxI)
 #define HSD_LIN_P(WF, NB)                                                  \
   switch (pair) {                                                          \
     case kRB: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_BF16); break;             \

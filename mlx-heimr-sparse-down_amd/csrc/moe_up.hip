@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
     const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
     uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
     int E, Router rt) {
-  // x pairs: piece j, word m, pair n at xp[(4 j + m) 4 + n] = (x[32 j + 8 m + n], x[.. + 4])
+  // x pairs: piece j, word m, pair n at xp[4 (m NP + j) + n] = (x[32 j + 8 m + n], x[.. + 4])
   __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
   __shared__ int nib[kUpWaves];
@@ -181,7 +181,9 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
       pr.y = el(1) | (el(5) << 16);
       pr.z = el(2) | (el(6) << 16);
       pr.w = el(3) | (el(7) << 16);
-      *reinterpret_cast<uint4*>(&xp[4 * t]) = pr;
+      // word m of piece j at [m][j]: lanes holding consecutive pieces read consecutive
+      // 16-byte words (no LDS bank conflicts)
+      *reinterpret_cast<uint4*>(&xp[4 * ((t & 3) * NP + (t >> 2))]) = pr;
     }
     float s8 = 0.0f;
 #pragma unroll
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
       float acc = 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[(4 * j + m) * 4]);
+        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[4 * (m * NP + j)]);
         const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
         // nibble n (bits 4n..4n+3 of each half) to bits 3..6: a left shift by 3 for n = 0,
         // right shifts by 1, 5, 9 for the others
