@@ -15,7 +15,6 @@ bit-identical to L single-row steps.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Callable, Optional
 
 import torch
 
@@ -29,9 +28,8 @@ CONV_K = 4
 class Mamba2Mixer:
     """The parameters of one Mamba-2 mixer (the attributes mamba.py:24-43 reads from
     mlx-lm's mixer): conv_w [CD, K] bf16, conv_b [CD] bf16, A_log / dt_bias / D [H] f32,
-    norm_w [H*P] bf16. in_proj / out_proj are optional callables (x [L, hidden] ->
-    [L, 2*H*P + 2*G*N + H] and [L, H*P] -> [L, hidden]); without in_proj the verify input
-    is the in_proj output itself."""
+    norm_w [H*P] bf16 (the gated RMSNorm's weight). The block around it (pre-norm,
+    in_proj, out_proj) is hsd.model.MambaBlock."""
     conv_w: torch.Tensor
     conv_b: torch.Tensor
     A_log: torch.Tensor
@@ -45,8 +43,6 @@ class Mamba2Mixer:
     norm_group: int = 512
     eps: float = 1e-5
     time_step_limit: tuple = (0.0, float("inf"))
-    in_proj: Optional[Callable] = None
-    out_proj: Optional[Callable] = None
 
     @property
     def intermediate_size(self):
@@ -141,17 +137,28 @@ def ssm_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out=None, status=None)
 
 def mamba_verify(block, x3, cache, records):
     """hsd/mamba.py:19-44. One Mamba-2 block on x3 [1, L, *] with the cache advanced by L
-    rows (per-row checkpoints written), remembering in `records` what mamba_rollback
-    needs. `block` is a Mamba2Mixer or has one as `.mixer`. With in_proj set x3 is the
-    block's input (hidden) and the result is x3 + out_proj(y); without, x3 is the in_proj
-    output and the result is y [1, L, H*P]."""
+    rows (the per-row checkpoints written), remembering in `records` what mamba_rollback
+    needs.
+
+    `block` with the reference's structure -- `.norm_w` (the block pre-norm, mamba.py:25),
+    `.in_proj` / `.out_proj` (4-bit nn.QWeight) and `.mixer` (a Mamba2Mixer), such as
+    hsd.model.MambaBlock: x3 is the block input [1, L, D] and the result is
+    x3 + out_proj(gated_norm(ssm(conv(in_proj(norm(x3)))))) (mamba.py:25-44), in bf16.
+    A bare Mamba2Mixer (the kernel-level form): x3 is the in_proj output
+    [1, L, 2*H*P + 2*G*N + H] and the result the gated-norm output y [1, L, H*P]."""
+    x = N.contig(x3[0])
+    L = x.shape[0]
+    if hasattr(block, "in_proj") and hasattr(block, "norm_w") and hasattr(block, "rows"):
+        m = block.mixer
+        buf = dict(proj=torch.empty((L, block.in_proj.O), dtype=torch.bfloat16, device=x.device),
+                   y_pre=torch.empty((L, m.intermediate_size), dtype=torch.float32, device=x.device))
+        out = x.clone()
+        block.rows(out, buf, cache)
+        records.append((cache, L))
+        return out[None]
     m = getattr(block, "mixer", block)
-    x = x3[0]
-    proj = m.in_proj(x) if m.in_proj is not None else x
-    y = verify_rows(m, proj, cache)
-    records.append((cache, x.shape[0]))
-    if m.out_proj is not None:
-        return x3 + m.out_proj(y)[None]
+    y = verify_rows(m, x, cache)
+    records.append((cache, L))
     return y[None]
 
 

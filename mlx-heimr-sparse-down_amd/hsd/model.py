@@ -238,6 +238,74 @@ class MoEBlock:
                c.n_experts, 1 if dense else 0, None, None, N.ptr(ws), ws.numel(), N.stream(x.device))
         return x
 
+    # ---- the reference's per-block call surface (model.py:110-175) on fresh buffers: any
+    # number of rows, results identical to rows() on the same rows
+    def _front_packed(self, x):
+        c = self.cfg
+        x = N.contig(x)
+        xn = torch.empty_like(x)
+        logits = nn.linear(x, self.gate, norm=self.norm_w, eps=c.eps, xn_out=xn)
+        sel, gains = router_topk(logits, self.e_bias, topk=c.topk, routed_scale=c.routed_scale, norm_topk=c.norm_topk)
+        hcat = up_relu2(xn, sel, self.w1, self.s1, self.b1, self.sw1, self.ss1, self.sb1, topk=c.topk)
+        return hcat, sel, gains
+
+    def front(self, x):
+        """model.py:110-121. x [B, D] bf16 -> (inds [B, topk] int32, scores [B, topk] f32,
+        h [B, topk, F], hs [B, FS]) after ReLU^2 (views of one hcat block)."""
+        c = self.cfg
+        hcat, sel, gains = self._front_packed(x)
+        B, KF = x.shape[0], c.topk * c.moe_inter
+        return sel, gains[:, :c.topk], hcat[:, :KF].view(B, c.topk, c.moe_inter), hcat[:, KF:]
+
+    def pack(self, inds, scores, h, hs):
+        """model.py:123-129 -> (hcat [B, topk*F + FS], sel [B, topk] int32, gains [B, topk+1]
+        f32: the scores, then 1 for the shared expert)."""
+        B = h.shape[0]
+        hcat = torch.cat([h.reshape(B, -1), hs.to(h.dtype)], dim=1).contiguous()
+        gains = torch.cat([scores.float(), torch.ones((B, 1), dtype=torch.float32, device=h.device)], dim=1)
+        return hcat, N.contig(inds.to(torch.int32)), gains.contiguous()
+
+    def _down_residual(self, x, hcat, sel, gains, dense):
+        c = self.cfg
+        B = x.shape[0]
+        out = N.contig(x).clone()
+        nb = N.lib().hsd_sparse_down_workspace_bytes(B, c.hidden, c.moe_inter, c.shared_inter, c.topk)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
+        N.call("hsd_sparse_down_residual", N.ptr(hcat), N.DT_BF16, N.ptr(sel), N.ptr(gains),
+               N.ptr(N.as_words(self.pw)), N.ptr(self.ps), N.ptr(self.pb), N.ptr(N.as_words(self.spw)),
+               N.ptr(self.sps), N.ptr(self.spb), N.ptr(out), N.ptr(out), B, c.hidden, c.moe_inter, c.shared_inter,
+               c.topk, c.n_experts, 1 if dense else 0, None, None, N.ptr(ws), ws.numel(), N.stream(x.device))
+        return out
+
+    def decode_sparse(self, x):
+        """model.py:135-139: x [B, D] -> x + the MoE output, the down projection over the
+        live rows of the neuron-major layout (a new tensor; x is not written)."""
+        return self._down_residual(x, *self._front_packed(x), dense=False)
+
+    def decode_dense(self, x):
+        """model.py:132-133, the dense-h control: the same kernel over every row of the
+        layout (the stock layout is not kept), bit-identical to decode_sparse."""
+        return self._down_residual(x, *self._front_packed(x), dense=True)
+
+    def prefill(self, x, mode="sparse"):
+        """model.py:151-154."""
+        return self.prefill_sparse(x) if mode == "sparse" else self.decode_dense(x)
+
+    def prefill_sparse(self, x, tt=32):
+        """model.py:156-175: x [T, D] -> x + the MoE output, the down projection as the
+        grouped MFMA GEMM over each expert tile's union of live rows (tiles, unions and
+        the GEMM on the device)."""
+        from . import prefill as P
+        c = self.cfg
+        hcat, sel, gains = self._front_packed(x)
+        tiles = P.build_tiles(sel, c.n_experts, tt)
+        union = P.build_union(hcat, tiles[0], tiles[1], F=c.moe_inter, FS=c.shared_inter, topk=c.topk,
+                              E=c.n_experts, tt=tt)
+        y = P.sparse_down_prefill(hcat, sel, gains, self.pw, self.ps, self.pb, self.spw, self.sps, self.spb,
+                                  F=c.moe_inter, FS=c.shared_inter, D=c.hidden, topk=c.topk, E=c.n_experts, tt=tt,
+                                  tiles=tiles, union=union)
+        return x + y.to(x.dtype)
+
     def nbytes(self):
         t = [self.gate.w, self.w1, self.s1, self.b1, self.sw1, self.ss1, self.sb1, self.pw, self.ps, self.pb,
              self.spw, self.sps, self.spb]
@@ -448,17 +516,17 @@ class NemotronModel:
         return out
 
     # ---- the MTP head forward (mtp.py:74-88)
-    def mtp_rows(self, h, toks, buf, cache: ModelCache, pos, keys=None):
+    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None):
         """Head rows: h [B, D] (the target's pre-norm hidden), toks [B] int32 (the token
-        after each row's position) at head-cache positions pos .. pos+B-1. Leaves the
-        normed hidden rows in buf["hn"] and (with keys) the argmax keys of the head's
-        logits."""
+        after each row's position) at positions pos .. pos+B-1 of the head's KV cache kv.
+        Leaves the normed hidden rows in buf["hn"] and (with keys) the argmax keys of the
+        head's logits."""
         B = h.shape[0]
         hd, c = self.mtp, self.cfg
         e = self.embed(toks, out=buf["emb"][:B])
         pair = nn.pair_norm(e, h, hd.enorm, hd.hnorm, eps=c.eps, out=buf["pair"][:B])
         x = nn.linear(pair, hd.eh_proj, out=buf["hx"][:B])
-        hd.attn.rows(x, buf, cache.head_kv, pos)
+        hd.attn.rows(x, buf, kv, pos)
         hd.moe.rows(x, buf, dense=self.mode == "dense")
         if keys is not None:
             nn.linear(x, self.lm_head, norm=hd.final_norm, eps=c.eps, argmax_keys=keys, xn_out=buf["hn"][:B])
@@ -475,7 +543,7 @@ class NemotronModel:
             pend = buf["pend"][:3]
             N.call("hsd_gather_tokens", N.ptr(prompt_dev), T, N.ptr(cache.seq), 1, 3, N.ptr(pend),
                    N.stream(self.device))
-            self.mtp_rows(x, pend, buf, cache, cache.head_pos)
+            self.mtp_rows(x, pend, buf, cache.head_kv, cache.head_pos)
         N.call("hsd_prefill_advance", N.ptr(cache.seq), T, 3, NSLAB, N.stream(self.device))
 
     def prefill(self, tokens, cache: ModelCache, with_head=None, graph=True):
@@ -593,11 +661,11 @@ class NemotronModel:
         c = self.cfg
         st = N.stream(self.device)
         # the head over the rows the last verify confirmed (R of them valid)
-        self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache, cache.head_pos, keys=b3["keys"])
+        self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos, keys=b3["keys"])
         N.call("hsd_mtp_chain", N.ptr(b3["keys"]), b3["keys"].stride(0), self.slots, N.ptr(b3["hn"]),
                b3["hn"].stride(0), c.hidden, N.ptr(cache.seq), N.ptr(b3["d1"]), N.ptr(b1["h2"]), st)
         # the chained call on its own normed hidden row (mtp.py, model.py:411-413)
-        self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache, cache.head_pos2, keys=b1["keys2"])
+        self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"])
         ids = b3["ids"]
         N.call("hsd_draft_ids", N.ptr(b3["d1"]), N.ptr(b1["keys2"]), self.slots, 2, N.ptr(cache.seq),
                N.ptr(script), 0 if script is None else script.numel(), N.ptr(accepts),

@@ -58,13 +58,14 @@ def linear(x, W: QWeight, *, norm=None, eps=1e-5, gate=None, residual=None, out=
     written when out is given). xn_out: receives xn (bf16 [B, I])."""
     B = x.shape[0]
     if B > MAX_ROWS:
-        if argmax_keys is not None or xn_out is not None:
-            raise N.HSDError(f"argmax / xn_out take at most {MAX_ROWS} rows")
+        if argmax_keys is not None:
+            raise N.HSDError(f"argmax takes at most {MAX_ROWS} rows")
         y = out if out is not None else torch.empty((B, W.O), dtype=out_dtype, device=x.device)
         for r in range(0, B, MAX_ROWS):
-            linear(x[r:r + MAX_ROWS], W, norm=norm, eps=eps, gate=None if gate is None else gate[r:r + MAX_ROWS],
-                   residual=None if residual is None else residual[r:r + MAX_ROWS], out=y[r:r + MAX_ROWS],
-                   out_dtype=out_dtype)
+            sl = slice(r, r + MAX_ROWS)
+            linear(x[sl], W, norm=norm, eps=eps, gate=None if gate is None else gate[sl],
+                   residual=None if residual is None else residual[sl], out=y[sl], out_dtype=out_dtype,
+                   xn_out=None if xn_out is None else xn_out[sl])
         return y
     if x.shape[1] != W.I:
         raise N.HSDError(f"linear: x has {x.shape[1]} columns, the weight {W.I} inputs")

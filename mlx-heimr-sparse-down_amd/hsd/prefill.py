@@ -57,10 +57,16 @@ def sparse_down_prefill(h, sel, gains, pw, ps, pb, spw, sps, spb, *, F, FS, D, t
     """hsd/prefill.py:294-321. h [T, topk*F + FS] bf16, sel [T, topk] int32,
     gains [T, topk+1] f32 -> y [T, D] (out_dtype, default h.dtype). tt in {32, 64}:
     slots per tile. nb / kc / nsg are Metal tile knobs, accepted and ignored (the HIP
-    GEMM uses one wavefront per 128-column block (64 for tt=64) and 16-row k-blocks)."""
+    GEMM uses one wavefront per 128-column block (64 for tt=64) and 16-row k-blocks).
+    The GEMM's A operand is bf16: an f16 or f32 h is rounded to bf16 first (the reference
+    rounds its A tile to half, prefill.py:113), so such inputs agree to bf16 precision;
+    the live rows (exact zeros) are the same either way."""
     del nb, nsg
-    if h.dtype != torch.bfloat16:
-        raise N.HSDError("sparse_down_prefill takes bf16 activations (the MFMA operand type)")
+    od = out_dtype or h.dtype
+    if h.dtype in (torch.float16, torch.float32):
+        h = h.to(torch.bfloat16)
+    elif h.dtype != torch.bfloat16:
+        raise N.HSDError("sparse_down_prefill takes bf16, f16 or f32 activations")
     h = N.contig(h)
     T = h.shape[0]
     tile_e, tile_slot = tiles if tiles is not None else build_tiles(sel, E, tt)
@@ -68,7 +74,6 @@ def sparse_down_prefill(h, sel, gains, pw, ps, pb, spw, sps, spb, *, F, FS, D, t
                                                                 topk=topk, E=E, tt=tt, kc=kc)
     NT = tile_e.shape[0]
     gains = N.contig(gains.to(torch.float32))
-    od = out_dtype or h.dtype
     y = torch.empty((T, D), dtype=od, device=h.device)
     ws = _workspace(N.lib().hsd_prefill_gemm_workspace_bytes(T, D, F, FS, topk, E, tt), h.device,
                     workspace)

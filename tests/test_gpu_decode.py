@@ -38,7 +38,7 @@ def run_case(layer, dev, seed, B, zero_frac, out_dtype=torch.float32, h_dtype=to
     return h, sel, gains, hd, y
 
 
-@pytest.mark.parametrize("zero_frac", [0.0, 0.7, 0.9, 0.97, 1.0])
+@pytest.mark.parametrize("zero_frac", [0.0, 0.7, 0.85, 0.9, 0.95, 0.97, 1.0])
 def test_sparse_down_matches_oracle(layer, dev, zero_frac):
     h, sel, gains, hd, y = run_case(layer, dev, 11, 1, zero_frac)
     ref = O.sparse_down(O.bf16_to_f32(h), sel, gains, *layer["nm_np"], **KW)
@@ -119,3 +119,21 @@ def test_dense_stock_comparator(layer, dev):
     ref = O.dense_reference(O.bf16_to_f32(h), sel, gains, lay["w"], lay["s"], lay["b"], lay["sw"], lay["ss"],
                             lay["sb"], **KW)
     assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("zero_frac", [0.85, 0.9, 0.95])
+def test_hot_neurons_match_oracle(layer, dev, zero_frac):
+    """The hot-neuron activation model (a fixed 5 % of each slot's neurons live with
+    p = 0.6, the rest at the rate that keeps the mean zero fraction), B = 3."""
+    rng = np.random.default_rng(15)
+    hot_mask = rng.random(TOPK * F + FS) < 0.05
+    p_hot, p_cold = S.hot_cold_rates(zero_frac)
+    h, sel, gains = S.decode_inputs_np(16, B=3, zero_frac=zero_frac, hot=(hot_mask, p_hot, p_cold))
+    y = decode.sparse_down(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev), *layer["nm"],
+                           out_dtype=torch.float32, **KW)
+    ref = O.sparse_down(O.bf16_to_f32(h), sel, gains, *layer["nm_np"], **KW)
+    yh = y.cpu().numpy()
+    scale = np.abs(ref).max()
+    print(f"hot neurons, zero_frac {zero_frac}: measured {np.mean(h == 0):.3f}, "
+          f"max rel err {np.abs(yh - ref).max() / scale:.2e}")
+    assert np.abs(yh - ref).max() <= 1e-5 * scale

@@ -18,6 +18,8 @@ from hsd import _native as N
 from hsd import model as Mdl
 from hsd import mtp
 
+from . import hostw
+
 pytestmark = pytest.mark.gpu
 CFG = Mdl.ModelConfig(hidden=512, pattern="MEM*EME", vocab=4096, n_experts=16, topk=6, moe_inter=256,
                       shared_inter=512, max_seq=256, mtp=True)
@@ -129,32 +131,6 @@ def test_verify_rollback_equals_single_steps(model):
             assert torch.equal(u.view(torch.uint8), v.view(torch.uint8))
 
 
-def host_weights(model):
-    """The reduced model's weights as host arrays in the oracle's conventions."""
-    from hsd import synth as S
-    u32 = lambda t: S.to_host(t).view(np.uint32)
-    out = []
-    for t, blk in zip(model.cfg.pattern, model.blocks):
-        if t == "M":
-            m = blk.mixer
-            out.append(dict(norm_w=S.to_host(blk.norm_w), in_w=u32(blk.in_proj.w), in_s=S.to_host(blk.in_proj.scales),
-                            in_b=S.to_host(blk.in_proj.biases), out_w=u32(blk.out_proj.w),
-                            out_s=S.to_host(blk.out_proj.scales), out_b=S.to_host(blk.out_proj.biases),
-                            conv_w=m.conv_w.float().cpu().numpy(), conv_b=m.conv_b.float().cpu().numpy(),
-                            A_log=m.A_log.cpu().numpy(), dt_bias=m.dt_bias.cpu().numpy(), D=m.D.cpu().numpy(),
-                            gnorm_w=S.to_host(m.norm_w)))
-        elif t == "*":
-            out.append(dict(norm_w=S.to_host(blk.norm_w), qkv_w=u32(blk.qkv.w), qkv_s=S.to_host(blk.qkv.scales),
-                            qkv_b=S.to_host(blk.qkv.biases), o_w=u32(blk.o_proj.w), o_s=S.to_host(blk.o_proj.scales),
-                            o_b=S.to_host(blk.o_proj.biases)))
-        else:
-            out.append(dict(norm_w=S.to_host(blk.norm_w), gate=S.to_host(blk.gate.w), e_bias=blk.e_bias.cpu().numpy(),
-                            w1=u32(blk.w1), s1=S.to_host(blk.s1), b1=S.to_host(blk.b1), sw1=u32(blk.sw1),
-                            ss1=S.to_host(blk.ss1), sb1=S.to_host(blk.sb1), pw=u32(blk.pw), ps=S.to_host(blk.ps),
-                            pb=S.to_host(blk.pb), spw=u32(blk.spw), sps=S.to_host(blk.sps), spb=S.to_host(blk.spb)))
-    return out
-
-
 def test_decode_step_matches_oracle(model):
     """One decode step of the whole reduced model against the oracle's composition of the
     blocks (float64 sums, bf16 activations between ops), from the GPU's caches after the
@@ -186,7 +162,7 @@ def test_decode_step_matches_oracle(model):
     # the oracle from the same token and states
     E = model.embedding
     x = O.embed_q4(np.array([tok0]), S.to_host(E.w).view(np.uint32), S.to_host(E.scales), S.to_host(E.biases))[0]
-    for t, w, st in zip(c.pattern, host_weights(model), states):
+    for t, w, st in zip(c.pattern, hostw.model_blocks(model), states):
         if t == "M":
             x, _, _ = O.mamba_block_step(x, w, st[0], st[1], n_groups=c.n_groups, eps=c.eps)
         elif t == "*":
@@ -203,3 +179,53 @@ def test_decode_step_matches_oracle(model):
     top = np.sort(lg)[::-1]
     if top[0] - top[1] > 6e-2 * np.abs(lg).max():
         assert int(np.argmax(logits_gpu)) == int(np.argmax(lg))
+
+
+def test_mtp_head_call_surface(model):
+    """hsd.mtp.MTPHead (mtp.py:41-88): rows in chunks equal single rows bit for bit,
+    trim drops rows, reset empties the cache; the first row against the oracle's head
+    (pair norm, eh_proj, attention over itself, MoE, final norm, lm_head)."""
+    from hsd import synth as S
+    from oracle import hsd_oracle as O
+    dev = model.device
+    c = model.cfg
+    rng = np.random.default_rng(77)
+    hb = O.f32_to_bf16(rng.standard_normal((5, c.hidden)).astype(np.float32))
+    h = S.to_device(hb, dev)
+    toks = torch.from_numpy(rng.integers(0, c.vocab, 5).astype(np.int32)).to(dev)
+    head = mtp.MTPHead(model)
+    pred, hn = head(h, toks)
+    assert head.rows == 5
+    single = mtp.MTPHead(model)
+    for r in range(5):
+        p1, h1 = single(h[r:r + 1], toks[r:r + 1])
+        assert int(p1[0]) == int(pred[r])
+        assert torch.equal(h1[0].view(torch.int16), hn[r].view(torch.int16))
+    head.trim(2)
+    p2, h2 = head(h[3:5], toks[3:5])
+    assert torch.equal(p2, pred[3:5]) and torch.equal(h2.view(torch.int16), hn[3:5].view(torch.int16))
+    head.reset()
+    p3, h3 = head(h[:1], toks[:1])
+    assert int(p3[0]) == int(pred[0])
+    # the oracle's head on row 0 (an empty cache: attention over the row itself)
+    hd = model.mtp
+    E = model.embedding
+    e = O.embed_q4(np.array([int(toks[0])]), S.to_host(E.w).view(np.uint32), S.to_host(E.scales),
+                   S.to_host(E.biases))[0]
+    pair = np.concatenate([O.rms_norm_bf16(O._vals(e), O._vals(S.to_host(hd.enorm)), c.eps),
+                           O.rms_norm_bf16(O._vals(hb[0]), O._vals(S.to_host(hd.hnorm)), c.eps)])
+    x = O.f32_to_bf16(O.linear_bf16(O._vals(pair)[None], S.to_host(hd.eh_proj.w))[0].astype(np.float32))
+    HKV, HD = c.kv_heads, c.head_dim
+    x, _, _ = O.attn_block_step(x, hostw.attn_block(hd.attn), np.zeros((HKV, 0, HD)), np.zeros((HKV, 0, HD)),
+                                n_heads=c.attn_heads, n_kv_heads=HKV, eps=c.eps)
+    x = O.moe_block_step(x, hostw.moe_block(hd.moe), topk=c.topk, routed_scale=c.routed_scale, eps=c.eps)
+    hn_ref = O.bf16_to_f32(O.rms_norm_bf16(O._vals(x), O._vals(S.to_host(hd.final_norm)), c.eps))
+    got = hn[0].float().cpu().numpy()
+    err = np.abs(got - hn_ref).max() / np.abs(hn_ref).max()
+    print(f"MTP head row 0 vs oracle: hn max rel err {err:.2e}")
+    assert err <= 3e-2
+    lg = O.lm_head_logits(x, S.to_host(hd.final_norm), S.to_host(model.lm_head.w).view(np.uint32),
+                          S.to_host(model.lm_head.scales), S.to_host(model.lm_head.biases), c.eps)
+    top = np.sort(lg)[::-1]
+    if top[0] - top[1] > 6e-2 * np.abs(lg).max():
+        assert int(pred[0]) == int(np.argmax(lg))

@@ -3,12 +3,14 @@
 (model.py:123-129), with the canonical live masks.
 
 Bars:
-* h within one bf16 ulp of the pre-activation of the float64 oracle: the kernel
-  accumulates in fp32 and rounds u to bf16 before squaring, so a u on a rounding boundary
-  can land one ulp away, which moves h = u^2 by at most 2^-5 relative; |h - ref| <=
-  2^-5 |ref| + 1e-4 (the absolute term covers the fp32 summation error of a u near 0);
-  at least 99 % of the elements are bit-identical, and zero / nonzero disagree on at most
-  1e-3 of them;
+* h bit-identical to the oracle's relu2(bf16(u)) wherever the float64 pre-activation u
+  is farther than the kernel's fp32 accumulation error from a bf16 rounding boundary.
+  The error bound is 2^-20 M + 2^-23 |u| with M = sum_i (|s| (16 + q) + |b - 16 s|) |x_i|,
+  the magnitude of every partial sum the kernel forms (u = 16 s sum (1 + q/16) x +
+  (b - 16 s) sum x per 32-input piece: 16 roundings at the full magnitude, the depth of
+  one piece's dot2 chain; the cross-piece sum adds far less). Within that distance
+  of a boundary h must lie between relu2 of the two neighbouring bf16 values (the
+  fraction of such elements is printed; at least 99 % are bit-identical overall);
 * integer work bit-exact: the live masks equal those of the kernel's own h;
 * a routed id outside [0, E): status flag, that slot exactly 0, the others unchanged.
 """
@@ -37,12 +39,30 @@ def masks_of(h_bits):
     return (live.reshape(live.shape[0], -1, 64).astype(np.uint64) * w).sum(-1, dtype=np.uint64).reshape(-1)
 
 
-def check(h, ref):
-    hf, rf = O.bf16_to_f32(h).astype(np.float64), O.bf16_to_f32(ref).astype(np.float64)
-    nz = (hf != 0) & (rf != 0)
+def check(h, ref, x_bits, sel, lay, F, FS, topk):
+    """h, ref [B, topk*F + FS] bf16 bits (kernel, oracle); the bar in the module doc."""
     assert np.mean(h == ref) >= 0.99
-    assert np.all(np.abs(hf - rf)[nz] <= 2 ** -5 * np.abs(rf[nz]) + 1e-4)
-    assert np.mean((hf == 0) != (rf == 0)) <= 1e-3
+    x = O.bf16_to_f32(x_bits).astype(np.float64)
+    n_edge = 0
+    for b in range(x.shape[0]):
+        slots = [(k * F, lay["w1"][e], lay["s1"][e], lay["b1"][e]) for k, e in enumerate(sel[b])]
+        slots.append((topk * F, lay["sw1"], lay["ss1"], lay["sb1"]))
+        for off, w, sc, bi in slots:
+            q = O.unpack_nibbles(w).astype(np.float64)
+            sf = np.repeat(O.bf16_to_f32(sc).astype(np.float64), 64, axis=-1)
+            bf = np.repeat(O.bf16_to_f32(bi).astype(np.float64), 64, axis=-1)
+            u = (sf * q + bf) @ x[b]
+            m = (np.abs(sf) * (16 + q) + np.abs(bf - 16 * sf)) @ np.abs(x[b])
+            err = 2.0 ** -20 * m + 2.0 ** -23 * np.abs(u)
+            lo, mid, hi = O.relu2_bf16(u - err), O.relu2_bf16(u), O.relu2_bf16(u + err)
+            got = h[b, off:off + len(u)]
+            edge = lo != hi
+            assert np.array_equal(got[~edge], mid[~edge])
+            gv = O.bf16_to_f32(got[edge])
+            assert np.all((O.bf16_to_f32(lo[edge]) <= gv) & (gv <= O.bf16_to_f32(hi[edge])))
+            n_edge += int(edge.sum())
+    print(f"bit-identical {np.mean(h == ref):.5f}; within the accumulation error of a bf16 boundary "
+          f"{n_edge / h.size:.4f}")
 
 
 @pytest.fixture(scope="module")
@@ -59,7 +79,7 @@ def test_up_relu2_matches_oracle(up, dev):
                  dv["sb1"], topk=K, live_masks=masks)
     hb = h.view(torch.int16).cpu().numpy().view(np.uint16)
     ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=F, FS=FS, topk=K)
-    check(hb, ref)
+    check(hb, ref, x, sel, lay, F, FS, K)
     assert np.array_equal(masks.cpu().numpy().view(np.uint64), masks_of(hb))
 
 
@@ -90,7 +110,7 @@ def test_small_shape(dev):
     h = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"],
                  dv["sb1"], topk=k)
     ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=f, FS=fs, topk=k)
-    check(h.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+    check(h.view(torch.int16).cpu().numpy().view(np.uint16), ref, x, sel, lay, f, fs, k)
 
 
 def test_front_end_feeds_the_down_projection(up, dev):
