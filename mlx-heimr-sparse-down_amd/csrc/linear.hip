@@ -12,10 +12,12 @@
 // greedy argmax of the bf16-rounded outputs (per-workgroup best keys, reduced by
 // hsd_argmax_keys; lm_head + argmax without writing the logits).
 //
-// Work split: a workgroup (4 wavefronts) owns 8 consecutive output rows (4-bit: 2 per
+// Work split: a workgroup (4 wavefronts) owns 16 consecutive output rows (4-bit: 4 per
 // wavefront) or 4 (bf16: 1 per wavefront) and loops over row blocks strided by the grid
-// (at most 2048 workgroups, so the prologue is paid once per workgroup). A row's 16-byte
-// pieces are dealt over the wavefront's 64 lanes; the next block's pieces are loaded
+// (as many workgroups as are resident at once, so the prologue is paid once per
+// workgroup). Lane l owns the 16-byte pieces l, l + 64, ... of every row of its wavefront:
+// an x piece read from LDS serves all the wavefront's rows (at three token rows, reading x
+// once per row and piece made LDS the bound of lm_head). The next block's pieces are loaded
 // while the current one is computed. 4-bit pieces are turned into bf16 pairs (1 + q/16)
 // with a shift, a mask and an OR, and v_dot2_f32_bf16 accumulates x (1 + q/16); per
 // 32-input piece u += 16 s acc + (b - 16 s) sum(x) (the affine dequantisation folded per
@@ -38,6 +40,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kLT = 256;                 // threads per workgroup
 constexpr int kLMaxB = 4;                // token rows per launch
 constexpr int kLMaxI = 6144;             // inputs per row
+constexpr int kLSmallQ4 = 4096;          // 4-bit rows up to this length: 2 pieces per lane
 constexpr int kLMaxGrid = 2048;
 constexpr uint32_t kBfOne2 = 0x3F803F80u;
 constexpr uint32_t kNibHi = 0x00780078u;
@@ -65,8 +68,8 @@ template <> struct WTraits<HSD_W_Q4> {
 template <> struct WTraits<HSD_W_BF16> {
   static constexpr int kIn = 8;
 };
-// pieces per lane for RW rows of up to I inputs per wavefront
-template <int WF> constexpr int pieces_per_lane(int RW, int I) { return (RW * (I / WTraits<WF>::kIn) + 63) / 64; }
+// pieces of one row per lane for rows of up to I inputs
+template <int WF> constexpr int pieces_per_lane(int I) { return (I / WTraits<WF>::kIn + 63) / 64; }
 
 struct LinArgs {
   const void* x;
@@ -99,13 +102,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
-// IMAX: the largest row length the instance serves (kIt weight pieces per lane, XIT x
+// IMAX: the largest row length the instance serves (kIt pieces of a row per lane, XIT x
 // words of 8 inputs per thread in the prologue).
-// RW: output rows per wavefront (a block = 4 RW rows).
+// RW: output rows per wavefront (a block = 4 RW rows). Lane l owns pieces l, l + 64, ... of
+// each of its wavefront's RW rows, so an x piece read from LDS serves RW rows.
 template <int WF, int NB, int XK, int YK, int IMAX, int RW>
 __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   using T = WTraits<WF>;
-  constexpr int kRW = RW, kIt = pieces_per_lane<WF>(RW, IMAX);
+  constexpr int kRW = RW, kIt = pieces_per_lane<WF>(IMAX);
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   constexpr int kRows = 4 * kRW;                       // rows per block
   constexpr int kSc = WF == HSD_W_Q4 ? kIt : 1;
@@ -119,27 +123,29 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   uint32_t* xp = lsm;
   float* xh = reinterpret_cast<float*>(lsm + NB * (I / 2));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nblk = O / kRows;
+  const int nblk = (O + kRows - 1) / kRows;            // the last block may be partial
   const int NPr = I / T::kIn;                          // pieces per row
-  const int npw = kRW * NPr;                           // pieces per wavefront
-  const int nit = (npw + 63) / 64;
+  const int nit = (NPr + 63) / 64;
 
-  // ---- weight pieces of a block: piece p = lane + 64 it of the wave's kRW rows
-  auto load_block = [&](int blk, uint4 (&qq)[kIt], float (&ss)[kSc], float (&bb)[kSc]) {
+  // ---- weight pieces of a block: piece j = lane + 64 it of each of the wave's kRW rows
+  // (rows past O re-read row O-1, pieces past the row re-read its last piece; unused)
+  auto load_block = [&](int blk, uint4 (&qq)[kRW][kIt], uint32_t (&sb)[kRW][kSc]) {
     const int r0 = blk * kRows + kRW * wave;
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int p = min(lane + 64 * it, npw - 1);      // past the end: re-read the last piece
-      const int pr = p / NPr, pj = p - pr * NPr;
-      if constexpr (WF == HSD_W_Q4) {
-        const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)(r0 + pr) * NW;
-        qq[it] = reinterpret_cast<const uint4*>(wr)[pj];
-        const size_t gi = (size_t)(r0 + pr) * (I / 64) + (pj >> 1);
-        ss[it] = bf16_bits_to_f32(a.s[gi]);
-        bb[it] = bf16_bits_to_f32(a.bq[gi]);
-      } else {
-        const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w) + (size_t)(r0 + pr) * I;
-        qq[it] = reinterpret_cast<const uint4*>(wr)[pj];
+    for (int r = 0; r < kRW; ++r) {
+      const int row = min(r0 + r, O - 1);
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int j = min(lane + 64 * it, NPr - 1);
+        if constexpr (WF == HSD_W_Q4) {
+          const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)row * NW;
+          qq[r][it] = reinterpret_cast<const uint4*>(wr)[j];
+          const size_t gi = (size_t)row * (I / 64) + (j >> 1);
+          sb[r][it] = (uint32_t)a.s[gi] | ((uint32_t)a.bq[gi] << 16);
+        } else {
+          const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w) + (size_t)row * I;
+          qq[r][it] = reinterpret_cast<const uint4*>(wr)[j];
+        }
       }
     }
   };
@@ -167,10 +173,10 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   }
   // the first block's weight pieces, issued after x: the prologue waits for x only (loads
   // complete in issue order), while the weights are still on their way
-  uint4 q[kIt];
-  float sc[kSc], bi[kSc];
+  uint4 q[kRW][kIt];
+  uint32_t sb[kRW][kSc];
   int blk = blockIdx.x;
-  load_block(blk, q, sc, bi);
+  load_block(blk, q, sb);
   // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
   uint32_t xo[NB][XIT][4];
   if constexpr (XK == HSD_X_BF16) {
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   uint64_t best[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
-  auto do_block = [&](int blk_, const uint4 (&qq)[kIt], const float (&ss)[kSc], const float (&bb)[kSc]) {
+  auto do_block = [&](int blk_, const uint4 (&qq)[kRW][kIt], const uint32_t (&sbq)[kRW][kSc]) {
     float pr[NB][kRW];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -292,46 +298,60 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       if (it < nit) {                                   // uniform
-        const int p0 = lane + 64 * it;
-        const bool use = p0 < npw;
-        const int p = min(p0, npw - 1);
-        const int prow = p / NPr, j = p - prow * NPr;
-        const uint32_t qw[4] = {qq[it].x, qq[it].y, qq[it].z, qq[it].w};
+        const int j0 = lane + 64 * it;
+        const bool use = j0 < NPr;
+        const int j = min(j0, NPr - 1);
         if constexpr (WF == HSD_W_Q4) {
-          uint32_t wc[4][4];
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
-            wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
-            wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
-            wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
-          }
-          const float s16 = 16.0f * ss[it], bo = fmaf(-16.0f, ss[it], bb[it]);
+          // the token rows' x piece j (32 inputs) and its sum, read once for the kRW rows
+          uint4 xq[NB][4];
+          float xs[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) xq[b][m] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
+            xs[b] = xh[b * (I / 32) + j];
+          }
+#pragma unroll
+          for (int r = 0; r < kRW; ++r) {
+            const uint32_t qw[4] = {qq[r][it].x, qq[r][it].y, qq[r][it].z, qq[r][it].w};
+            uint32_t wc[4][4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
-              acc = dot2_bf16(xq.x, wc[m][0], acc);
-              acc = dot2_bf16(xq.y, wc[m][1], acc);
-              acc = dot2_bf16(xq.z, wc[m][2], acc);
-              acc = dot2_bf16(xq.w, wc[m][3], acc);
+              wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
+              wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
+              wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
+              wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
             }
-            const float t = use ? fmaf(s16, acc, bo * xh[b * (I / 32) + j]) : 0.0f;
+            const float sv = lo_f(sbq[r][it]), bv = hi_f(sbq[r][it]);
+            const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
 #pragma unroll
-            for (int r = 0; r < kRW; ++r) pr[b][r] += prow == r ? t : 0.0f;
+            for (int b = 0; b < NB; ++b) {
+              float acc = 0.0f;
+#pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                acc = dot2_bf16(xq[b][m].x, wc[m][0], acc);
+                acc = dot2_bf16(xq[b][m].y, wc[m][1], acc);
+                acc = dot2_bf16(xq[b][m].z, wc[m][2], acc);
+                acc = dot2_bf16(xq[b][m].w, wc[m][3], acc);
+              }
+              pr[b][r] += use ? fmaf(s16, acc, bo * xs[b]) : 0.0f;
+            }
           }
         } else {
+          uint4 xq[NB];
 #pragma unroll
-          for (int b = 0; b < NB; ++b) {
-            const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
-            float acc = 0.0f;
-            acc = dot2_bf16(xq.x, qw[0], acc);
-            acc = dot2_bf16(xq.y, qw[1], acc);
-            acc = dot2_bf16(xq.z, qw[2], acc);
-            acc = dot2_bf16(xq.w, qw[3], acc);
-            pr[b][0] += use ? acc : 0.0f;
+          for (int b = 0; b < NB; ++b) xq[b] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
+#pragma unroll
+          for (int r = 0; r < kRW; ++r) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              float acc = 0.0f;
+              acc = dot2_bf16(xq[b].x, qq[r][it].x, acc);
+              acc = dot2_bf16(xq[b].y, qq[r][it].y, acc);
+              acc = dot2_bf16(xq[b].z, qq[r][it].z, acc);
+              acc = dot2_bf16(xq[b].w, qq[r][it].w, acc);
+              pr[b][r] += use ? acc : 0.0f;
+            }
           }
         }
       }
@@ -357,10 +377,11 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
     }
     const int ob = lane / kRW, orr = lane - ob * kRW;
     const int o = blk_ * kRows + kRW * wave + orr;
+    const bool live = lane < NB * kRW && o < O;
     if constexpr (YK == HSD_Y_ARGMAX) {
       const uint16_t lb = f32_to_bf16_bits(outv);
-      const uint64_t key = lane < NB * kRW ? argmax_key(lb, o) : 0;
-      if (a.y && lane < NB * kRW) reinterpret_cast<uint16_t*>(a.y)[ob * a.y_ld + o] = lb;
+      const uint64_t key = live ? argmax_key(lb, o) : 0;
+      if (a.y && live) reinterpret_cast<uint16_t*>(a.y)[ob * a.y_ld + o] = lb;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         uint64_t kb = 0;
@@ -372,7 +393,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
         }
         best[b] = kb > best[b] ? kb : best[b];
       }
-    } else if (lane < NB * kRW) {
+    } else if (live) {
       const int64_t yi = ob * a.y_ld + o;
       if constexpr (YK == HSD_Y_F32) {
         reinterpret_cast<float*>(a.y)[yi] = outv;
@@ -386,24 +407,26 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   };
 
   if ((int)gridDim.x >= nblk) {
-    do_block(blk, q, sc, bi);                          // one block per workgroup
+    do_block(blk, q, sb);                              // one block per workgroup
   } else {
     // several blocks: the next block's pieces are in flight while one is computed; the
     // load is unconditional (the last block re-reads its own lines), so the compiler's
     // wait before the arithmetic counts only the current block's loads
     for (;;) {
       const int nxt = blk + (int)gridDim.x;
-      uint4 qn[kIt];
-      float scn[kSc], bin[kSc];
-      load_block(nxt < nblk ? nxt : blk, qn, scn, bin);
-      do_block(blk, q, sc, bi);
+      uint4 qn[kRW][kIt];
+      uint32_t sbn[kRW][kSc];
+      load_block(nxt < nblk ? nxt : blk, qn, sbn);
+      do_block(blk, q, sb);
       if (nxt >= nblk) break;
       blk = nxt;
 #pragma unroll
-      for (int it = 0; it < kIt; ++it) {
-        q[it] = qn[it];
-        if constexpr (WF == HSD_W_Q4) { sc[it] = scn[it]; bi[it] = bin[it]; }
-      }
+      for (int r = 0; r < kRW; ++r)
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          q[r][it] = qn[r][it];
+          if constexpr (WF == HSD_W_Q4) sb[r][it] = sbn[r][it];
+        }
     }
   }
   if constexpr (YK == HSD_Y_ARGMAX) {
@@ -448,9 +471,15 @@ __global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict
   }
 }
 
+// Output rows per wavefront: 4 for 4-bit weights (an x piece read from LDS serves 4 rows),
+// 1 for bf16. Two rows per wavefront for the shorter projections (more workgroups: 336
+// rather than 168 for out_proj) measured slower for out_proj (6.3 against 5.9 us at one
+// token row, 10.6 against 9.8 at three) and the decode step as a whole.
+int rows_per_wave(int O, int w_kind) { (void)O; return w_kind == HSD_W_Q4 ? 4 : 1; }
+
 int linear_grid(int O, int w_kind) {
-  const int rows = w_kind == HSD_W_Q4 ? 8 : 4;
-  return std::min(O / rows, kLMaxGrid);
+  const int rows = 4 * rows_per_wave(O, w_kind);
+  return std::min((O + rows - 1) / rows, kLMaxGrid);
 }
 
 // Workgroups of `kernel` that are resident at once on the current device (occupancy x
@@ -475,23 +504,12 @@ int resident_workgroups(const void* kernel, size_t lds) {
   return r;
 }
 
-}  // namespace
-}  // namespace hsd
-
-using namespace hsd;
-
-extern "C" int64_t hsd_linear_argmax_slots(int64_t O, int w_kind) {
-  if (O <= 0 || (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16)) return 0;
-  return linear_grid((int)std::min<int64_t>(O, 1 << 30), w_kind);
-}
-
-extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
-                          const uint16_t* norm_w, float eps, const void* w, const uint16_t* scales,
-                          const uint16_t* biases, int w_kind, void* y, int64_t y_ld, int y_kind,
-                          const uint16_t* res, int64_t res_ld, uint16_t* xn_out, int64_t xn_ld,
-                          uint64_t* argmax_keys, int64_t key_ld, int64_t B, int64_t O, int64_t I,
-                          void* stream) {
-  const char* fn = "hsd_linear";
+// The checks and the launch of hsd_linear.
+int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
+                  const uint16_t* norm_w, float eps, const void* w, const uint16_t* scales, const uint16_t* biases,
+                  int w_kind, void* y, int64_t y_ld, int y_kind, const uint16_t* res, int64_t res_ld,
+                  uint16_t* xn_out, int64_t xn_ld, uint64_t* argmax_keys, int64_t key_ld, int64_t B, int64_t O,
+                  int64_t I, void* stream) {
   if (!x || !w || (y_kind != HSD_Y_ARGMAX && !y)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (w_kind == HSD_W_Q4 && (!scales || !biases)) return set_error(HSD_ERR_ARG, "%s: 4-bit weights need scales and biases", fn);
   if (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16) return set_error(HSD_ERR_DTYPE, "%s: w_kind %d", fn, w_kind);
@@ -526,7 +544,7 @@ extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_
             argmax_keys, key_ld, slots, (int)O, (int)I};
   const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
   hipStream_t st = as_stream(stream);
-  const bool small = I <= 3072;
+  const bool small = I <= (w_kind == HSD_W_Q4 ? kLSmallQ4 : 3072);
   const int grid = slots;
   // the (x_kind, y_kind) pairs this library instantiates
   const int pair = x_kind * 8 + y_kind;
@@ -539,15 +557,23 @@ extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_
   if (!ok)
     return set_error(HSD_ERR_SHAPE, "%s: unsupported combination x_kind %d, y_kind %d, w_kind %d", fn, x_kind,
                      y_kind, w_kind);
-#define HSD_LIN(WF, NB, XK, YK, IM)                                                                   \
+#define HSD_LIN_R(WF, NB, XK, YK, IM, RW)                                                             \
   {                                                                                                   \
-    constexpr int RW = WF == HSD_W_Q4 ? 2 : 1;                                                        \
     const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW>);               \
     const int g = std::max(1, std::min(grid, resident_workgroups(kf, lds)));                         \
     hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW>), dim3(g), dim3(kLT), lds, st, a);           \
   }
-#define HSD_LIN_I(WF, NB, XK, YK)     \
-  if (small) HSD_LIN(WF, NB, XK, YK, 3072) else HSD_LIN(WF, NB, XK, YK, kLMaxI)
+#define HSD_LIN(WF, NB, XK, YK, IM)                      \
+  {                                                      \
+    if constexpr (WF == HSD_W_Q4) {                      \
+      HSD_LIN_R(WF, NB, XK, YK, IM, 4)                   \
+    } else {                                             \
+      HSD_LIN_R(WF, NB, XK, YK, IM, 1)                   \
+    }                                                    \
+  }
+#define HSD_LIN_I(WF, NB, XK, YK)                                              \
+  if (small) HSD_LIN(WF, NB, XK, YK, (WF == HSD_W_Q4 ? kLSmallQ4 : 3072)) else \
+    HSD_LIN(WF, NB, XK, YK, kLMaxI)
 #define HSD_LIN_P(WF, NB)                                                  \
   switch (pair) {                                                          \
     case kRB: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_BF16); break;             \
@@ -578,7 +604,28 @@ extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_
 #undef HSD_LIN_P
 #undef HSD_LIN_I
 #undef HSD_LIN
+#undef HSD_LIN_R
   return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace hsd
+
+using namespace hsd;
+
+extern "C" int64_t hsd_linear_argmax_slots(int64_t O, int w_kind) {
+  if (O <= 0 || (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16)) return 0;
+  return linear_grid((int)std::min<int64_t>(O, 1 << 30), w_kind);
+}
+
+extern "C" int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
+                          const uint16_t* norm_w, float eps, const void* w, const uint16_t* scales,
+                          const uint16_t* biases, int w_kind, void* y, int64_t y_ld, int y_kind,
+                          const uint16_t* res, int64_t res_ld, uint16_t* xn_out, int64_t xn_ld,
+                          uint64_t* argmax_keys, int64_t key_ld, int64_t B, int64_t O, int64_t I,
+                          void* stream) {
+  return launch_linear("hsd_linear", x, x_ld, x_kind, gate, gate_ld, norm_w, eps, w, scales, biases, w_kind, y,
+                       y_ld, y_kind, res, res_ld, xn_out, xn_ld, argmax_keys, key_ld, B, O, I, stream);
 }
 
 extern "C" int hsd_argmax_keys(const uint64_t* keys, int64_t key_ld, int64_t slots, int64_t B, int32_t* tok,
