@@ -12,9 +12,9 @@
 //   k_attn_part: one workgroup per (kv head, 64-key chunk, half of the kv head's query
 //     heads). The chunk's keys go to LDS (rows padded by 16 bytes against bank
 //     conflicts); lane j of wave w scores key j against query heads 2w, 2w+1 (a q.k dot in
-//     fp32 with v_dot2_f32_bf16, times the scale); a wave's max and sum over its 64 keys
-//     (DPP); then p = exp(s - m) times V (LDS) into acc[128]. Writes the chunk's (m, l, acc)
-//     per row and head.
+//     fp32 with v_dot2_f32_bf16 in four partial sums, times the scale); a wave's max and
+//     sum over its 64 keys (DPP); then p = exp(s - m) times V (LDS) into acc[128] (even and
+//     odd keys in separate sums). Writes the chunk's (m, l, acc) per row and head.
 //   k_attn_combine: one workgroup per (row, query head): the chunks of keys 0 .. P+r in
 //     chunk order: M = max m, L = sum l e^(m-M), o = sum acc e^(m-M) / L, rounded to bf16.
 // The chunk boundaries are absolute positions and each row's chunks are combined in the
@@ -125,15 +125,20 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) {
           const int h = 2 * wave + hi;
-          float s = 0.0f;
+          // four partial dot products (16-byte pieces i % 4), so that four dependency chains
+          // of 16 interleave instead of one of 64
+          float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int i = 0; i < kHD / 8; ++i) {
             const uint4 qv = *reinterpret_cast<const uint4*>(&qs[r][h][4 * i]);
-            s = dot2(qv.x, kr[4 * i], s);
-            s = dot2(qv.y, kr[4 * i + 1], s);
-            s = dot2(qv.z, kr[4 * i + 2], s);
-            s = dot2(qv.w, kr[4 * i + 3], s);
+            float t = s4[i & 3];
+            t = dot2(qv.x, kr[4 * i], t);
+            t = dot2(qv.y, kr[4 * i + 1], t);
+            t = dot2(qv.z, kr[4 * i + 2], t);
+            t = dot2(qv.w, kr[4 * i + 3], t);
+            s4[i & 3] = t;
           }
+          float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
           s = vis ? s * a.scale : -INFINITY;
           // wave max (DPP inside rows, then the four row maxima)
           float mx = s;
@@ -159,27 +164,40 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
   // ---- acc = sum_j p_j v_j: thread = (head h = tid / 32, dims 4 (tid % 32) .. +3)
   {
     const int h = tid >> 5, d0 = 4 * (tid & 31);
-    float acc[kAMaxB][4];
+    // two accumulator sets (even and odd keys), added at the end: twice the independent
+    // chains for the latency of the fma and LDS reads
+    float acc[kAMaxB][4], acc2[kAMaxB][4];
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
-#pragma unroll 8
-    for (int jl = 0; jl < kCH; ++jl) {
-      const uint2 vv = *reinterpret_cast<const uint2*>(&vs[jl][d0 / 2]);
-      const float v0 = bf16_bits_to_f32(vv.x & 0xFFFFu), v1 = bf16_bits_to_f32(vv.x >> 16);
-      const float v2 = bf16_bits_to_f32(vv.y & 0xFFFFu), v3 = bf16_bits_to_f32(vv.y >> 16);
+      for (int e = 0; e < 4; ++e) acc[r][e] = acc2[r][e] = 0.0f;
+#pragma unroll 4
+    for (int jl = 0; jl < kCH; jl += 2) {
+      const uint2 va = *reinterpret_cast<const uint2*>(&vs[jl][d0 / 2]);
+      const uint2 vb = *reinterpret_cast<const uint2*>(&vs[jl + 1][d0 / 2]);
+      const float a0 = bf16_bits_to_f32(va.x & 0xFFFFu), a1 = bf16_bits_to_f32(va.x >> 16);
+      const float a2 = bf16_bits_to_f32(va.y & 0xFFFFu), a3 = bf16_bits_to_f32(va.y >> 16);
+      const float b0 = bf16_bits_to_f32(vb.x & 0xFFFFu), b1 = bf16_bits_to_f32(vb.x >> 16);
+      const float b2 = bf16_bits_to_f32(vb.y & 0xFFFFu), b3 = bf16_bits_to_f32(vb.y >> 16);
 #pragma unroll
       for (int r = 0; r < kAMaxB; ++r) {
         if (r < B) {
-          const float p = ps[r][h][jl];
-          acc[r][0] = fmaf(p, v0, acc[r][0]);
-          acc[r][1] = fmaf(p, v1, acc[r][1]);
-          acc[r][2] = fmaf(p, v2, acc[r][2]);
-          acc[r][3] = fmaf(p, v3, acc[r][3]);
+          const float2 p = *reinterpret_cast<const float2*>(&ps[r][h][jl]);
+          acc[r][0] = fmaf(p.x, a0, acc[r][0]);
+          acc[r][1] = fmaf(p.x, a1, acc[r][1]);
+          acc[r][2] = fmaf(p.x, a2, acc[r][2]);
+          acc[r][3] = fmaf(p.x, a3, acc[r][3]);
+          acc2[r][0] = fmaf(p.y, b0, acc2[r][0]);
+          acc2[r][1] = fmaf(p.y, b1, acc2[r][1]);
+          acc2[r][2] = fmaf(p.y, b2, acc2[r][2]);
+          acc2[r][3] = fmaf(p.y, b3, acc2[r][3]);
         }
       }
     }
+#pragma unroll
+    for (int r = 0; r < kAMaxB; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][e] += acc2[r][e];
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r) {
       if (r < B && j0 <= P + r) {
@@ -220,6 +238,11 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   }
   const int nc = (P + r) / kCH + 1;
   const float* src = a.part + ((size_t)r * a.HQ + h) * a.nch * kRec;
+  // this dimension's values of the first 8 chunks, issued with the (m, l) loads (they do
+  // not depend on the maximum)
+  float v0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v0[u] = src[(size_t)min(u, nc - 1) * kRec + 4 + d];
   // (m, l) of every chunk in one round trip, into LDS
   for (int c = d; c < nc; c += kHD) {
     mw[c] = src[(size_t)c * kRec];
@@ -244,7 +267,7 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   for (; c + 8 <= nc; c += 8) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(c + u) * kRec + 4 + d];
+    for (int u = 0; u < 8; ++u) v[u] = c == 0 ? v0[u] : src[(size_t)(c + u) * kRec + 4 + d];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       L = fmaf(lw[c + u], mw[c + u], L);
@@ -253,7 +276,7 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   }
   for (; c < nc; ++c) {
     L = fmaf(lw[c], mw[c], L);
-    acc = fmaf(src[(size_t)c * kRec + 4 + d], mw[c], acc);
+    acc = fmaf(c < 8 ? v0[c] : src[(size_t)c * kRec + 4 + d], mw[c], acc);
   }
   o[d] = f32_to_bf16_bits(acc / L);
 }
