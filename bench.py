@@ -16,7 +16,8 @@ decode sweep; `workloads` holds the decode sweep, the prefill grouped GEMM, the 
 verify + rollback over 23 Mamba-2 layers and the MoE front end, each with its roofline and
 its CPU baseline (the NumPy oracle on the host cores, a bounded sample).
 
---workload e2e|decode|prefill|mtp|up prints one of them alone.
+--workload e2e|decode|prefill|mtp|up prints one of them alone; --workload step --mode
+mtp|sparse|dense replays one captured step of the model (for per-kernel profiles).
 """
 from __future__ import annotations
 
@@ -749,6 +750,26 @@ def bench_e2e(args):
     return rec
 
 
+def bench_step(args):
+    """One captured step of the end-to-end model replayed `--steps` times after a
+    `--prompt`-token prefill: --mode mtp (the head's own two drafts, the 3-row verify, the
+    acceptance and the rollback; the kernels of a step do not depend on how many drafts are
+    accepted), sparse or dense (a plain decode step). For per-kernel profiles of a step."""
+    cfg = Mdl.ModelConfig()
+    model = Mdl.NemotronModel(cfg, mode="dense" if args.mode == "dense" else "sparse", seed=args.seed)
+    prompt = np.random.default_rng(args.seed + 11).integers(0, cfg.vocab, args.prompt).astype(np.int32)
+    K = args.steps if args.steps > 0 else 200
+    s = model.session(prompt, mtp=args.mode == "mtp", cap=4 * K + 16)
+    s.step(max(args.warmup, 0))
+    sec = s.step(K)
+    log(f"[step] {args.mode}: {1e3 * sec / K:.3f} ms per step over {K} steps after a {len(prompt)}-token prompt")
+    return dict(metric=f"captured {args.mode} step time", value=round(1e3 * sec / K, 4), unit="ms/step", n_gpus=1,
+                steps=K, warmup=args.warmup, ms_per_step=round(1e3 * sec / K, 4), higher_is_better=False,
+                scaling="weak", vs_baseline=None, dtype="f32 accumulate (4-bit weights, bf16 activations)",
+                data="synthetic", config=dict(workload=f"one {args.mode} step of the 52-layer random-init model",
+                                              prompt_tokens=len(prompt)))
+
+
 def _sub(rec):
     """A workload's record inside the combined line (the fields the run record repeats dropped)."""
     drop = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "data")
@@ -782,7 +803,8 @@ def main():
     ap.add_argument("--steps", type=int, default=0,
                     help="timed steps (0: the workload's default; end to end: the steps that make 256 tokens)")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="all", choices=("all", "e2e", "decode", "prefill", "mtp", "up"))
+    ap.add_argument("--workload", default="all", choices=("all", "e2e", "decode", "prefill", "mtp", "up", "step"))
+    ap.add_argument("--mode", default="mtp", choices=("mtp", "sparse", "dense"), help="step: which step")
     ap.add_argument("--prompt", type=int, default=2048, help="end to end: prompt tokens")
     ap.add_argument("--gen", type=int, default=256, help="end to end: generated tokens")
     ap.add_argument("--zero-frac", type=float, default=0.9)
@@ -802,12 +824,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    if args.workload not in ("all", "e2e"):
+    if args.workload not in ("all", "e2e", "step"):
         defaults = dict(decode=(200, 20), prefill=(3, 1), mtp=(200, 20), up=(200, 20))[args.workload]
         if args.steps <= 0:
             args.steps, args.warmup = defaults
     fn = dict(all=bench_all, e2e=bench_e2e, decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp,
-              up=bench_up)[args.workload]
+              up=bench_up, step=bench_step)[args.workload]
     rec = fn(args)
     rec["device"] = torch.cuda.get_device_name(0)
     rec["torch"] = torch.__version__
