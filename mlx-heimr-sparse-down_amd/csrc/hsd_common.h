@@ -21,6 +21,12 @@ int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Workgroups of `kernel` (`threads` each, `lds` bytes of dynamic LDS) resident at once on
+// the current device (occupancy x CUs), looked up once per kernel, size and device;
+// `fallback` when the runtime cannot say. A grid no larger than this has no workgroup
+// waiting for another to finish.
+int resident_workgroups(const void* kernel, int threads, size_t lds, int fallback);
+
 // ---------------------------------------------------------------- bf16 / f16
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);

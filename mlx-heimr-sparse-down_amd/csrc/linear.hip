@@ -482,27 +482,6 @@ int linear_grid(int O, int w_kind) {
   return std::min((O + rows - 1) / rows, kLMaxGrid);
 }
 
-// Workgroups of `kernel` that are resident at once on the current device (occupancy x
-// CUs), looked up once per kernel, LDS size and device. A grid no larger than this has no
-// workgroup waiting for another to finish; each workgroup loops over its row blocks.
-std::mutex g_occ_mu;
-std::map<std::tuple<const void*, size_t, int>, int> g_occ;
-
-int resident_workgroups(const void* kernel, size_t lds) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return kLMaxGrid;
-  std::lock_guard<std::mutex> lock(g_occ_mu);
-  auto key = std::make_tuple(kernel, lds, dev);
-  auto it = g_occ.find(key);
-  if (it != g_occ.end()) return it->second;
-  int per_cu = 0, cus = 0;
-  int r = kLMaxGrid;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kLT, lds) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && per_cu > 0 && cus > 0)
-    r = per_cu * cus;
-  g_occ[key] = r;
-  return r;
-}
 
 // The checks and the launch of hsd_linear.
 int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,
@@ -560,7 +539,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
 #define HSD_LIN_R(WF, NB, XK, YK, IM, RW)                                                             \
   {                                                                                                   \
     const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW>);               \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, lds)));                         \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds, kLMaxGrid)));                         \
     hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW>), dim3(g), dim3(kLT), lds, st, a);           \
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                      \

@@ -54,9 +54,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // (a NaN choice ranks below every number); the topk largest choices in descending order
 // (equal choices: the smaller expert id); gain_k = score_k / (sum of the selected scores +
 // 1e-20) * scale (norm_topk), else score_k * scale. E <= 256.
-// Each workgroup ranks the E choices itself (a choice's rank = the number of choices
-// before it in that order; thread e counts over the E choices in LDS), so no wavefront
-// reduction chain sits in front of the weight loads.
+// One wavefront ranks the experts: lane l holds experts l, l + 64, l + 128, l + 192 as keys
+// (the choice's order-preserving bits << 32 | ~id, so a larger key is a larger choice, then
+// a smaller id); topk rounds of a 64-lane maximum pick them in order. No LDS and no
+// barrier, so a workgroup of the up projection can afford it in front of its weight loads.
 struct Router {
   const uint16_t* logits;   // [B, E] bf16
   const float* bias;        // [E] f32 (nullable)
@@ -68,37 +69,63 @@ struct Router {
 constexpr int kMaxTopk = 8;
 constexpr int kMaxE = 256;
 
-// sel[0..topk) and gain[0..topk) of token b into LDS (every thread of the workgroup calls it)
-__device__ __forceinline__ void route_topk(const Router& rt, int b, int E, int topk, int tid, float* chs, float* scs,
-                                           int* tsel, float* tgain) {
-  if (tid < E) {
-    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + tid]);
-    const float sg = 1.0f / (1.0f + expf(-x));
-    const float c = sg + (rt.bias ? rt.bias[tid] : 0.0f);
-    chs[tid] = c != c ? -INFINITY : c;
-    scs[tid] = sg;
+__device__ __forceinline__ uint32_t ordered_bits(float c) {
+  const uint32_t u = __float_as_uint(c);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
+                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
+    k = o > k ? o : k;
   }
-  lds_barrier();
-  if (tid < E) {
-    const float v = chs[tid];
-    int r = 0;
-    for (int e = 0; e < E; e += 4) {                 // E % 4 == 0
-      const float4 c4 = *reinterpret_cast<const float4*>(&chs[e]);
-      r += (c4.x > v || (c4.x == v && e < tid)) ? 1 : 0;
-      r += (c4.y > v || (c4.y == v && e + 1 < tid)) ? 1 : 0;
-      r += (c4.z > v || (c4.z == v && e + 2 < tid)) ? 1 : 0;
-      r += (c4.w > v || (c4.w == v && e + 3 < tid)) ? 1 : 0;
+  return k;
+}
+
+// Token row b's experts e[0..topk) and gains g[0..topk) (every lane gets them); every lane
+// of one wavefront calls it.
+__device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, int topk, int lane,
+                                                int (&e_out)[kMaxTopk], float (&g_out)[kMaxTopk]) {
+  uint64_t key[4];
+  float sg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    const int ec = min(e, E - 1);
+    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + ec]);
+    const float s = 1.0f / (1.0f + expf(-x));
+    float c = s + (rt.bias ? rt.bias[ec] : 0.0f);
+    c = c != c ? -INFINITY : c;
+    key[i] = e < E ? ((uint64_t)ordered_bits(c) << 32) | (uint32_t)~(uint32_t)e : 0;
+    sg[i] = s;
+  }
+  float ssum = 0.0f;
+  float sc[kMaxTopk];
+#pragma unroll
+  for (int r = 0; r < kMaxTopk; ++r) {
+    e_out[r] = 0;
+    sc[r] = 0.0f;
+    if (r < topk) {                                    // uniform
+      uint64_t m = key[0];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) m = key[i] > m ? key[i] : m;
+      m = wave_max_u64(m);
+      const int e = (int)~(uint32_t)m;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) key[i] = key[i] == m ? 0 : key[i];
+      const int ii = e >> 6;
+      const float own = ii == 0 ? sg[0] : ii == 1 ? sg[1] : ii == 2 ? sg[2] : sg[3];
+      const float s = __shfl(own, e & 63, 64);
+      e_out[r] = e;
+      sc[r] = s;
+      ssum += s;
     }
-    if (r < topk) tsel[r] = tid;
   }
-  lds_barrier();
-  if (tid < topk) {
-    float ssum = 0.0f;
-    for (int k = 0; k < topk; ++k) ssum += scs[tsel[k]];
-    const float s = scs[tsel[tid]];
-    tgain[tid] = rt.norm_topk ? s / (ssum + 1e-20f) * rt.scale : s * rt.scale;
-  }
-  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < kMaxTopk; ++r)
+    g_out[r] = rt.norm_topk ? sc[r] / (ssum + 1e-20f) * rt.scale : sc[r] * rt.scale;
 }
 
 template <bool ROUTE>
@@ -132,15 +159,31 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
     xv[i] = reinterpret_cast<const uint4*>(x + (size_t)b * D)[min(tid + kUpThreads * i, NW - 1)];
   int e;
   if constexpr (ROUTE) {
-    __shared__ __attribute__((aligned(16))) float chs[kMaxE];
-    __shared__ float scs[kMaxE];
+    // wavefront 0 ranks the experts (a routed block needs its id; block 0 writes the row's
+    // selection and gains); the shared expert's blocks skip it
     __shared__ int tsel[kMaxTopk];
-    __shared__ float tgain[kMaxTopk];
-    route_topk(rt, b, E, topk, tid, chs, scs, tsel, tgain);
-    e = routed ? tsel[k] : 0;
-    if (blk == 0 && tid <= topk) {                     // one writer per token row
-      if (tid < topk) rt.sel_out[b * topk + tid] = tsel[tid];
-      rt.gains_out[b * (topk + 1) + tid] = tid < topk ? tgain[tid] : 1.0f;
+    if (routed) {
+      if (wave == 0) {
+        int es[kMaxTopk];
+        float gs[kMaxTopk];
+        route_topk_wave(rt, b, E, topk, lane, es, gs);
+        int ek = es[0];
+        float gk = gs[0];
+#pragma unroll
+        for (int r = 1; r < kMaxTopk; ++r) {
+          ek = lane == r ? es[r] : ek;
+          gk = lane == r ? gs[r] : gk;
+        }
+        if (lane < topk) tsel[lane] = ek;
+        if (blk == 0 && lane <= topk) {               // one writer per token row
+          if (lane < topk) rt.sel_out[b * topk + lane] = ek;
+          rt.gains_out[b * (topk + 1) + lane] = lane < topk ? gk : 1.0f;
+        }
+      }
+      lds_barrier();
+      e = tsel[k];
+    } else {
+      e = 0;
     }
   } else {
     e = routed ? sel[b * topk + k] : 0;
@@ -269,18 +312,23 @@ __global__ __launch_bounds__(kUpThreads) void k_moe_up(
   if (!ok && tid == 0 && f0 == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
 }
 
-// The router's top-k alone: one workgroup per token row writes sel and gains (the shared
+// The router's top-k alone: one wavefront per token row writes sel and gains (the shared
 // expert's gain 1.0 last).
-__global__ __launch_bounds__(kUpThreads) void k_router_topk(Router rt, int E, int topk) {
-  __shared__ __attribute__((aligned(16))) float chs[kMaxE];
-  __shared__ float scs[kMaxE];
-  __shared__ int tsel[kMaxTopk];
-  __shared__ float tgain[kMaxTopk];
-  const int b = blockIdx.x, tid = threadIdx.x;
-  route_topk(rt, b, E, topk, tid, chs, scs, tsel, tgain);
-  if (tid <= topk) {
-    if (tid < topk) rt.sel_out[b * topk + tid] = tsel[tid];
-    rt.gains_out[b * (topk + 1) + tid] = tid < topk ? tgain[tid] : 1.0f;
+__global__ __launch_bounds__(64) void k_router_topk(Router rt, int E, int topk) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  int es[kMaxTopk];
+  float gs[kMaxTopk];
+  route_topk_wave(rt, b, E, topk, lane, es, gs);
+  int ek = es[0];
+  float gk = gs[0];
+#pragma unroll
+  for (int r = 1; r < kMaxTopk; ++r) {
+    ek = lane == r ? es[r] : ek;
+    gk = lane == r ? gs[r] : gk;
+  }
+  if (lane <= topk) {
+    if (lane < topk) rt.sel_out[b * topk + lane] = ek;
+    rt.gains_out[b * (topk + 1) + lane] = lane < topk ? gk : 1.0f;
   }
 }
 
@@ -355,6 +403,6 @@ extern "C" int hsd_router_topk(const uint16_t* logits, const float* e_bias, floa
     return set_error(HSD_ERR_SHAPE, "%s: need topk <= %d, topk <= E <= %d, E %% 4 == 0", fn, kMaxTopk, kMaxE);
   if (B == 0) return HSD_OK;
   Router rt{logits, e_bias, sel, gains, routed_scale, norm_topk};
-  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)B), dim3(kUpThreads), 0, as_stream(stream), rt, (int)E, (int)topk);
+  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)B), dim3(64), 0, as_stream(stream), rt, (int)E, (int)topk);
   return check_launch(fn);
 }

@@ -32,7 +32,7 @@ import torch
 
 from . import _native as N
 from . import layout, mamba as M, nn
-from .moe import router_topk, up_relu2
+from .moe import route_up_relu2, router_topk, up_relu2
 
 NSLAB = 4          # Mamba checkpoint ring: a verify of up to 3 rows
 ROWS = (1, 3)      # row counts with preallocated buffers: decode, verify / prefill steps
@@ -222,13 +222,20 @@ class MoEBlock:
         c = self.cfg
         xn = buf["xn"][:B]
         logits = nn.linear(x, self.gate, norm=self.norm_w, eps=c.eps, out=buf["logits"][:B], xn_out=xn)
-        # the router's top-k as a kernel of its own, then the up projections with the experts
-        # read from memory: measured faster than the top-k fused into every up-projection
-        # workgroup (14.5 against 18.0 us per layer at one row, 25.3 against 39.9 at three)
-        sel, gains = router_topk(logits, self.e_bias, topk=c.topk, routed_scale=c.routed_scale,
-                                 norm_topk=c.norm_topk, sel=buf["sel"][:B], gains=buf["gains"][:B])
-        hcat = up_relu2(xn, sel, self.w1, self.s1, self.b1, self.sw1, self.ss1, self.sb1, topk=c.topk,
-                        out=buf["hcat"][:B])
+        if B == 1:
+            # one row: the router's top-k fused into the up projections (a wavefront of every
+            # routed workgroup ranks the experts), one launch fewer: 12.2 against 13.9 us
+            hcat, sel, gains = route_up_relu2(xn, logits, self.e_bias, self.w1, self.s1, self.b1, self.sw1,
+                                              self.ss1, self.sb1, topk=c.topk, routed_scale=c.routed_scale,
+                                              norm_topk=c.norm_topk, out=buf["hcat"][:B], sel=buf["sel"][:B],
+                                              gains=buf["gains"][:B])
+        else:
+            # three rows: three times the ranking work in the fused form (28.7 us), so the
+            # router runs on its own first (25.1 us for both); same selection, same bits
+            sel, gains = router_topk(logits, self.e_bias, topk=c.topk, routed_scale=c.routed_scale,
+                                     norm_topk=c.norm_topk, sel=buf["sel"][:B], gains=buf["gains"][:B])
+            hcat = up_relu2(xn, sel, self.w1, self.s1, self.b1, self.sw1, self.ss1, self.sb1, topk=c.topk,
+                            out=buf["hcat"][:B])
         if self.trace is not None:                       # calibration / statistics only
             self.trace.append(float((hcat == 0).float().mean().item()))
         ws = buf["ws_down"]
