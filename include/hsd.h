@@ -275,9 +275,16 @@ int hsd_spec_accept(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, 
 /* Replaces the chaining of hsd/model.py:408-414: from the MTP head's first call over 3
  * pending rows (R = seq[HSD_SEQ_R] valid), d1[0] = the argmax of row R-1, h2 = its normed
  * hidden row hn[R-1] (D bf16), and seq[HSD_SEQ_HEAD_POS2] = HEAD_POS + R (the cache row of
- * the chained call). */
+ * the chained call). key_ld = 0 and hn_ld = 0: the keys and hn hold that one row already
+ * (hsd_seq_select_row before lm_head). */
 int hsd_mtp_chain(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, const uint16_t* hn,
                   int64_t hn_ld, int64_t D, int32_t* seq, int32_t* d1, uint16_t* h2, void* stream);
+
+/* The row of the MTP head's first call whose prediction is the first draft (model.py:408-411:
+ * only the last confirmed row's argmax is used): dst [D] = src[R-1] (bf16, row stride src_ld;
+ * R = seq[HSD_SEQ_R] clamped to [1, 3]), so that lm_head runs on one row. */
+int hsd_seq_select_row(const uint16_t* src, int64_t src_ld, const int32_t* seq, uint16_t* dst, int64_t D,
+                       void* stream);
 
 /* The verify ids of hsd/model.py:416: ids = [TOK, d1[0], argmax(keys2)] for k = 2 drafts.
  * With `script` (the true continuation, indexed by N) and `accepts` (an accepted count

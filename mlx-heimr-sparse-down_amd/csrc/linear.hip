@@ -68,8 +68,6 @@ template <> struct WTraits<HSD_W_Q4> {
 template <> struct WTraits<HSD_W_BF16> {
   static constexpr int kIn = 8;
 };
-// pieces of one row per lane for rows of up to I inputs
-template <int WF> constexpr int pieces_per_lane(int I) { return (I / WTraits<WF>::kIn + 63) / 64; }
 
 struct LinArgs {
   const void* x;
@@ -102,17 +100,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
-// IMAX: the largest row length the instance serves (kIt pieces of a row per lane, XIT x
+// IMAX: the largest row length the instance serves (kFull full passes of 64 pieces, XIT x
 // words of 8 inputs per thread in the prologue).
 // RW: output rows per wavefront (a block = 4 RW rows). Lane l owns pieces l, l + 64, ... of
 // each of its wavefront's RW rows, so an x piece read from LDS serves RW rows.
-template <int WF, int NB, int XK, int YK, int IMAX, int RW>
-__global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
+// At one token row the projections with a single block per workgroup (in_proj: 644
+// blocks) want three workgroups per CU (8.5 against 9.1 us); lm_head (many blocks per
+// workgroup, the next block in flight) is faster with the registers of two (49 against 59 us).
+template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM>
+__global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void k_linear(LinArgs a) {
   using T = WTraits<WF>;
-  constexpr int kRW = RW, kIt = pieces_per_lane<WF>(IMAX);
+  constexpr int kRW = RW;
+  constexpr int kFull = (IMAX / T::kIn) / 64 > 0 ? (IMAX / T::kIn) / 64 : 1;  // full passes (max)
+  constexpr int kRP = REM ? (kRW * 63 + 63) / 64 : 1;  // remainder passes (max; none without REM)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   constexpr int kRows = 4 * kRW;                       // rows per block
-  constexpr int kSc = WF == HSD_W_Q4 ? kIt : 1;
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
   // LDS: x as bf16 pairs [NB][I/2] (4-bit: pairs (x[i], x[i+4]) in a word's nibble
   // order, word m of 32-input piece j at [m][j]; bf16: natural pairs), then the 32-input
@@ -125,28 +127,52 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nblk = (O + kRows - 1) / kRows;            // the last block may be partial
   const int NPr = I / T::kIn;                          // pieces per row
-  const int nit = (NPr + 63) / 64;
+  // pieces 0 .. 64 nfull - 1 of every row: lane l owns pieces l + 64 it of each of the
+  // wavefront's kRW rows; the nrem pieces left of each row are dealt as (row, piece) pairs
+  // over the lanes, so no pass runs with most lanes idle (84 pieces a row at I = 2688: one
+  // full pass and two pair passes instead of two full passes with 20 lanes busy in the
+  // second)
+  const int nfull = NPr / 64, nrem = REM ? NPr - 64 * nfull : 0;
+  const int npair = kRW * nrem, npass = (npair + 63) / 64;
+  int prr[kRP], prj[kRP];                              // a pair's row and piece
+#pragma unroll
+  for (int ps = 0; ps < kRP; ++ps) {
+    const int p = min(lane + 64 * ps, max(npair - 1, 0));
+    prr[ps] = nrem > 0 ? p / nrem : 0;
+    prj[ps] = min(64 * nfull + (p - prr[ps] * max(nrem, 1)), NPr - 1);
+  }
 
-  // ---- weight pieces of a block: piece j = lane + 64 it of each of the wave's kRW rows
-  // (rows past O re-read row O-1, pieces past the row re-read its last piece; unused)
-  auto load_block = [&](int blk, uint4 (&qq)[kRW][kIt], uint32_t (&sb)[kRW][kSc]) {
+  // ---- weight pieces of a block (rows past O re-read row O-1, pieces past the row re-read
+  // its last piece; unused)
+  struct Blk {
+    uint4 q[kRW][kFull];
+    uint32_t s[kRW][kFull];
+    uint4 qr[kRP];
+    uint32_t sr[kRP];
+  };
+  auto load_piece = [&](int row, int j, uint4& qq, uint32_t& sq) {
+    if constexpr (WF == HSD_W_Q4) {
+      const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)row * NW;
+      qq = reinterpret_cast<const uint4*>(wr)[j];
+      const size_t gi = (size_t)row * (I / 64) + (j >> 1);
+      sq = (uint32_t)a.s[gi] | ((uint32_t)a.bq[gi] << 16);
+    } else {
+      const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w) + (size_t)row * I;
+      qq = reinterpret_cast<const uint4*>(wr)[j];
+      sq = 0;
+    }
+  };
+  auto load_block = [&](int blk, Blk& bk) {
     const int r0 = blk * kRows + kRW * wave;
 #pragma unroll
     for (int r = 0; r < kRW; ++r) {
       const int row = min(r0 + r, O - 1);
 #pragma unroll
-      for (int it = 0; it < kIt; ++it) {
-        const int j = min(lane + 64 * it, NPr - 1);
-        if constexpr (WF == HSD_W_Q4) {
-          const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)row * NW;
-          qq[r][it] = reinterpret_cast<const uint4*>(wr)[j];
-          const size_t gi = (size_t)row * (I / 64) + (j >> 1);
-          sb[r][it] = (uint32_t)a.s[gi] | ((uint32_t)a.bq[gi] << 16);
-        } else {
-          const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.w) + (size_t)row * I;
-          qq[r][it] = reinterpret_cast<const uint4*>(wr)[j];
-        }
-      }
+      for (int it = 0; it < kFull; ++it) load_piece(row, min(lane + 64 * it, NPr - 1), bk.q[r][it], bk.s[r][it]);
+    }
+    if constexpr (REM) {
+#pragma unroll
+      for (int ps = 0; ps < kRP; ++ps) load_piece(min(r0 + prr[ps], O - 1), prj[ps], bk.qr[ps], bk.sr[ps]);
     }
   };
 
@@ -173,10 +199,9 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   }
   // the first block's weight pieces, issued after x: the prologue waits for x only (loads
   // complete in issue order), while the weights are still on their way
-  uint4 q[kRW][kIt];
-  uint32_t sb[kRW][kSc];
+  Blk cur;
   int blk = blockIdx.x;
-  load_block(blk, q, sb);
+  load_block(blk, cur);
   // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
   uint32_t xo[NB][XIT][4];
   if constexpr (XK == HSD_X_BF16) {
@@ -285,24 +310,63 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   }
   __syncthreads();
 
+  // one 16-byte piece j of a row against the token rows: the partial of each token row
+  auto piece_terms = [&](int j, const uint4& qv, uint32_t sq, float (&t)[NB]) {
+    if constexpr (WF == HSD_W_Q4) {
+      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+      uint32_t wc[4][4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
+        wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
+        wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
+        wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
+      }
+      const float sv = lo_f(sq), bv = hi_f(sq);
+      const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
+          acc = dot2_bf16(xq.x, wc[m][0], acc);
+          acc = dot2_bf16(xq.y, wc[m][1], acc);
+          acc = dot2_bf16(xq.z, wc[m][2], acc);
+          acc = dot2_bf16(xq.w, wc[m][3], acc);
+        }
+        t[b] = fmaf(s16, acc, bo * xh[b * (I / 32) + j]);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
+        float acc = 0.0f;
+        acc = dot2_bf16(xq.x, qv.x, acc);
+        acc = dot2_bf16(xq.y, qv.y, acc);
+        acc = dot2_bf16(xq.z, qv.z, acc);
+        acc = dot2_bf16(xq.w, qv.w, acc);
+        t[b] = acc;
+      }
+    }
+  };
+
   // ---- one block: the lane's pieces into per-row partials, the 64-lane sums, the epilogue
   uint64_t best[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
-  auto do_block = [&](int blk_, const uint4 (&qq)[kRW][kIt], const uint32_t (&sbq)[kRW][kSc]) {
+  auto do_block = [&](int blk_, const Blk& bk) {
     float pr[NB][kRW];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int r = 0; r < kRW; ++r) pr[b][r] = 0.0f;
+    if constexpr (WF == HSD_W_Q4) {
+      // full passes: the x piece read once from LDS serves the wavefront's kRW rows
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      if (it < nit) {                                   // uniform
-        const int j0 = lane + 64 * it;
-        const bool use = j0 < NPr;
-        const int j = min(j0, NPr - 1);
-        if constexpr (WF == HSD_W_Q4) {
-          // the token rows' x piece j (32 inputs) and its sum, read once for the kRW rows
+      for (int it = 0; it < kFull; ++it) {
+        if (it < nfull) {                                // uniform
+          const int j = lane + 64 * it;
           uint4 xq[NB][4];
           float xs[NB];
 #pragma unroll
@@ -313,7 +377,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
           }
 #pragma unroll
           for (int r = 0; r < kRW; ++r) {
-            const uint32_t qw[4] = {qq[r][it].x, qq[r][it].y, qq[r][it].z, qq[r][it].w};
+            const uint32_t qw[4] = {bk.q[r][it].x, bk.q[r][it].y, bk.q[r][it].z, bk.q[r][it].w};
             uint32_t wc[4][4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -322,7 +386,7 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
               wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
               wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
             }
-            const float sv = lo_f(sbq[r][it]), bv = hi_f(sbq[r][it]);
+            const float sv = lo_f(bk.s[r][it]), bv = hi_f(bk.s[r][it]);
             const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -334,10 +398,16 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
                 acc = dot2_bf16(xq[b][m].z, wc[m][2], acc);
                 acc = dot2_bf16(xq[b][m].w, wc[m][3], acc);
               }
-              pr[b][r] += use ? fmaf(s16, acc, bo * xs[b]) : 0.0f;
+              pr[b][r] += fmaf(s16, acc, bo * xs[b]);
             }
           }
-        } else {
+        }
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kFull; ++it) {
+        if (it < nfull) {                                // uniform
+          const int j = lane + 64 * it;
           uint4 xq[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) xq[b] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
@@ -346,14 +416,27 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
               float acc = 0.0f;
-              acc = dot2_bf16(xq[b].x, qq[r][it].x, acc);
-              acc = dot2_bf16(xq[b].y, qq[r][it].y, acc);
-              acc = dot2_bf16(xq[b].z, qq[r][it].z, acc);
-              acc = dot2_bf16(xq[b].w, qq[r][it].w, acc);
-              pr[b][r] += use ? acc : 0.0f;
+              acc = dot2_bf16(xq[b].x, bk.q[r][it].x, acc);
+              acc = dot2_bf16(xq[b].y, bk.q[r][it].y, acc);
+              acc = dot2_bf16(xq[b].z, bk.q[r][it].z, acc);
+              acc = dot2_bf16(xq[b].w, bk.q[r][it].w, acc);
+              pr[b][r] += acc;
             }
           }
         }
+      }
+    }
+    // pair passes: lane l's pair p = l + 64 ps is piece prj of row prr of the wavefront
+#pragma unroll
+    for (int ps = 0; ps < kRP; ++ps) {
+      if (REM && ps < npass) {                           // uniform
+        const bool use = lane + 64 * ps < npair;
+        float t[NB];
+        piece_terms(prj[ps], bk.qr[ps], bk.sr[ps], t);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int r = 0; r < kRW; ++r) pr[b][r] += (use && prr[ps] == r) ? t[b] : 0.0f;
       }
     }
     // row sums: lane b*kRW + r ends with row r of token row b
@@ -407,26 +490,19 @@ __global__ __launch_bounds__(kLT) void k_linear(LinArgs a) {
   };
 
   if ((int)gridDim.x >= nblk) {
-    do_block(blk, q, sb);                              // one block per workgroup
+    do_block(blk, cur);                                // one block per workgroup
   } else {
     // several blocks: the next block's pieces are in flight while one is computed; the
     // load is unconditional (the last block re-reads its own lines), so the compiler's
     // wait before the arithmetic counts only the current block's loads
     for (;;) {
       const int nxt = blk + (int)gridDim.x;
-      uint4 qn[kRW][kIt];
-      uint32_t sbn[kRW][kSc];
-      load_block(nxt < nblk ? nxt : blk, qn, sbn);
-      do_block(blk, q, sb);
+      Blk nx;
+      load_block(nxt < nblk ? nxt : blk, nx);
+      do_block(blk, cur);
       if (nxt >= nblk) break;
       blk = nxt;
-#pragma unroll
-      for (int r = 0; r < kRW; ++r)
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-          q[r][it] = qn[r][it];
-          if constexpr (WF == HSD_W_Q4) sb[r][it] = sbn[r][it];
-        }
+      cur = nx;
     }
   }
   if constexpr (YK == HSD_Y_ARGMAX) {
@@ -523,7 +599,9 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
             argmax_keys, key_ld, slots, (int)O, (int)I};
   const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
   hipStream_t st = as_stream(stream);
-  const bool small = I <= (w_kind == HSD_W_Q4 ? kLSmallQ4 : 3072);
+  // IMAX 3072 (pieces left over after full passes: dealt as pairs), 4096 for 4-bit rows of
+  // exactly 128 pieces (no pairs), the maximum otherwise
+  const int isz = I <= 3072 ? 0 : (w_kind == HSD_W_Q4 && I == kLSmallQ4) ? 1 : 2;
   const int grid = slots;
   // the (x_kind, y_kind) pairs this library instantiates
   const int pair = x_kind * 8 + y_kind;
@@ -538,9 +616,10 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
                      y_kind, w_kind);
 #define HSD_LIN_R(WF, NB, XK, YK, IM, RW)                                                             \
   {                                                                                                   \
-    const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW>);               \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds, kLMaxGrid)));                         \
-    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW>), dim3(g), dim3(kLT), lds, st, a);           \
+    constexpr bool REM = !(WF == HSD_W_Q4 && IM == kLSmallQ4);                                        \
+    const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW, REM>);          \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds, kLMaxGrid)));          \
+    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), lds, st, a);      \
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                      \
   {                                                      \
@@ -550,9 +629,10 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
       HSD_LIN_R(WF, NB, XK, YK, IM, 1)                   \
     }                                                    \
   }
-#define HSD_LIN_I(WF, NB, XK, YK)                                              \
-  if (small) HSD_LIN(WF, NB, XK, YK, (WF == HSD_W_Q4 ? kLSmallQ4 : 3072)) else \
-    HSD_LIN(WF, NB, XK, YK, kLMaxI)
+#define HSD_LIN_I(WF, NB, XK, YK)                          \
+  if (isz == 0) HSD_LIN(WF, NB, XK, YK, 3072)              \
+  else if (WF == HSD_W_Q4 && isz == 1) HSD_LIN(WF, NB, XK, YK, kLSmallQ4) \
+  else HSD_LIN(WF, NB, XK, YK, kLMaxI)
 #define HSD_LIN_P(WF, NB)                                                  \
   switch (pair) {                                                          \
     case kRB: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_BF16); break;             \

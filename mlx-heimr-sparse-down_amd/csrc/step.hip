@@ -168,6 +168,14 @@ __global__ __launch_bounds__(256) void k_mtp_chain(const uint64_t* __restrict__ 
   for (int i = threadIdx.x; i < D; i += 256) h2[i] = hn[(size_t)r * hn_ld + i];
 }
 
+// dst = src row R-1 (R = the pending-row count, clamped to [1, 3]).
+__global__ __launch_bounds__(256) void k_select_row(const uint16_t* __restrict__ src, int64_t src_ld,
+                                                    const int32_t* __restrict__ seq, uint16_t* __restrict__ dst,
+                                                    int D) {
+  const int r = min(max(seq[HSD_SEQ_R], 1), 3) - 1;
+  for (int i = threadIdx.x; i < D; i += 256) dst[i] = src[(size_t)r * src_ld + i];
+}
+
 // The verify ids [tok, d_0 .. d_{k-1}]: d_0 = the chained call's input prediction, d_1
 // = the chained call's argmax (k = 2). With `script` (true tokens, indexed by the count
 // of emitted tokens) and `accepts` (one accepted-draft count per step), the drafts are
@@ -294,9 +302,19 @@ extern "C" int hsd_mtp_chain(const uint64_t* argmax_keys, int64_t key_ld, int64_
                              int64_t hn_ld, int64_t D, int32_t* seq, int32_t* d1, uint16_t* h2, void* stream) {
   const char* fn = "hsd_mtp_chain";
   if (!argmax_keys || !hn || !seq || !d1 || !h2) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
-  if (slots <= 0 || slots > key_ld || D <= 0 || hn_ld < D) return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  if (slots <= 0 || (key_ld != 0 && slots > key_ld) || D <= 0 || (hn_ld != 0 && hn_ld < D) || key_ld < 0 || hn_ld < 0)
+    return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
   hipLaunchKernelGGL(k_mtp_chain, dim3(1), dim3(256), 0, as_stream(stream), argmax_keys, key_ld, (int)slots, hn,
                      hn_ld, (int)D, seq, d1, h2);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_seq_select_row(const uint16_t* src, int64_t src_ld, const int32_t* seq, uint16_t* dst, int64_t D,
+                                  void* stream) {
+  const char* fn = "hsd_seq_select_row";
+  if (!src || !seq || !dst) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (D <= 0 || D > (1 << 24) || src_ld < D) return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  hipLaunchKernelGGL(k_select_row, dim3(1), dim3(256), 0, as_stream(stream), src, src_ld, seq, dst, (int)D);
   return check_launch(fn);
 }
 

@@ -430,7 +430,8 @@ class NemotronModel:
                     # MTP head
                     pair=e(B, 2 * c.hidden), emb=e(B, c.hidden), hx=e(B, c.hidden), hn=e(B, c.hidden),
                     pend=e(4, dt=torch.int32), d1=e(4, dt=torch.int32), keys2=e(1, self.slots, dt=torch.int64),
-                    h2=e(1, c.hidden))
+                    h2=e(1, c.hidden), x1=e(1, c.hidden), hn1=e(1, c.hidden),
+                    keys1=e(1, self.slots, dt=torch.int64))
 
     def moe_blocks(self):
         out = [b for t, b in zip(self.cfg.pattern, self.blocks) if t == "E"]
@@ -667,10 +668,14 @@ class NemotronModel:
         b3, b1 = self._bufs[3], self._bufs[1]
         c = self.cfg
         st = N.stream(self.device)
-        # the head over the rows the last verify confirmed (R of them valid)
-        self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos, keys=b3["keys"])
-        N.call("hsd_mtp_chain", N.ptr(b3["keys"]), b3["keys"].stride(0), self.slots, N.ptr(b3["hn"]),
-               b3["hn"].stride(0), c.hidden, N.ptr(cache.seq), N.ptr(b3["d1"]), N.ptr(b1["h2"]), st)
+        # the head over the rows the last verify confirmed (R of them valid); only row R-1's
+        # prediction is a draft (model.py:408-411), so lm_head runs on that row alone
+        x3 = self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos)
+        N.call("hsd_seq_select_row", N.ptr(x3), x3.stride(0), N.ptr(cache.seq), N.ptr(b1["x1"]), c.hidden, st)
+        nn.linear(b1["x1"], self.lm_head, norm=self.mtp.final_norm, eps=c.eps, argmax_keys=b1["keys1"],
+                  xn_out=b1["hn1"])
+        N.call("hsd_mtp_chain", N.ptr(b1["keys1"]), 0, self.slots, N.ptr(b1["hn1"]), 0, c.hidden, N.ptr(cache.seq),
+               N.ptr(b3["d1"]), N.ptr(b1["h2"]), st)
         # the chained call on its own normed hidden row (mtp.py, model.py:411-413)
         self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"])
         ids = b3["ids"]
