@@ -3,8 +3,8 @@
 // the shared expert, ReLU^2, written to hcat [B, topk*F + FS] (bf16), plus the canonical
 // live mask of every 64-row group (the decode kernels' compaction input).
 //
-// k_moe_up: one workgroup per (token, 8-row block of hcat): 4 wavefronts x 2 rows, so a
-// 64-row mask group takes eight workgroups (each writes its byte of the group's mask).
+// k_moe_up: one workgroup per (token, 16-row block of hcat): 4 wavefronts x 4 rows, so a
+// 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
 //   1. one round trip: the token's x, the block's expert id (a scalar load), the 8 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
 //      share of its 2 rows' 16-byte pieces (2 D/32 pieces dealt over the 64 lanes in
@@ -30,14 +30,16 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kUpWaves = 4;
 constexpr int kUpThreads = 64 * kUpWaves;
-constexpr int kUpRows = 2;                      // rows per wavefront
+constexpr int kUpRows = 4;                      // rows per wavefront
 constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (an eighth of a mask group)
 constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS
 constexpr int kUpMaxP = kUpMaxD / 32;
 constexpr int kUpXIt = (kUpMaxD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
               "a block is a quarter or an eighth of a mask group; one scale load per thread");
-// Small workgroups measured faster than 64-row ones (1024 threads; 9.0 us per call with 8
+// 16-row workgroups (4 rows per wavefront): at three token rows 19.0 against 19.8 us per
+// call for 8-row ones (fewer rounds of workgroups), at one row the same. Small workgroups
+// measured faster than 64-row ones (1024 threads; 9.0 us per call with 8
 // rows, 9.1 with 16, 10.1 with 64): a workgroup starts its arithmetic as soon as its own
 // loads are in, and 1856 workgroups fill all CUs at the reference shape where 232 left 24
 // idle.
