@@ -5,9 +5,9 @@
 //
 // k_moe_up: one workgroup per (token, 16-row block of hcat): 4 wavefronts x 4 rows, so a
 // 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
-//   1. one round trip: the token's x, the block's expert id (a scalar load), the 8 rows'
+//   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
-//      share of its 2 rows' 16-byte pieces (2 D/32 pieces dealt over the 64 lanes in
+//      share of its 4 rows' 16-byte pieces (4 D/32 pieces dealt over the 64 lanes in
 //      turn, so every lane has the same count but the last round);
 //   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
 //      and the sum of x over every 32-input piece;
