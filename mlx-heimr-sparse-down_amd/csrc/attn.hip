@@ -9,9 +9,9 @@
 // written into the cache at P .. P+B-1; the cache is read only below P, so no kernel reads
 // what this launch writes.
 //
-//   k_attn_part: one workgroup per (kv head, 64-key chunk, half of the kv head's query
+//   k_attn_part: one workgroup per (kv head, 64-key chunk, 4 of the kv head's 16 query
 //     heads). The chunk's keys go to LDS (rows padded by 16 bytes against bank
-//     conflicts); lane j of wave w scores key j against query heads 2w, 2w+1 (a q.k dot in
+//     conflicts); lane j of wave w scores key j against query head w (a q.k dot in
 //     fp32 with v_dot2_f32_bf16 in four partial sums, times the scale); a wave's max and
 //     sum over its 64 keys (DPP); then p = exp(s - m) times V (LDS) into acc[128] (even and
 //     odd keys in separate sums). Writes the chunk's (m, l, acc) per row and head.
@@ -30,7 +30,10 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kHD = 128;        // head dim
 constexpr int kCH = 64;         // keys per chunk
 constexpr int kAMaxB = 4;
-constexpr int kHPW = 8;         // query heads per workgroup (2 per wavefront)
+constexpr int kHPW = 4;         // query heads per workgroup (one per wavefront)
+constexpr int kHW = kHPW / 4;   // query heads per wavefront in the scores
+constexpr int kTPH = 256 / kHPW;  // threads per head in the value sum
+constexpr int kDPT = 128 / kTPH;  // head dims per thread there
 constexpr int kKP = kHD / 2 + 4;  // padded K row in u32 (272 bytes)
 constexpr int kAT = 256;
 constexpr int kRec = kHD + 4;     // partial record: m, l, 2 unused, acc[128] (16-byte aligned)
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
         reinterpret_cast<uint4*>(a.vc + ((size_t)g * a.smax + j) * kHD)[piece] = vv;
       }
     }
-    // queries: B rows x 8 heads x 16 pieces
+    // queries: B rows x kHPW heads x 16 pieces
     for (int i = tid; i < B * kHPW * 16; i += kAT) {
       const int r = i / (kHPW * 16), rem2 = i - r * kHPW * 16, h = rem2 >> 4, pc = rem2 & 15;
       const uint4 qv = reinterpret_cast<const uint4*>(a.qkv + (size_t)r * a.qkv_ld + (hq0 + h) * kHD)[pc];
@@ -108,9 +111,9 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- scores: lane = key j, wave w = heads 2w, 2w+1
+  // ---- scores: lane = key j, wave w = heads kHW w .. kHW w + kHW - 1
   const int j = j0 + lane;
-  float m[kAMaxB][2], l[kAMaxB][2];
+  float m[kAMaxB][kHW], l[kAMaxB][kHW];
   {
     uint32_t kr[kHD / 2];
 #pragma unroll
@@ -123,8 +126,8 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
       if (r < B) {                               // uniform
         const bool vis = j <= P + r;
 #pragma unroll
-        for (int hi = 0; hi < 2; ++hi) {
-          const int h = 2 * wave + hi;
+        for (int hi = 0; hi < kHW; ++hi) {
+          const int h = kHW * wave + hi;
           // four partial dot products (16-byte pieces i % 4), so that four dependency chains
           // of 16 interleave instead of one of 64
           float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -161,48 +164,49 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- acc = sum_j p_j v_j: thread = (head h = tid / 32, dims 4 (tid % 32) .. +3)
+  // ---- acc = sum_j p_j v_j: thread = (head h = tid / kTPH, dims kDPT (tid % kTPH) ..)
   {
-    const int h = tid >> 5, d0 = 4 * (tid & 31);
+    const int h = tid / kTPH, d0 = kDPT * (tid % kTPH);
     // two accumulator sets (even and odd keys), added at the end: twice the independent
     // chains for the latency of the fma and LDS reads
-    float acc[kAMaxB][4], acc2[kAMaxB][4];
+    float acc[kAMaxB][kDPT], acc2[kAMaxB][kDPT];
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[r][e] = acc2[r][e] = 0.0f;
+      for (int e = 0; e < kDPT; ++e) acc[r][e] = acc2[r][e] = 0.0f;
 #pragma unroll 4
     for (int jl = 0; jl < kCH; jl += 2) {
-      const uint2 va = *reinterpret_cast<const uint2*>(&vs[jl][d0 / 2]);
-      const uint2 vb = *reinterpret_cast<const uint2*>(&vs[jl + 1][d0 / 2]);
-      const float a0 = bf16_bits_to_f32(va.x & 0xFFFFu), a1 = bf16_bits_to_f32(va.x >> 16);
-      const float a2 = bf16_bits_to_f32(va.y & 0xFFFFu), a3 = bf16_bits_to_f32(va.y >> 16);
-      const float b0 = bf16_bits_to_f32(vb.x & 0xFFFFu), b1 = bf16_bits_to_f32(vb.x >> 16);
-      const float b2 = bf16_bits_to_f32(vb.y & 0xFFFFu), b3 = bf16_bits_to_f32(vb.y >> 16);
+      float va[kDPT], vb[kDPT];
+#pragma unroll
+      for (int e = 0; e < kDPT; e += 2) {
+        const uint32_t wa = vs[jl][d0 / 2 + e / 2], wb = vs[jl + 1][d0 / 2 + e / 2];
+        va[e] = bf16_bits_to_f32(wa & 0xFFFFu);
+        va[e + 1] = bf16_bits_to_f32(wa >> 16);
+        vb[e] = bf16_bits_to_f32(wb & 0xFFFFu);
+        vb[e + 1] = bf16_bits_to_f32(wb >> 16);
+      }
 #pragma unroll
       for (int r = 0; r < kAMaxB; ++r) {
         if (r < B) {
           const float2 p = *reinterpret_cast<const float2*>(&ps[r][h][jl]);
-          acc[r][0] = fmaf(p.x, a0, acc[r][0]);
-          acc[r][1] = fmaf(p.x, a1, acc[r][1]);
-          acc[r][2] = fmaf(p.x, a2, acc[r][2]);
-          acc[r][3] = fmaf(p.x, a3, acc[r][3]);
-          acc2[r][0] = fmaf(p.y, b0, acc2[r][0]);
-          acc2[r][1] = fmaf(p.y, b1, acc2[r][1]);
-          acc2[r][2] = fmaf(p.y, b2, acc2[r][2]);
-          acc2[r][3] = fmaf(p.y, b3, acc2[r][3]);
+#pragma unroll
+          for (int e = 0; e < kDPT; ++e) {
+            acc[r][e] = fmaf(p.x, va[e], acc[r][e]);
+            acc2[r][e] = fmaf(p.y, vb[e], acc2[r][e]);
+          }
         }
       }
     }
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[r][e] += acc2[r][e];
+      for (int e = 0; e < kDPT; ++e) acc[r][e] += acc2[r][e];
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r) {
       if (r < B && j0 <= P + r) {
-        float* dst = a.part + (((size_t)r * HQ + hq0 + h) * a.nch + c) * kRec;
-        *reinterpret_cast<float4*>(dst + 4 + d0) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        float* dst = a.part + (((size_t)r * HQ + hq0 + h) * a.nch + c) * kRec + 4 + d0;
+#pragma unroll
+        for (int e = 0; e < kDPT; e += 2) *reinterpret_cast<float2*>(dst + e) = make_float2(acc[r][e], acc[r][e + 1]);
       }
     }
   }
@@ -212,8 +216,8 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
     for (int r = 0; r < kAMaxB; ++r) {
       if (r < B && j0 <= P + r) {
 #pragma unroll
-        for (int hi = 0; hi < 2; ++hi) {
-          float* dst = a.part + (((size_t)r * HQ + hq0 + 2 * wave + hi) * a.nch + c) * kRec;
+        for (int hi = 0; hi < kHW; ++hi) {
+          float* dst = a.part + (((size_t)r * HQ + hq0 + kHW * wave + hi) * a.nch + c) * kRec;
           dst[0] = m[r][hi];
           dst[1] = l[r][hi];
         }
