@@ -193,6 +193,26 @@ def time_graphs_cold(graphs, steps, flush):
     return tot
 
 
+def launch_floors(dev, nbytes, ntok, steps, warm):
+    """What one call cannot beat on this machine, timed like the calls (graphs of NL
+    back-to-back launches, ntok graphs rotated): a one-element fill (the launch floor), and
+    a copy of the call's algorithmic byte count from a pool larger than the 256 MB Infinity
+    Cache (one launch streaming that many bytes from HBM, plus the same written back)."""
+    tiny = torch.zeros(1, device=dev)
+    n4 = max(nbytes // 4, 64)
+    pool = torch.ones((ntok, NL, n4), dtype=torch.float32, device=dev)
+    dst = torch.empty(n4, dtype=torch.float32, device=dev)
+    g_fill = capture_steps(lambda t, l: tiny.fill_(float(l)), ntok)
+    us_fill = 1e3 * time_graphs(g_fill, steps, warm) / (steps * NL)
+    g_copy = capture_steps(lambda t, l: dst.copy_(pool[t, l]), ntok)
+    us_copy = 1e3 * time_graphs(g_copy, steps, warm) / (steps * NL)
+    del g_fill, g_copy, pool
+    return dict(empty_launch_us=round(us_fill, 3), two_launch_us=round(2 * us_fill, 3),
+                stream_copy_us=round(us_copy, 3), stream_copy_bytes=int(4 * n4),
+                note="a call of two dependent launches cannot beat two_launch_us; stream_copy_us is one "
+                     "launch reading the call's byte count from HBM and writing it back")
+
+
 def cpu_baseline_decode(layers, h, sel, gains, budget_s=15.0):
     """The oracle (NumPy, float64 accumulation) on host cores over a bounded sample of the
     same workload: token-layers in order until ~budget_s of CPU time."""
@@ -291,6 +311,9 @@ def bench_decode(args):
     log(f"[decode] sparse: {ms_step * 1e3:.1f} us/token (23 layers), {gbs:.0f} GB/s touched, "
         f"{per_launch_bytes / 1e6:.2f} MB/layer")
     extra = {}
+    floor = launch_floors(dev, int(per_launch_bytes), ntok, steps, warm)
+    log(f"[decode] floors: empty launch {floor['empty_launch_us']:.2f} us, one-launch copy of "
+        f"{per_launch_bytes / 1e6:.2f} MB {floor['stream_copy_us']:.2f} us; the call: {per_launch_us:.2f} us")
     # dense-h control: the same kernel reading every row
     graphs_dh = capture_steps(lambda t, l: sparse_layer(t, l, dense=True), min(ntok, 8))
     ms_dh = time_graphs(graphs_dh, steps, warm)
@@ -331,7 +354,8 @@ def bench_decode(args):
                roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                              frac=round(achieved / HBM_PEAK_GBS, 4), traffic=pmc_traffic("decode"),
                              kernel="k_sparse_down_part + k_sum_parts (one decode call)",
-                             bytes_per_launch=int(per_launch_bytes), us_per_launch=round(per_launch_us, 3)),
+                             bytes_per_launch=int(per_launch_bytes), us_per_launch=round(per_launch_us, 3),
+                             floor=floor),
                cpu_baseline=cpu,
                down_proj_tok_s=round(1e3 / ms_step, 1),
                layout_permute=dict(ms_23_layers=round(perm_ms, 2), gbs_rw=round(perm_bytes / perm_ms / 1e6, 1)),

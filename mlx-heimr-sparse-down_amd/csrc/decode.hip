@@ -391,6 +391,157 @@ __global__ __launch_bounds__(64 * kDenseWaves) void k_dense_down(
   }
 }
 
+// The comparator for bf16 h, organised like the projections' GEMV: a workgroup (4
+// wavefronts) owns kDQRows consecutive outputs of one token row, kDQRW per wavefront.
+// Lane l owns pieces l, l + 64, ... (16 bytes, 32 neurons) of the slots' concatenated rows
+// (topk F + FS neurons: 464 pieces at the reference shape) for its wavefront's outputs.
+// The slot ids and h are loaded first, then every weight, scale and bias load is issued
+// before the lane waits for h. h goes to LDS once per
+// workgroup as bf16 pairs in a word's nibble order, with the sum of every piece. Per
+// piece: a shift, a mask and an OR turn each nibble into a bf16 (1 + q/16) pair,
+// v_dot2_f32_bf16 accumulates h (1 + q/16) in fp32, and the lane adds
+// gain * (16 s acc + (b - 16 s) hsum) (W = s q + b folded per piece); a DPP sum gives y.
+// Loads are never under a branch: a piece past the row or of a bad slot reads a valid
+// address and is dropped by a select.
+// Measured per call at the reference shape: 11.7 us with one output per wavefront, 13.1
+// with two. With the weights issued before h (the wait for h then waited for every
+// weight): 14.7 us with one output per wavefront, 15.7 with two, 17.3 with four, 16.1 with
+// 8-wavefront workgroups, 18.3 with 2-wavefront ones.
+constexpr int kDQRW = 1;                 // outputs per wavefront
+constexpr int kDQWaves = 4;
+constexpr int kDQRows = kDQRW * kDQWaves;
+constexpr int kDQPass = 8;               // pieces per lane: (topk F + FS) / 32 <= 512
+constexpr int kDQXIt = kDQPass * 64 * 4 / (64 * kDQWaves);  // h words (8 values) per thread
+constexpr uint32_t kBfOne2 = 0x3F803F80u;
+constexpr uint32_t kNibHi = 0x00780078u;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+template <int YDT>
+__global__ __launch_bounds__(64 * kDQWaves) void k_dense_down_q(
+    const uint16_t* __restrict__ h, const int32_t* __restrict__ sel, const float* __restrict__ gains,
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ bias,
+    const uint32_t* __restrict__ sw, const uint16_t* __restrict__ ss, const uint16_t* __restrict__ sbias,
+    typename Elem<YDT>::T* __restrict__ y, int32_t* __restrict__ status, int D, int F, int FS, int topk,
+    int E) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t qsm[];
+  const int NR = topk * F + FS, NP = NR / 32, NW = NR / 8;
+  uint32_t* xp = qsm;                                    // word m of piece j at 4 (m NP + j)
+  float* xh = reinterpret_cast<float*>(qsm + NR / 2);    // piece sums
+  const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int o0 = blockIdx.x * kDQRows + wave * kDQRW;
+  const int ur = F / 32;
+  // ---- loads in the order they are waited for: the slots' ids and gains, h (neither
+  // depends on the other), then the weights, whose addresses need the ids
+  int ek[kDQPass];
+  float gn[kDQPass];
+#pragma unroll
+  for (int it = 0; it < kDQPass; ++it) {
+    const int u = min(lane + 64 * it, NP - 1);
+    const int k = u < topk * ur ? u / ur : topk;
+    gn[it] = gains[b * (topk + 1) + k];
+    ek[it] = sel[b * topk + min(k, topk - 1)];
+  }
+  // words t = tid + 64 kDQWaves i hold neurons 8t .. 8t+7
+  uint4 hv[kDQXIt];
+#pragma unroll
+  for (int i = 0; i < kDQXIt; ++i)
+    hv[i] = reinterpret_cast<const uint4*>(h + (size_t)b * NR)[min(tid + 64 * kDQWaves * i, NW - 1)];
+  // this lane's pieces: where row o of the piece's matrix starts
+  const uint32_t* rowp[kDQPass];
+  const uint16_t* scp[kDQPass];
+  const uint16_t* bip[kDQPass];
+  int rstride[kDQPass], gstride[kDQPass];
+  bool pv[kDQPass];
+#pragma unroll
+  for (int it = 0; it < kDQPass; ++it) {
+    const int u = min(lane + 64 * it, NP - 1);
+    const bool routed = u < topk * ur;
+    const int k = routed ? u / ur : topk;
+    const int uu = routed ? u - k * ur : u - topk * ur;
+    const int e = routed ? ek[it] : 0;
+    const bool ok = (unsigned)e < (unsigned)E;
+    pv[it] = lane + 64 * it < NP && ok;
+    if (routed && !ok && uu == 0 && lane + 64 * it < NP && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
+    const size_t eo = ok ? (size_t)e : 0;
+    rstride[it] = routed ? F / 8 : FS / 8;
+    gstride[it] = routed ? F / 64 : FS / 64;
+    rowp[it] = routed ? w + eo * D * (F / 8) + 4 * uu : sw + 4 * uu;
+    scp[it] = routed ? s + eo * D * (F / 64) + uu / 2 : ss + uu / 2;
+    bip[it] = routed ? bias + eo * D * (F / 64) + uu / 2 : sbias + uu / 2;
+  }
+  uint4 q[kDQRW][kDQPass];
+  uint32_t sb[kDQRW][kDQPass];
+#pragma unroll
+  for (int it = 0; it < kDQPass; ++it) {
+#pragma unroll
+    for (int r = 0; r < kDQRW; ++r) {
+      const size_t o = (size_t)min(o0 + r, D - 1);
+      q[r][it] = *reinterpret_cast<const uint4*>(rowp[it] + o * rstride[it]);
+      sb[r][it] = (uint32_t)scp[it][o * gstride[it]] | ((uint32_t)bip[it][o * gstride[it]] << 16);
+    }
+  }
+  // ---- h into LDS as bf16 pairs (h[8t + n], h[8t + n + 4]) in the order of a word's
+  // nibble pairs, and the piece sums
+#pragma unroll
+  for (int i = 0; i < kDQXIt; ++i) {
+    const int t = tid + 64 * kDQWaves * i;
+    const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+    if (t < NW) {
+      uint4 pr;
+      pr.x = (hw[0] & 0xFFFFu) | (hw[2] << 16);
+      pr.y = (hw[0] >> 16) | (hw[2] & 0xFFFF0000u);
+      pr.z = (hw[1] & 0xFFFFu) | (hw[3] << 16);
+      pr.w = (hw[1] >> 16) | (hw[3] & 0xFFFF0000u);
+      *reinterpret_cast<uint4*>(&xp[4 * ((t & 3) * NP + (t >> 2))]) = pr;
+    }
+    float s8 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s8 = dot2_bf16(hw[c], kBfOne2, s8);
+    s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
+    s8 += dpp_f32<0x4E>(s8);
+    if (t < NW && (t & 3) == 0) xh[t >> 2] = s8;
+  }
+  lds_barrier();
+  // ---- the lane's pieces against its wavefront's outputs
+  float tot[kDQRW];
+#pragma unroll
+  for (int r = 0; r < kDQRW; ++r) tot[r] = 0.0f;
+#pragma unroll
+  for (int it = 0; it < kDQPass; ++it) {
+    const int j = min(lane + 64 * it, NP - 1);
+    uint4 xq[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xq[m] = *reinterpret_cast<const uint4*>(&xp[4 * (m * NP + j)]);
+    const float xs = xh[j];
+#pragma unroll
+    for (int r = 0; r < kDQRW; ++r) {
+      const uint32_t qw[4] = {q[r][it].x, q[r][it].y, q[r][it].z, q[r][it].w};
+      float acc = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        acc = dot2_bf16(xq[m].x, ((qw[m] << 3) & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].y, ((qw[m] >> 1) & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].z, ((qw[m] >> 5) & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].w, ((qw[m] >> 9) & kNibHi) | kBfOne2, acc);
+      }
+      const float sv = lo_bf16(sb[r][it]), bv = hi_bf16(sb[r][it]);
+      const float u = fmaf(16.0f * sv, acc, fmaf(-16.0f, sv, bv) * xs);
+      tot[r] = pv[it] ? fmaf(gn[it], u, tot[r]) : tot[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kDQRW; ++r) {
+    const float v = wave_sum_dpp(tot[r]);
+    const int o = o0 + r;
+    if (lane == 0 && o < D) Elem<YDT>::store(y, (size_t)b * D + o, v);
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -607,6 +758,24 @@ extern "C" int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* 
     case HSD_DT_F16: HSD_DENSE(HD, HSD_DT_F16); break;           \
     case HSD_DT_F32: HSD_DENSE(HD, HSD_DT_F32); break;           \
     default: return set_error(HSD_ERR_DTYPE, "%s: y_dtype %d", fn, y_dtype); \
+  }
+  if (h_dtype == HSD_DT_BF16 && aligned16(h)) {  // bf16 h: the GEMV-shaped kernel
+    if (NR > 64 * 32 * kDQPass) return set_error(HSD_ERR_SHAPE, "%s: h row of %lld elements too long", fn, (long long)NR);
+    dim3 gq((unsigned)((D + kDQRows - 1) / kDQRows), (unsigned)B);
+    const size_t lq = (size_t)NR * 2 + (size_t)(NR / 32) * 4;
+#define HSD_DENSE_Q(YD)                                                                           \
+  hipLaunchKernelGGL((k_dense_down_q<YD>), gq, dim3(64 * kDQWaves), lq, st,                       \
+                     reinterpret_cast<const uint16_t*>(h), sel, gains, w, s, b, sw, ss, sb,        \
+                     reinterpret_cast<typename Elem<YD>::T*>(y), dev_status, (int)D, (int)F, (int)FS, \
+                     (int)topk, (int)E)
+    switch (y_dtype) {
+      case HSD_DT_BF16: HSD_DENSE_Q(HSD_DT_BF16); break;
+      case HSD_DT_F16: HSD_DENSE_Q(HSD_DT_F16); break;
+      case HSD_DT_F32: HSD_DENSE_Q(HSD_DT_F32); break;
+      default: return set_error(HSD_ERR_DTYPE, "%s: y_dtype %d", fn, y_dtype);
+    }
+#undef HSD_DENSE_Q
+    return check_launch(fn);
   }
   switch (h_dtype) {
     case HSD_DT_BF16: HSD_DENSE_Y(HSD_DT_BF16); break;

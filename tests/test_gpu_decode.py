@@ -110,15 +110,31 @@ def test_bad_expert_id_is_flagged_and_skipped(layer, dev):
     assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
-def test_dense_stock_comparator(layer, dev):
+@pytest.mark.parametrize("h_dtype", [torch.bfloat16, torch.float32])
+def test_dense_stock_comparator(layer, dev, h_dtype):
+    """bf16 h takes the GEMV-shaped kernel (pieces of the 7 slots' rows per lane), f32 h the
+    element-wise one; both against the oracle's dequantise-then-mat-vec (float64), and a
+    bad expert id adds nothing and sets the status bit."""
     h, sel, gains = S.decode_inputs_np(18, B=2, zero_frac=0.9)
     dv = layer["dev"]
-    y = decode.dense_down(S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev), dv["w"], dv["s"],
-                          dv["b"], dv["sw"], dv["ss"], dv["sb"], out_dtype=torch.float32, **KW)
+    hd = S.to_device(h, dev).to(h_dtype)
     lay = layer["np"]
+    y = decode.dense_down(hd, S.to_device(sel, dev), S.to_device(gains, dev), dv["w"], dv["s"],
+                          dv["b"], dv["sw"], dv["ss"], dv["sb"], out_dtype=torch.float32, **KW)
     ref = O.dense_reference(O.bf16_to_f32(h), sel, gains, lay["w"], lay["s"], lay["b"], lay["sw"], lay["ss"],
                             lay["sb"], **KW)
     assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+    bad = sel.copy()
+    bad[1, 4] = -3
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    yb = decode.dense_down(hd, S.to_device(bad, dev), S.to_device(gains, dev), dv["w"], dv["s"], dv["b"], dv["sw"],
+                           dv["ss"], dv["sb"], out_dtype=torch.float32, status=status, **KW)
+    g0 = gains.copy()
+    g0[1, 4] = 0.0
+    ref_b = O.dense_reference(O.bf16_to_f32(h), sel, g0, lay["w"], lay["s"], lay["b"], lay["sw"], lay["ss"],
+                              lay["sb"], **KW)
+    assert int(status.item()) == 1
+    assert np.abs(yb.cpu().numpy() - ref_b).max() <= 1e-5 * np.abs(ref_b).max()
 
 
 @pytest.mark.parametrize("zero_frac", [0.85, 0.9, 0.95])
