@@ -22,6 +22,9 @@
 // with a shift, a mask and an OR, and v_dot2_f32_bf16 accumulates x (1 + q/16); per
 // 32-input piece u += 16 s acc + (b - 16 s) sum(x) (the affine dequantisation folded per
 // piece). A row's 64 lane partials are summed with DPP in a fixed order.
+// 4-bit projections of more 16-row blocks than one grid (lm_head) run on the matrix cores
+// instead (k_linear_q4 below): at several token rows the per-row dot products above bound
+// them.
 //
 // Every token row is computed by the same instruction sequence whatever B is: a row of a
 // B-row call is bit-identical to the same row alone (verify rows == decode rows).
@@ -36,6 +39,8 @@ namespace hsd {
 namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLT = 256;                 // threads per workgroup
 constexpr int kLMaxB = 4;                // token rows per launch
@@ -100,13 +105,162 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
+// The prologue on x, shared by the kernels: this workgroup's copy of the NB input rows,
+// normalised if asked, into LDS as bf16 pairs (4-bit weights: pairs (x[i], x[i+4]) in the
+// order of a word's nibble pairs, word m of 32-input piece j at [m][j]; bf16: natural
+// pairs), and for 4-bit weights the input sums of every PS inputs (32: a piece, 64: a
+// group). load() issues the loads; the caller issues its first weight loads next, so
+// finish() waits for x only (loads complete in issue order) while the weights are still
+// on their way. Words t = tid + 256 i hold inputs 8t .. 8t+7.
+template <int WF, int NB, int XK, int XIT>
+struct XIn {
+  uint4 xv[NB][XIT];
+  float4 yv0[XK == HSD_X_GATED ? NB : 1][XIT], yv1[XK == HSD_X_GATED ? NB : 1][XIT];
+  uint4 nwv[XIT];
+
+  __device__ __forceinline__ void load(const LinArgs& a, int tid) {
+    const int NW = a.I / 8;
+#pragma unroll
+    for (int i = 0; i < XIT; ++i) {
+      const int tc = min(tid + kLT * i, NW - 1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if constexpr (XK == HSD_X_GATED) {
+          const float4* yr = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + b * a.x_ld);
+          yv0[b][i] = yr[2 * tc];
+          yv1[b][i] = yr[2 * tc + 1];
+          xv[b][i] = reinterpret_cast<const uint4*>(a.gate + b * a.gate_ld)[tc];
+        } else {
+          xv[b][i] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + b * a.x_ld)[tc];
+        }
+      }
+      if constexpr (XK != HSD_X_BF16) nwv[i] = reinterpret_cast<const uint4*>(a.nw)[tc];
+    }
+  }
+
+  template <int PS>
+  __device__ __forceinline__ void finish(const LinArgs& a, uint32_t* xp, float* xs, float (*wsum)[4], int tid,
+                                         int lane, int wave) {
+    const int I = a.I, NW = I / 8;
+    // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
+    uint32_t xo[NB][XIT][4];
+    if constexpr (XK == HSD_X_BF16) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < XIT; ++i) {
+          xo[b][i][0] = xv[b][i].x; xo[b][i][1] = xv[b][i].y; xo[b][i][2] = xv[b][i].z; xo[b][i][3] = xv[b][i].w;
+        }
+    } else if constexpr (XK == HSD_X_RMS) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XIT; ++i) {
+          const bool tv = tid + kLT * i < NW;
+          const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t v = tv ? xw[c] : 0u;
+            ss = dot2_bf16(v, v, ss);
+          }
+        }
+        ss = wave_sum_dpp(ss);
+        if (lane == 0) wsum[b][wave] = ss;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float tot = ((wsum[b][0] + wsum[b][1]) + wsum[b][2]) + wsum[b][3];
+        const float inv = __builtin_amdgcn_rsqf(tot / (float)I + a.eps);
+#pragma unroll
+        for (int i = 0; i < XIT; ++i) {
+          const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+          const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t t = pack_bf16x2(lo_f(xw[c]) * inv, hi_f(xw[c]) * inv);
+            xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
+          }
+        }
+      }
+    } else {  // HSD_X_GATED: a wavefront's 64 words of iteration i are one 512-element group
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int i = 0; i < XIT; ++i) {
+          const bool tv = tid + kLT * i < NW;
+          const uint32_t gw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
+          const float yy[8] = {yv0[b][i].x, yv0[b][i].y, yv0[b][i].z, yv0[b][i].w,
+                               yv1[b][i].x, yv1[b][i].y, yv1[b][i].z, yv1[b][i].w};
+          float z[8];
+          float g = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            z[2 * c] = tv ? yy[2 * c] * silu_f32(lo_f(gw[c])) : 0.0f;
+            z[2 * c + 1] = tv ? yy[2 * c + 1] * silu_f32(hi_f(gw[c])) : 0.0f;
+            g = fmaf(z[2 * c], z[2 * c], g);
+            g = fmaf(z[2 * c + 1], z[2 * c + 1], g);
+          }
+          g = wave_sum_dpp(g);
+          const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
+          const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t t = pack_bf16x2(z[2 * c] * inv, z[2 * c + 1] * inv);
+            xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
+          }
+        }
+      }
+    }
+    // ---- into LDS (and the side output)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int i = 0; i < XIT; ++i) {
+        const int t = tid + kLT * i;
+        const uint32_t* w = xo[b][i];
+        if (t < NW) {
+          uint4 pr;
+          if constexpr (WF == HSD_W_Q4) {
+            // pairs (x[8t + n], x[8t + n + 4]): element n of the word is half (n & 1) of w[n / 2]
+            pr.x = (w[0] & 0xFFFFu) | (w[2] << 16);
+            pr.y = (w[0] >> 16) | (w[2] & 0xFFFF0000u);
+            pr.z = (w[1] & 0xFFFFu) | (w[3] << 16);
+            pr.w = (w[1] >> 16) | (w[3] & 0xFFFF0000u);
+          } else {
+            pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
+          }
+          // 4-bit: word m of piece j at [m][j] (lanes holding consecutive pieces then read
+          // consecutive 16-byte words, free of bank conflicts); bf16: word t at t
+          const int slot = WF == HSD_W_Q4 ? (t & 3) * (I / 32) + (t >> 2) : t;
+          *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * slot]) = pr;
+          if (a.xn_out && blockIdx.x == 0)
+            reinterpret_cast<uint4*>(a.xn_out + b * a.xn_ld)[t] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if constexpr (WF == HSD_W_Q4) {
+          float s8 = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s8 = dot2_bf16(w[c], kBfOne2, s8);
+          s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
+          s8 += dpp_f32<0x4E>(s8);
+          if constexpr (PS == 64) s8 += dpp_f32<0x141>(s8);  // the other piece: row_half_mirror
+          constexpr int kWS = PS / 8;                        // words per sum
+          if (t < NW && (t & (kWS - 1)) == 0) xs[b * (I / PS) + t / kWS] = s8;
+        }
+      }
+    }
+  }
+};
+
 // IMAX: the largest row length the instance serves (kFull full passes of 64 pieces, XIT x
 // words of 8 inputs per thread in the prologue).
 // RW: output rows per wavefront (a block = 4 RW rows). Lane l owns pieces l, l + 64, ... of
 // each of its wavefront's RW rows, so an x piece read from LDS serves RW rows.
 // At one token row the projections with a single block per workgroup (in_proj: 644
-// blocks) want three workgroups per CU (8.5 against 9.1 us); lm_head (many blocks per
-// workgroup, the next block in flight) is faster with the registers of two (49 against 59 us).
+// blocks) want three workgroups per CU (8.5 against 9.1 us); the argmax instances (many
+// blocks per workgroup, the next block in flight: lm_head took 49 against 59 us here before
+// it moved to the matrix cores) are faster with the registers of two.
 template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM>
 __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void k_linear(LinArgs a) {
   using T = WTraits<WF>;
@@ -177,137 +331,14 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
   };
 
   // ---- prologue: this workgroup's copy of the NB input rows, normalised if asked
-  // words t = tid + 256 i hold inputs 8t .. 8t+7
-  uint4 xv[NB][XIT];
-  float4 yv0[XK == HSD_X_GATED ? NB : 1][XIT], yv1[XK == HSD_X_GATED ? NB : 1][XIT];
-  uint4 nwv[XIT];
-#pragma unroll
-  for (int i = 0; i < XIT; ++i) {
-    const int tc = min(tid + kLT * i, NW - 1);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if constexpr (XK == HSD_X_GATED) {
-        const float4* yr = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + b * a.x_ld);
-        yv0[b][i] = yr[2 * tc];
-        yv1[b][i] = yr[2 * tc + 1];
-        xv[b][i] = reinterpret_cast<const uint4*>(a.gate + b * a.gate_ld)[tc];
-      } else {
-        xv[b][i] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + b * a.x_ld)[tc];
-      }
-    }
-    if constexpr (XK != HSD_X_BF16) nwv[i] = reinterpret_cast<const uint4*>(a.nw)[tc];
-  }
+  XIn<WF, NB, XK, XIT> xin;
+  xin.load(a, tid);
   // the first block's weight pieces, issued after x: the prologue waits for x only (loads
   // complete in issue order), while the weights are still on their way
   Blk cur;
   int blk = blockIdx.x;
   load_block(blk, cur);
-  // xo[b][i][c]: the prologue's output elements 8t + 2c, 8t + 2c + 1 as a bf16 pair
-  uint32_t xo[NB][XIT][4];
-  if constexpr (XK == HSD_X_BF16) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < XIT; ++i) {
-        xo[b][i][0] = xv[b][i].x; xo[b][i][1] = xv[b][i].y; xo[b][i][2] = xv[b][i].z; xo[b][i][3] = xv[b][i].w;
-      }
-  } else if constexpr (XK == HSD_X_RMS) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int i = 0; i < XIT; ++i) {
-        const bool tv = tid + kLT * i < NW;
-        const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t v = tv ? xw[c] : 0u;
-          ss = dot2_bf16(v, v, ss);
-        }
-      }
-      ss = wave_sum_dpp(ss);
-      if (lane == 0) wsum[b][wave] = ss;
-    }
-    lds_barrier();
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const float tot = ((wsum[b][0] + wsum[b][1]) + wsum[b][2]) + wsum[b][3];
-      const float inv = __builtin_amdgcn_rsqf(tot / (float)I + a.eps);
-#pragma unroll
-      for (int i = 0; i < XIT; ++i) {
-        const uint32_t xw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
-        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t t = pack_bf16x2(lo_f(xw[c]) * inv, hi_f(xw[c]) * inv);
-          xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
-        }
-      }
-    }
-  } else {  // HSD_X_GATED: a wavefront's 64 words of iteration i are one 512-element group
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int i = 0; i < XIT; ++i) {
-        const bool tv = tid + kLT * i < NW;
-        const uint32_t gw[4] = {xv[b][i].x, xv[b][i].y, xv[b][i].z, xv[b][i].w};
-        const float yy[8] = {yv0[b][i].x, yv0[b][i].y, yv0[b][i].z, yv0[b][i].w,
-                             yv1[b][i].x, yv1[b][i].y, yv1[b][i].z, yv1[b][i].w};
-        float z[8];
-        float g = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          z[2 * c] = tv ? yy[2 * c] * silu_f32(lo_f(gw[c])) : 0.0f;
-          z[2 * c + 1] = tv ? yy[2 * c + 1] * silu_f32(hi_f(gw[c])) : 0.0f;
-          g = fmaf(z[2 * c], z[2 * c], g);
-          g = fmaf(z[2 * c + 1], z[2 * c + 1], g);
-        }
-        g = wave_sum_dpp(g);
-        const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
-        const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t t = pack_bf16x2(z[2 * c] * inv, z[2 * c + 1] * inv);
-          xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
-        }
-      }
-    }
-  }
-  // ---- into LDS (and the side output)
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-#pragma unroll
-    for (int i = 0; i < XIT; ++i) {
-      const int t = tid + kLT * i;
-      const uint32_t* w = xo[b][i];
-      if (t < NW) {
-        uint4 pr;
-        if constexpr (WF == HSD_W_Q4) {
-          // pairs (x[8t + n], x[8t + n + 4]): element n of the word is half (n & 1) of w[n / 2]
-          pr.x = (w[0] & 0xFFFFu) | (w[2] << 16);
-          pr.y = (w[0] >> 16) | (w[2] & 0xFFFF0000u);
-          pr.z = (w[1] & 0xFFFFu) | (w[3] << 16);
-          pr.w = (w[1] >> 16) | (w[3] & 0xFFFF0000u);
-        } else {
-          pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
-        }
-        // 4-bit: word m of piece j at [m][j] (lanes holding consecutive pieces then read
-        // consecutive 16-byte words, free of bank conflicts); bf16: word t at t
-        const int slot = WF == HSD_W_Q4 ? (t & 3) * (I / 32) + (t >> 2) : t;
-        *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * slot]) = pr;
-        if (a.xn_out && blockIdx.x == 0)
-          reinterpret_cast<uint4*>(a.xn_out + b * a.xn_ld)[t] = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-      if constexpr (WF == HSD_W_Q4) {
-        float s8 = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) s8 = dot2_bf16(w[c], kBfOne2, s8);
-        s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
-        s8 += dpp_f32<0x4E>(s8);
-        if (t < NW && (t & 3) == 0) xh[b * (I / 32) + (t >> 2)] = s8;
-      }
-    }
-  }
+  xin.template finish<32>(a, xp, xh, wsum, tid, lane, wave);
   __syncthreads();
 
   // one 16-byte piece j of a row against the token rows: the partial of each token row
@@ -521,6 +552,193 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
   }
 }
 
+// 4-bit weights on the matrix cores, for projections with more 16-row blocks than
+// resident workgroups (lm_head: 8192), where the per-token-row dot products of the kernel
+// above bound the time at several token rows. A workgroup (4 wavefronts) loops over blocks
+// of 16 consecutive output rows strided by the grid, the next block's weights and scales in
+// flight while one is computed; wavefront w takes the 64-input groups g = w, w + 4, ... of
+// the block's rows, and the four partial sums meet in LDS, added in wavefront order.
+// Per group, lane l (n = l % 16, q = l / 16) holds 8 bytes of row n: words 2 (q % 2) and
+// 2 (q % 2) + 1 of the group's piece q / 2. A word's 8 nibbles become the lane's B operand
+// of one v_mfma_f32_16x16x32_bf16 as four bf16 pairs (1 + q_j/16, 1 + q_{j+4}/16) (a shift,
+// a mask and an OR each, exact); the A operand is the same 8 inputs of token row l % 16
+// from LDS (rows from B on repeat row B-1; their outputs are not used). Two MFMAs give
+// acc[m][n] = sum over the group of x (1 + q/16) in fp32; then lane n adds
+// 16 s acc + (b - 16 s) sum_g(x) (W = s q + b folded per group) for the group's scale and
+// bias of row n, staged in LDS per block ([group][row]: the 16 lanes read 16 banks). The
+// vector-ALU work is the unpacking and the scale step, the same for any number of token
+// rows; a token row's result depends on its own row of A only, so it is the same bits
+// whatever B is. At one token row the kernel above is as fast (lm_head 49.7 against 51.8
+// us); at three, 51.0 against 84.0 us.
+// For projections of one round of blocks it was slower at one token row: in_proj 9.5
+// against 8.5 us, out_proj 8.3 against 5.9 (the MFMA chains of a wavefront's groups and the
+// cross-wavefront sum are on the critical path of a single block), and loading a 16-byte
+// piece per lane (two groups per load, the other group's lanes multiplying a zero A operand:
+// four MFMAs per group) slower still (in_proj 9.9, lm_head 57.0 us).
+constexpr int kQR = 16;                  // output rows per block (the MFMA's N)
+
+template <int NB, int XK, int YK, int IMAX>
+__global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
+  constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
+  constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
+  extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
+  __shared__ float wsum[NB][4];
+  __shared__ float red[2][4][NB][kQR];                 // [block parity][wavefront][token row][row]
+  const int I = a.I, O = a.O, G = I / 64, NPr = I / 32;
+  // LDS: x pairs [NB][I/2] words, the group sums [NB][G], then per block parity the
+  // (scale | bias << 16) words of the block's rows [2][G][16]
+  uint32_t* xp = lsm;
+  float* xg = reinterpret_cast<float*>(lsm + NB * (I / 2));
+  uint32_t* sbl = lsm + NB * (I / 2) + NB * G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, q = lane >> 4;
+  const int nblk = (O + kQR - 1) / kQR;
+
+  // a block's scales and biases: thread t < 16 G / 8 loads 8 consecutive (row, group)
+  // entries of each (the rows of a block are contiguous in [O][G])
+  auto load_sc = [&](int blk_, uint4& sv, uint4& bv) {
+    const int lim = min(kQR, O - blk_ * kQR) * G / 8;
+    const int t = min(tid, lim - 1);
+    sv = reinterpret_cast<const uint4*>(a.s + (size_t)blk_ * kQR * G)[t];
+    bv = reinterpret_cast<const uint4*>(a.bq + (size_t)blk_ * kQR * G)[t];
+  };
+  auto store_sc = [&](int par, int blk_, const uint4& sv, const uint4& bv) {
+    const int lim = min(kQR, O - blk_ * kQR) * G / 8;
+    if (tid < lim) {
+      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+      uint32_t* dst = sbl + par * kQR * G;
+      int r = (8 * tid) / G, g = 8 * tid - r * G;      // entry 8 tid + c: row r, group g
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sh = (c & 1) ? 16 : 0;
+        dst[g * kQR + r] = ((sw[c >> 1] >> sh) & 0xFFFFu) | (((bw[c >> 1] >> sh) & 0xFFFFu) << 16);
+        if (++g == G) { g = 0; ++r; }
+      }
+    }
+  };
+  // a block's weight words for this lane (groups past the row re-read the last group)
+  struct Wq {
+    uint2 w[kGW];
+  };
+  auto load_w = [&](int blk_, Wq& wb) {
+    const int row = min(blk_ * kQR + n, O - 1);
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)row * (I / 8) + 4 * (q >> 1) + 2 * (q & 1);
+#pragma unroll
+    for (int it = 0; it < kGW; ++it) wb.w[it] = *reinterpret_cast<const uint2*>(wr + 8 * min(wave + 4 * it, G - 1));
+  };
+
+  // ---- prologue: scales of the first block, x, the first block's weights
+  int blk = blockIdx.x;
+  uint4 sv, bv;
+  load_sc(blk, sv, bv);
+  XIn<HSD_W_Q4, NB, XK, XIT> xin;
+  xin.load(a, tid);
+  Wq cur;
+  load_w(blk, cur);
+  store_sc(0, blk, sv, bv);
+  xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
+  __syncthreads();
+
+  uint64_t best = 0;                                   // wavefront 0, lanes of token row l / 16
+  const int arow = min(n, NB - 1);                     // the token row of this lane's A operand
+  // one block: the wavefront's groups, its partial sums to LDS, then wavefront 0 adds the
+  // four partials and runs the epilogue. With next_sc, the next block's scales go to the
+  // other LDS parity before the barrier (their last readers were the previous block's).
+  auto do_block = [&](int blk_, const Wq& wb, int par, bool next_sc, int nblk_, const uint4& nsv,
+                      const uint4& nbv) {
+    float y[NB];
+#pragma unroll
+    for (int r = 0; r < NB; ++r) y[r] = 0.0f;
+    const uint32_t* sb = sbl + par * kQR * G;
+#pragma unroll
+    for (int it = 0; it < kGW; ++it) {
+      const int g = wave + 4 * it;
+      if (g < G) {                                     // uniform
+        const int p = 2 * g + (q >> 1);
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t qw = i ? wb.w[it].y : wb.w[it].x;
+          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * (I / 2) + 4 * ((2 * (q & 1) + i) * NPr + p)]);
+          const uint4 wq = make_uint4(((qw << 3) & kNibHi) | kBfOne2, ((qw >> 1) & kNibHi) | kBfOne2,
+                                      ((qw >> 5) & kNibHi) | kBfOne2, ((qw >> 9) & kNibHi) | kBfOne2);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
+                                                        acc, 0, 0, 0);
+        }
+        const uint32_t sq = sb[g * kQR + n];
+        const float sv_ = lo_f(sq), bv_ = hi_f(sq);
+        const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
+#pragma unroll
+        for (int r = 0; r < NB; ++r) y[r] += fmaf(s16, acc[r], bo * xg[r * G + g]);
+      }
+    }
+    // lanes 0..15 hold token rows 0..3 of output row n (acc[r]: token row 4 (l / 16) + r)
+    if (q == 0) {
+#pragma unroll
+      for (int r = 0; r < NB; ++r) red[par][wave][r][n] = y[r];
+    }
+    if (next_sc) store_sc(par ^ 1, nblk_, nsv, nbv);
+    __syncthreads();
+    if (wave == 0) {
+      const int m = q;                                 // token row of this lane
+      const int o = blk_ * kQR + n;
+      const bool live = m < NB && o < O;
+      const int mm = min(m, NB - 1);
+      const float v = ((red[par][0][mm][n] + red[par][1][mm][n]) + red[par][2][mm][n]) + red[par][3][mm][n];
+      if constexpr (YK == HSD_Y_ARGMAX) {
+        const uint16_t lb = f32_to_bf16_bits(v);
+        uint64_t key = live ? argmax_key(lb, o) : 0;
+        if (a.y && live) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + o] = lb;
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) {       // the best of the 16 lanes of token row m
+          const uint64_t ok = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), off, 64) << 32) |
+                              (uint32_t)__shfl_xor((int)(uint32_t)key, off, 64);
+          key = ok > key ? ok : key;
+        }
+        best = key > best ? key : best;
+      } else if (live) {
+        const int64_t yi = m * a.y_ld + o;
+        if constexpr (YK == HSD_Y_F32) {
+          reinterpret_cast<float*>(a.y)[yi] = v;
+        } else if constexpr (YK == HSD_Y_RESID) {
+          const float rv = bf16_bits_to_f32(a.res[m * a.res_ld + o]);
+          reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(rv + rne_bf16(v));
+        } else {
+          reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(v);
+        }
+      }
+    }
+  };
+
+  if ((int)gridDim.x >= nblk) {
+    do_block(blk, cur, 0, false, blk, sv, bv);         // one block per workgroup
+  } else {
+    // several blocks: the next block's scales and weights are in flight while one is
+    // computed (issued unconditionally: the last block re-reads its own lines)
+    int par = 0;
+    for (;;) {
+      const int nxt = blk + (int)gridDim.x;
+      const int nb = nxt < nblk ? nxt : blk;
+      uint4 nsv, nbv;
+      load_sc(nb, nsv, nbv);
+      Wq nx;
+      load_w(nb, nx);
+      do_block(blk, cur, par, nxt < nblk, nb, nsv, nbv);
+      if (nxt >= nblk) break;
+      blk = nxt;
+      cur = nx;
+      par ^= 1;
+    }
+  }
+  if constexpr (YK == HSD_Y_ARGMAX) {
+    if (wave == 0 && n == 0 && q < NB) {
+      a.keys[q * a.key_ld + blockIdx.x] = best;
+      // slots past the grid (the grid follows the occupancy) read as the smallest key
+      for (int sl = blockIdx.x + gridDim.x; sl < a.key_slots; sl += gridDim.x) a.keys[q * a.key_ld + sl] = 0;
+    }
+  }
+}
+
 // tok[b] = the index of the best key of row b (argmax with NaN first, then the larger
 // value, then the smaller index). One workgroup per row.
 __global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict__ keys, int64_t key_ld,
@@ -598,6 +816,12 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   LinArgs a{x, x_ld, gate, gate_ld, norm_w, eps, w, scales, biases, y, y_ld, res, res_ld, xn_out, xn_ld,
             argmax_keys, key_ld, slots, (int)O, (int)I};
   const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
+  // 4-bit projections of more 16-row blocks than one grid (lm_head) take the MFMA kernel;
+  // the choice depends on O only, so a token row is computed the same way at any B
+  const bool mfma = w_kind == HSD_W_Q4 && (O + kQR - 1) / kQR > kLMaxGrid;
+  if (mfma && (((uintptr_t)scales & 15u) || ((uintptr_t)biases & 15u)))
+    return set_error(HSD_ERR_ALIGN, "%s: scales and biases must be 16-byte aligned", fn);
+  const size_t lds_q4 = (size_t)B * (I / 2) * 4 + (size_t)B * (I / 64) * 4 + (size_t)2 * kQR * (I / 64) * 4;
   hipStream_t st = as_stream(stream);
   // IMAX 3072 (pieces left over after full passes: dealt as pairs), 4096 for 4-bit rows of
   // exactly 128 pieces (no pairs), the maximum otherwise
@@ -654,11 +878,40 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     case 3: HSD_LIN_P(WF, 3); break;         \
     default: HSD_LIN_P(WF, 4); break;        \
   }
-  if (w_kind == HSD_W_Q4) {
+#define HSD_Q4_R(NB, XK, YK, IM)                                                                  \
+  {                                                                                               \
+    const void* kf = reinterpret_cast<const void*>(&k_linear_q4<NB, XK, YK, IM>);                 \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds_q4, kLMaxGrid)));   \
+    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), lds_q4, st, a);         \
+  }
+#define HSD_Q4_I(NB, XK, YK)                                    \
+  if (I <= 3072) HSD_Q4_R(NB, XK, YK, 3072)                     \
+  else if (I <= kLSmallQ4) HSD_Q4_R(NB, XK, YK, kLSmallQ4)      \
+  else HSD_Q4_R(NB, XK, YK, kLMaxI)
+#define HSD_Q4_P(NB)                                                   \
+  switch (pair) {                                                      \
+    case kRB: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_BF16); break;              \
+    case kBB: HSD_Q4_I(NB, HSD_X_BF16, HSD_Y_BF16); break;             \
+    case kRA: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_ARGMAX); break;            \
+    case kRF: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_F32); break;               \
+    case kGR: HSD_Q4_I(NB, HSD_X_GATED, HSD_Y_RESID); break;           \
+    default: HSD_Q4_I(NB, HSD_X_BF16, HSD_Y_RESID); break;             \
+  }
+  if (mfma) {
+    switch (B) {
+      case 1: HSD_Q4_P(1); break;
+      case 2: HSD_Q4_P(2); break;
+      case 3: HSD_Q4_P(3); break;
+      default: HSD_Q4_P(4); break;
+    }
+  } else if (w_kind == HSD_W_Q4) {
     HSD_LIN_B(HSD_W_Q4);
   } else {
     HSD_LIN_B(HSD_W_BF16);
   }
+#undef HSD_Q4_P
+#undef HSD_Q4_I
+#undef HSD_Q4_R
 #undef HSD_LIN_B
 #undef HSD_LIN_P
 #undef HSD_LIN_I

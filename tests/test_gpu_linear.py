@@ -89,6 +89,39 @@ def test_rows_are_independent_and_epilogues_agree(dev):
     assert tok.tolist() == O.argmax_bf16(yb.float().cpu().numpy()).tolist()
 
 
+@pytest.mark.parametrize("I", [2688, 4096])
+def test_many_blocks_matrix_core_path(dev, I):
+    """O past 2048 blocks of 16 rows takes the MFMA kernel (lm_head's path): the oracle on
+    the first and last 1024 rows, rows independent of B, and the bf16 / residual / argmax
+    epilogues against the f32 output."""
+    O_ = 33024
+    (w, s, b), W = q4_weight(61 + I, O_, I, dev)
+    rng = np.random.default_rng(62)
+    nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))
+    nwd = S.to_device(nw, dev)
+    x, xd = bf16_rows(rng, 3, I, dev, 2.0)
+    xn = torch.empty((3, I), dtype=torch.bfloat16, device=dev)
+    y3 = nn.linear(xd, W, norm=nwd, out_dtype=torch.float32, xn_out=xn)
+    xn_h = S.to_host(xn)
+    yh = y3.cpu().numpy()
+    for rows in (slice(0, 1024), slice(O_ - 1024, O_)):
+        ref = O.linear_q4(O.bf16_to_f32(xn_h), w[rows], s[rows], b[rows])
+        assert np.abs(yh[:, rows] - ref).max() <= 1e-4 * np.abs(ref).max()
+    for r in range(3):
+        y1 = nn.linear(xd[r:r + 1], W, norm=nwd, out_dtype=torch.float32)
+        assert torch.equal(y1.view(torch.int32), y3[r:r + 1].view(torch.int32)), f"row {r}"
+    yb = nn.linear(xd, W, norm=nwd)
+    assert torch.equal(yb.view(torch.int16), y3.to(torch.bfloat16).view(torch.int16))
+    keys = torch.empty((3, nn.argmax_slots(O_)), dtype=torch.int64, device=dev)
+    nn.linear(xd, W, norm=nwd, argmax_keys=keys)
+    assert nn.argmax(keys).cpu().numpy().tolist() == O.argmax_bf16(yb.float().cpu().numpy()).tolist()
+    res = S.to_device(O.f32_to_bf16(rng.standard_normal((3, O_)).astype(np.float32)), dev)
+    yp = nn.linear(xd, W)
+    out = res.clone()
+    nn.linear(xd, W, residual=out, out=out)
+    assert torch.equal(out.view(torch.int16), (res.float() + yp.float()).to(torch.bfloat16).view(torch.int16))
+
+
 def test_residual_epilogue(dev):
     I, O_ = 4096, 2688
     (w, s, b), W = q4_weight(41, O_, I, dev)
