@@ -101,3 +101,42 @@ def test_python_layer_refuses_cpu_tensors():
     import torch
     with pytest.raises(N.HSDError):
         N.ptr(torch.zeros(4))
+
+
+def test_every_kernel_handle_has_device_code():
+    """Each kernel handle the host side of libhsd.so registers names a kernel of its gfx950
+    code object. A launch through a handle without one aborts the process in the HIP
+    runtime; a template argument whose type has no name (an unnamed enum) mangles
+    differently in the host and device compilations and produced exactly that."""
+    import shutil
+    import subprocess
+    import tempfile
+    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not (os.path.exists(bundler) and os.path.exists(readelf) and shutil.which("objcopy") and shutil.which("nm")):
+        pytest.skip("ROCm LLVM tools or binutils not installed")
+    so = N.LIB_PATH
+    with tempfile.TemporaryDirectory() as d:
+        fb, dev = os.path.join(d, "fb.bin"), os.path.join(d, "dev.o")
+        subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", so, fb], check=True)
+        blob = open(fb, "rb").read()
+        magic = b"__CLANG_OFFLOAD_BUNDLE__"
+        starts = [m.start() for m in re.finditer(re.escape(magic), blob)]
+        assert starts, "no offload bundle in libhsd.so"
+        devsyms = set()
+        for i, a in enumerate(starts):          # one bundle per object file
+            part = os.path.join(d, f"b{i}.bin")
+            with open(part, "wb") as f:
+                f.write(blob[a:starts[i + 1] if i + 1 < len(starts) else len(blob)])
+            subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={part}",
+                            f"--output={dev}", "--unbundle"], check=True)
+            devsyms |= {ln.split()[-1] for ln in subprocess.run([readelf, "-s", "-W", dev], check=True,
+                                                               capture_output=True, text=True).stdout.splitlines()
+                        if ln.strip()}
+    host = subprocess.run(["nm", so], check=True, capture_output=True, text=True).stdout.splitlines()
+    # kernel handles: local data symbols whose names are kernels of the code object's kind
+    handles = {ln.split()[2] for ln in host if len(ln.split()) == 3 and ln.split()[1] in "dD"
+               and "_GLOBAL__N_1" in ln.split()[2] and "k_" in ln.split()[2]}
+    assert handles, "no kernel handles found in libhsd.so"
+    missing = sorted(handles - devsyms)
+    assert not missing, f"{len(missing)} kernel handles without device code, e.g. {missing[:3]}"
