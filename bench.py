@@ -332,6 +332,9 @@ def bench_decode(args):
                                          speedup_sparse_vs_dense=round(ms_d / ms, 3))
         del graphs_d
         log(f"[decode] dense 4-bit (stock layout): {1e3 * ms_d / steps:.1f} us/token; sparse speedup {ms_d / ms:.2f}x")
+    sweep = batch_sweep(args, dev, layers, kw) if args.batch_sweep else []
+    if sweep:
+        extra["batch_sweep"] = sweep
     if args.cold:
         flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)                 # 1 GiB
         ncold = min(steps, 64)
@@ -361,6 +364,36 @@ def bench_decode(args):
                layout_permute=dict(ms_23_layers=round(perm_ms, 2), gbs_rw=round(perm_bytes / perm_ms / 1e6, 1)),
                **extra)
     return rec
+
+
+def batch_sweep(args, dev, layers, kw, ntok=8):
+    """The same 23-layer sparse down projection with B token rows per call (B independent
+    tokens, each with its own experts and activations: several sequences decoded at once),
+    timed like the batch-1 sweep (graphs of 23 calls, ntok graphs rotated). Bytes are the
+    per-row byte model summed over the rows (the rows' experts and live rows differ; the
+    shared expert's scales are counted once per row)."""
+    out = []
+    steps, warm = max(20, args.steps // 2), args.warmup
+    for B in [int(v) for v in args.batch_sweep.split(",") if v]:
+        hb, sb, gb = make_decode_inputs(dev, args.seed + 101 + B, ntok * B, args.zero_frac)
+        hb = hb.view(ntok, B, NL, NR).transpose(1, 2).contiguous()            # [ntok, NL, B, NR]
+        sb = sb.view(ntok, B, NL, K).transpose(1, 2).contiguous()
+        gb = gb.view(ntok, B, NL, K + 1).transpose(1, 2).contiguous()
+        tbb = touched_bytes_dev(hb).sum(-1)                                   # [ntok, NL]
+        wsb = [torch.empty(N.lib().hsd_sparse_down_workspace_bytes(B, D, F, FS, K), dtype=torch.uint8, device=dev)
+               for _ in range(NL)]
+        graphs = capture_steps(lambda t, l: decode.sparse_down(hb[t, l], sb[t, l], gb[t, l], *layers[l]["nm"],
+                                                               workspace=wsb[l], **kw), ntok)
+        ms = time_graphs(graphs, steps, warm)
+        nbytes = int(tbb[torch.arange(steps, device=dev) % ntok].sum().item())
+        us_call = 1e3 * ms / (steps * NL)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append(dict(rows=B, us_per_call=round(us_call, 3), mb_per_call=round(nbytes / (steps * NL) / 1e6, 2),
+                        gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
+        log(f"[decode] {B} rows per call: {us_call:.2f} us, {nbytes / (steps * NL) / 1e6:.1f} MB, {gbs:.0f} GB/s "
+            f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        del graphs, hb, sb, gb, wsb
+    return out
 
 
 # ------------------------------------------------------------------ prefill
@@ -835,6 +868,8 @@ def main():
     ap.add_argument("--hot", action="store_true", help="hot-neuron activation variant")
     ap.add_argument("--ntok", type=int, default=32, help="distinct tokens rotated (one graph each)")
     ap.add_argument("--cold", action="store_true", help="also time with a cache flush between tokens")
+    ap.add_argument("--batch-sweep", default="3,8,16,32,64",
+                    help="decode: token rows per call to time besides batch 1 (comma list; empty: skip)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense 4-bit comparator")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time (0: skip)")
     ap.add_argument("--layers", type=int, default=NL)
