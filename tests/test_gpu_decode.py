@@ -88,6 +88,40 @@ def test_rows_independent_of_batch(layer, dev):
         assert torch.equal(y1[0], y3[b])
 
 
+def test_many_rows(layer, dev):
+    """24 rows in one call (16128 workgroups, several rounds of what is resident): every row
+    equals the same row alone, bit for bit; rows against the oracle; live masks bit-exact;
+    a bad id in one row flagged and skipped; dense-h control equal."""
+    B = 24
+    h, sel, gains = S.decode_inputs_np(18, B=B, zero_frac=0.9)
+    sel[7, 1] = 4000
+    hd, seld, gd = S.to_device(h, dev), S.to_device(sel, dev), S.to_device(gains, dev)
+    masks = torch.zeros(B * (TOPK * F // 64 + FS // 64), dtype=torch.int64, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    y = decode.sparse_down(hd, seld, gd, *layer["nm"], out_dtype=torch.float32, live_masks=masks, status=status,
+                           **KW)
+    yd = decode.sparse_down(hd, seld, gd, *layer["nm"], out_dtype=torch.float32, dense=True, **KW)
+    assert int(status.item()) == 1
+    assert torch.equal(y, yd)
+    for b in range(B):
+        y1 = decode.sparse_down(hd[b:b + 1], seld[b:b + 1], gd[b:b + 1], *layer["nm"], out_dtype=torch.float32,
+                                **KW)
+        assert torch.equal(y1[0], y[b]), f"row {b}"
+    g0 = gains.copy()
+    g0[7, 1] = 0.0
+    s0 = sel.copy()
+    s0[7, 1] = 0
+    hf = O.bf16_to_f32(h)
+    for b in (0, 7, B - 1):
+        ref = O.sparse_down(hf[b:b + 1], s0[b:b + 1], g0[b:b + 1], *layer["nm_np"], **KW)
+        assert np.abs(y[b].cpu().numpy() - ref[0]).max() <= 1e-5 * np.abs(ref).max(), f"row {b}"
+    want = O.live_masks(hf, F, FS, TOPK).reshape(B, -1)
+    got = masks.cpu().numpy().view(np.uint64).reshape(B, -1)
+    ok = np.ones(B, dtype=bool)
+    ok[7] = False                                   # a bad id's slot reports no live rows
+    assert np.array_equal(got[ok], want[ok])
+
+
 @pytest.mark.parametrize("h_dtype", [torch.float32, torch.float16])
 def test_other_activation_dtypes(layer, dev, h_dtype):
     h, sel, gains, hd, y = run_case(layer, dev, 16, 1, 0.9, h_dtype=h_dtype)
