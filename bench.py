@@ -315,11 +315,12 @@ def bench_decode(args):
     log(f"[decode] floors: empty launch {floor['empty_launch_us']:.2f} us, one-launch copy of "
         f"{per_launch_bytes / 1e6:.2f} MB {floor['stream_copy_us']:.2f} us; the call: {per_launch_us:.2f} us")
     # dense-h control: the same kernel reading every row
-    graphs_dh = capture_steps(lambda t, l: sparse_layer(t, l, dense=True), min(ntok, 8))
-    ms_dh = time_graphs(graphs_dh, steps, warm)
-    extra["dense_h_control"] = dict(us_per_token=round(1e3 * ms_dh / steps, 2),
-                                    gbs=round(dense_bytes() * NL * steps / (ms_dh * 1e-3) / 1e9, 1))
-    del graphs_dh
+    if not args.no_control:
+        graphs_dh = capture_steps(lambda t, l: sparse_layer(t, l, dense=True), min(ntok, 8))
+        ms_dh = time_graphs(graphs_dh, steps, warm)
+        extra["dense_h_control"] = dict(us_per_token=round(1e3 * ms_dh / steps, 2),
+                                        gbs=round(dense_bytes() * NL * steps / (ms_dh * 1e-3) / 1e9, 1))
+        del graphs_dh
     if not args.no_dense:
         def dense_layer(t, l):
             st = layers[l]["stock"]
@@ -871,6 +872,8 @@ def main():
     ap.add_argument("--batch-sweep", default="3,8,16,32,64",
                     help="decode: token rows per call to time besides batch 1 (comma list; empty: skip)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense 4-bit comparator")
+    ap.add_argument("--no-control", action="store_true",
+                    help="decode: skip the dense-h control (so a profile holds the sparse calls only)")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time (0: skip)")
     ap.add_argument("--layers", type=int, default=NL)
     ap.add_argument("--tt", type=int, default=32)
