@@ -3,7 +3,8 @@
 // the shared expert, ReLU^2, written to hcat [B, topk*F + FS] (bf16), plus the canonical
 // live mask of every 64-row group (the decode kernels' compaction input).
 //
-// k_moe_up: one workgroup per (token, 16-row block of hcat): 4 wavefronts x 4 rows, so a
+// k_moe_up (instanced for D <= 3072 and D <= 4096, see UpShape): one workgroup per (token,
+// 16-row block of hcat): 4 wavefronts x 4 rows, so a
 // 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
 //   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
@@ -32,11 +33,19 @@ constexpr int kUpWaves = 4;
 constexpr int kUpThreads = 64 * kUpWaves;
 constexpr int kUpRows = 4;                      // rows per wavefront
 constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (an eighth of a mask group)
-constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS
-constexpr int kUpMaxP = kUpMaxD / 32;
-constexpr int kUpXIt = (kUpMaxD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
+constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS (the larger instance)
+constexpr int kUpSmallD = 3072;                 // the smaller instance (the reference shape's 2688)
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
               "a block is a quarter or an eighth of a mask group; one scale load per thread");
+// Two instances by the largest D: the register arrays (x words, the lane's weight pieces)
+// are sized for it, so D <= 3072 takes 72 VGPRs and runs 7 wavefronts per SIMD where the
+// 4096 instance takes 96 (5 per SIMD): at three token rows (11136 wavefronts) the MTP-2
+// step measured 2.196 against 2.221 ms; forcing 8 per SIMD spilled (2.433 ms).
+template <int MAXD> struct UpShape {
+  static constexpr int kMaxP = MAXD / 32;
+  static constexpr int kXIt = (MAXD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
+  static constexpr int kWaves = MAXD <= kUpSmallD ? 7 : 5;               // per SIMD
+};
 // 16-row workgroups (4 rows per wavefront): at three token rows 19.0 against 19.8 us per
 // call for 8-row ones (fewer rounds of workgroups), at one row the same. Small workgroups
 // measured faster than 64-row ones (1024 threads; 9.0 us per call with 8
@@ -130,19 +139,21 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
     g_out[r] = rt.norm_topk ? sc[r] / (ssum + 1e-20f) * rt.scale : sc[r] * rt.scale;
 }
 
-template <bool ROUTE>
-__global__ __launch_bounds__(kUpThreads) void k_moe_up(
+template <bool ROUTE, int MAXD>
+__global__ __launch_bounds__(kUpThreads)
+__attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves))) void k_moe_up(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ sel, const uint32_t* __restrict__ w1,
     const uint16_t* __restrict__ s1, const uint16_t* __restrict__ b1, const uint32_t* __restrict__ sw1,
     const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
     uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
     int E, Router rt) {
   // x pairs: piece j, word m, pair n at xp[4 (m NP + j) + n] = (x[32 j + 8 m + n], x[.. + 4])
-  __shared__ __attribute__((aligned(16))) uint32_t xp[kUpMaxD / 2];
+  constexpr int kUpMaxP = UpShape<MAXD>::kMaxP, kUpXIt = UpShape<MAXD>::kXIt;
+  __shared__ __attribute__((aligned(16))) uint32_t xp[MAXD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
   __shared__ int nib[kUpWaves];
-  __shared__ __attribute__((aligned(16))) uint16_t sl[kUpBlk * (kUpMaxD / 64)];  // [row][group]
-  __shared__ __attribute__((aligned(16))) uint16_t bl[kUpBlk * (kUpMaxD / 64)];
+  __shared__ __attribute__((aligned(16))) uint16_t sl[kUpBlk * (MAXD / 64)];  // [row][group]
+  __shared__ __attribute__((aligned(16))) uint16_t bl[kUpBlk * (MAXD / 64)];
   const int b = blockIdx.y, blk = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
@@ -360,10 +371,16 @@ extern "C" int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, 
     return set_error(HSD_ERR_ALIGN, "%s: x, the weights, scales and biases must be 16-byte aligned", fn);
   if (B == 0) return HSD_OK;
   const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
-  hipLaunchKernelGGL(k_moe_up<false>, grid, dim3(kUpThreads), 0, as_stream(stream),
-                     reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,
-                     reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F,
-                     (int)FS, (int)topk, (int)E, Router{});
+#define HSD_UP(MD)                                                                              \
+  hipLaunchKernelGGL((k_moe_up<false, MD>), grid, dim3(kUpThreads), 0, as_stream(stream),      \
+                     reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,    \
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F, \
+                     (int)FS, (int)topk, (int)E, Router{})
+  if (D <= kUpSmallD)
+    HSD_UP(kUpSmallD);
+  else
+    HSD_UP(kUpMaxD);
+#undef HSD_UP
   return check_launch(fn);
 }
 
@@ -390,10 +407,16 @@ extern "C" int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t
   if (B == 0) return HSD_OK;
   const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
   Router rt{logits, e_bias, sel, gains, routed_scale, norm_topk};
-  hipLaunchKernelGGL(k_moe_up<true>, grid, dim3(kUpThreads), 0, as_stream(stream),
-                     reinterpret_cast<const uint16_t*>(x), nullptr, w1, s1, b1, sw1, ss1, sb1,
-                     reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, (int)D, (int)F, (int)FS, (int)topk,
-                     (int)E, rt);
+#define HSD_UP(MD)                                                                                   \
+  hipLaunchKernelGGL((k_moe_up<true, MD>), grid, dim3(kUpThreads), 0, as_stream(stream),            \
+                     reinterpret_cast<const uint16_t*>(x), nullptr, w1, s1, b1, sw1, ss1, sb1,     \
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, (int)D, (int)F, (int)FS, \
+                     (int)topk, (int)E, rt)
+  if (D <= kUpSmallD)
+    HSD_UP(kUpSmallD);
+  else
+    HSD_UP(kUpMaxD);
+#undef HSD_UP
   return check_launch(fn);
 }
 

@@ -113,6 +113,21 @@ def test_small_shape(dev):
     check(h.view(torch.int16).cpu().numpy().view(np.uint16), ref, x, sel, lay, f, fs, k)
 
 
+def test_large_d_instance(dev):
+    """D=3584 takes the kernel instance sized for D <= 4096 (the reference shape's 2688
+    takes the one for D <= 3072): F=128, FS=192, 4 experts, top-2."""
+    d, f, fs, e, k = 3584, 128, 192, 4, 2
+    lay = S.moe_up_np(11, n_experts=e, d=d, f=f, fs=fs)
+    dv = {n: S.to_device(v, dev) for n, v in lay.items()}
+    rng = np.random.default_rng(12)
+    x = O.f32_to_bf16((rng.standard_normal((3, d)) * 0.5).astype(np.float32))
+    sel = np.stack([rng.permutation(e)[:k] for _ in range(3)]).astype(np.int32)
+    h = up_relu2(S.to_device(x, dev), S.to_device(sel, dev), dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"],
+                 dv["sb1"], topk=k)
+    ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=f, FS=fs, topk=k)
+    check(h.view(torch.int16).cpu().numpy().view(np.uint16), ref, x, sel, lay, f, fs, k)
+
+
 def test_front_end_feeds_the_down_projection(up, dev):
     """hcat from the front end goes straight into the sparse down projection; its live
     masks are the ones the down kernel derives from the same hcat."""
