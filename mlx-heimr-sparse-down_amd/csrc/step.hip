@@ -29,18 +29,34 @@ __global__ __launch_bounds__(256) void k_embed_q4(const int32_t* __restrict__ to
   const int t = tok[b];
   const bool ok = (unsigned)t < (unsigned)V;
   const size_t row = ok ? (size_t)t : 0;
-  for (int wi = threadIdx.x; wi < D / 8; wi += blockDim.x) {
-    const uint32_t q = w[row * (D / 8) + wi];
-    const float sc = bf16_bits_to_f32(s[row * (D / 64) + wi / 8]);
-    const float bi = bf16_bits_to_f32(bq[row * (D / 64) + wi / 8]);
-    uint32_t o[4];
+  // passes of 4 words per thread, each pass's loads issued before they are used
+  constexpr int kIt = 4;
+  const int NW = D / 8;
+  for (int p0 = 0; p0 < NW; p0 += 256 * kIt) {
+    uint32_t qv[kIt];
+    uint16_t sv[kIt], bv[kIt];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t lo = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c)) & 0xFu), bi)) : 0u;
-      const uint32_t hi = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c + 4)) & 0xFu), bi)) : 0u;
-      o[c] = lo | (hi << 16);
+    for (int it = 0; it < kIt; ++it) {
+      const int wi = min(p0 + (int)threadIdx.x + 256 * it, NW - 1);
+      qv[it] = w[row * (D / 8) + wi];
+      sv[it] = s[row * (D / 64) + wi / 8];
+      bv[it] = bq[row * (D / 64) + wi / 8];
     }
-    reinterpret_cast<uint4*>(out + (size_t)b * out_ld)[wi] = make_uint4(o[0], o[1], o[2], o[3]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int wi = p0 + (int)threadIdx.x + 256 * it;
+      const uint32_t q = qv[it];
+      const float sc = bf16_bits_to_f32(sv[it]), bi = bf16_bits_to_f32(bv[it]);
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c)) & 0xFu), bi)) : 0u;
+        const uint32_t hi = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c + 4)) & 0xFu), bi)) : 0u;
+        o[c] = lo | (hi << 16);
+      }
+      if (wi < NW) reinterpret_cast<uint4*>(out + (size_t)b * out_ld)[wi] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
   if (!ok && threadIdx.x == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_TOKEN);
 }
@@ -56,10 +72,20 @@ __global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ 
   const int b = blockIdx.x >> 1, half = blockIdx.x & 1;
   const uint16_t* x = half ? h + (size_t)b * h_ld : e + (size_t)b * e_ld;
   const uint16_t* w = half ? wh : we;
+  // a pass of 16 elements per thread: every load issued before the first is used (a loop
+  // with one load per step waits for each in turn); the sum keeps the element order
+  constexpr int kIt = 16;
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float v = bf16_bits_to_f32(x[i]);
-    ss = fmaf(v, v, ss);
+  for (int p0 = 0; p0 < D; p0 += 256 * kIt) {
+    uint16_t v[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) v[it] = x[min(p0 + (int)threadIdx.x + 256 * it, D - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const float f = p0 + (int)threadIdx.x + 256 * it < D ? bf16_bits_to_f32(v[it]) : 0.0f;
+      ss = p0 + (int)threadIdx.x + 256 * it < D ? fmaf(f, f, ss) : ss;
+    }
   }
   ss = wave_sum_dpp(ss);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
@@ -67,20 +93,56 @@ __global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ 
   const float tot = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
   const float inv = __builtin_amdgcn_rsqf(tot / (float)D + eps);
   uint16_t* o = out + (size_t)b * out_ld + half * D;
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float t = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(x[i]) * inv));
-    o[i] = f32_to_bf16_bits(t * bf16_bits_to_f32(w[i]));
+  for (int p0 = 0; p0 < D; p0 += 256 * kIt) {
+    uint16_t xv[kIt], wv[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int i = min(p0 + (int)threadIdx.x + 256 * it, D - 1);
+      xv[it] = x[i];
+      wv[it] = w[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int i = p0 + (int)threadIdx.x + 256 * it;
+      const float t = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(xv[it]) * inv));
+      if (i < D) o[i] = f32_to_bf16_bits(t * bf16_bits_to_f32(wv[it]));
+    }
+  }
+}
+
+// dst[i] = src[i] for i < n by one 256-thread workgroup, each pass's loads issued before
+// its stores
+__device__ __forceinline__ void copy_row_u16(uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, int n) {
+  constexpr int kIt = 16;
+  for (int p0 = 0; p0 < n; p0 += 256 * kIt) {
+    uint16_t v[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) v[it] = src[min(p0 + (int)threadIdx.x + 256 * it, n - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it)
+      if (p0 + (int)threadIdx.x + 256 * it < n) dst[p0 + threadIdx.x + 256 * it] = v[it];
   }
 }
 
 // ---------------------------------------------------------------- argmax of keys
 // The best key of row b over `slots` per-workgroup keys (hsd_linear's HSD_Y_ARGMAX), by
 // one wavefront: the index (low 32 bits inverted) of the largest key.
+// Up to 2048 keys (hsd_linear's most) are loaded in one pass, every load issued before the
+// first is used: a loop with one load per step waited for each in turn (32 dependent round
+// trips at 2048 slots). Indices past `slots` re-read the last key, which leaves the maximum
+// unchanged.
 __device__ int wave_argmax_keys(const uint64_t* keys, int slots, int lane) {
+  constexpr int kPer = 32;
   uint64_t k = 0;
-  for (int i = lane; i < slots; i += 64) {
-    const uint64_t v = keys[i];
-    k = v > k ? v : k;
+  for (int base = 0; base < slots; base += 64 * kPer) {
+    uint64_t v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = keys[min(base + lane + 64 * i, slots - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) k = v[i] > k ? v[i] : k;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -165,7 +227,7 @@ __global__ __launch_bounds__(256) void k_mtp_chain(const uint64_t* __restrict__ 
       seq[HSD_SEQ_HEAD_POS2] = seq[HSD_SEQ_HEAD_POS] + r + 1;
     }
   }
-  for (int i = threadIdx.x; i < D; i += 256) h2[i] = hn[(size_t)r * hn_ld + i];
+  copy_row_u16(h2, hn + (size_t)r * hn_ld, D);
 }
 
 // dst = src row R-1 (R = the pending-row count, clamped to [1, 3]).
@@ -173,7 +235,7 @@ __global__ __launch_bounds__(256) void k_select_row(const uint16_t* __restrict__
                                                     const int32_t* __restrict__ seq, uint16_t* __restrict__ dst,
                                                     int D) {
   const int r = min(max(seq[HSD_SEQ_R], 1), 3) - 1;
-  for (int i = threadIdx.x; i < D; i += 256) dst[i] = src[(size_t)r * src_ld + i];
+  copy_row_u16(dst, src + (size_t)r * src_ld, D);
 }
 
 // The verify ids [tok, d_0 .. d_{k-1}]: d_0 = the chained call's input prediction, d_1
