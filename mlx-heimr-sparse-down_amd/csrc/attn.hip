@@ -227,6 +227,7 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
 }
 
 constexpr int kMaxCh = 256;      // chunks per row the combine stages in LDS (smax <= 16384)
+constexpr int kPre = 64;         // chunks whose values the combine loads up front (4096 keys)
 
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   __shared__ float mw[kMaxCh];    // the chunks' maxima, then their weights e^(m - M)
@@ -242,11 +243,16 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   }
   const int nc = (P + r) / kCH + 1;
   const float* src = a.part + ((size_t)r * a.HQ + h) * a.nch * kRec;
-  // this dimension's values of the first 8 chunks, issued with the (m, l) loads (they do
-  // not depend on the maximum)
-  float v0[8];
+  // this dimension's values of the first kPre chunks, all issued with the (m, l) loads
+  // (they do not depend on the maximum), in blocks of 8 so that a short row issues few
+  float v0[kPre];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) v0[u] = src[(size_t)min(u, nc - 1) * kRec + 4 + d];
+  for (int b = 0; b < kPre; b += 8) {
+    if (b < nc) {
+#pragma unroll
+      for (int u = b; u < b + 8; ++u) v0[u] = src[(size_t)min(u, nc - 1) * kRec + 4 + d];
+    }
+  }
   // (m, l) of every chunk in one round trip, into LDS
   for (int c = d; c < nc; c += kHD) {
     mw[c] = src[(size_t)c * kRec];
@@ -264,23 +270,28 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   const float M = red[0];
   for (int c = d; c < nc; c += kHD) mw[c] = __expf(mw[c] - M);
   __syncthreads();
-  // L and this dimension's sum over the chunks in chunk order; the loads are issued in
-  // batches of 8 so that their latencies overlap
+  // L and this dimension's sum over the chunks in chunk order; chunks past kPre (contexts
+  // above kPre * kCH keys) load in passes of 16 whose loads are all issued before the sums
   float L = 0.0f, acc = 0.0f;
-  int c = 0;
-  for (; c + 8 <= nc; c += 8) {
-    float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = c == 0 ? v0[u] : src[(size_t)(c + u) * kRec + 4 + d];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      L = fmaf(lw[c + u], mw[c + u], L);
-      acc = fmaf(v[u], mw[c + u], acc);
+  for (int u = 0; u < kPre; ++u) {
+    if (u < nc) {
+      L = fmaf(lw[u], mw[u], L);
+      acc = fmaf(v0[u], mw[u], acc);
     }
   }
-  for (; c < nc; ++c) {
-    L = fmaf(lw[c], mw[c], L);
-    acc = fmaf(c < 8 ? v0[c] : src[(size_t)c * kRec + 4 + d], mw[c], acc);
+  for (int c = kPre; c < nc; c += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = src[(size_t)min(c + u, nc - 1) * kRec + 4 + d];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (c + u < nc) {
+        L = fmaf(lw[c + u], mw[c + u], L);
+        acc = fmaf(v[u], mw[c + u], acc);
+      }
+    }
   }
   o[d] = f32_to_bf16_bits(acc / L);
 }

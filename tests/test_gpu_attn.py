@@ -21,11 +21,11 @@ QKV = (HQ + 2 * HKV) * HD
 SCALE = 1.0 / math.sqrt(HD)
 
 
-def setup(dev, seed, P, B):
+def setup(dev, seed, P, B, smax=SMAX):
     rng = np.random.default_rng(seed)
-    cache = nn.KVCache(HKV, SMAX, dev)
-    kc = O.f32_to_bf16(rng.standard_normal((HKV, SMAX, HD)).astype(np.float32))
-    vc = O.f32_to_bf16(rng.standard_normal((HKV, SMAX, HD)).astype(np.float32))
+    cache = nn.KVCache(HKV, smax, dev)
+    kc = O.f32_to_bf16(rng.standard_normal((HKV, smax, HD)).astype(np.float32))
+    vc = O.f32_to_bf16(rng.standard_normal((HKV, smax, HD)).astype(np.float32))
     cache.k.copy_(S.to_device(kc, dev))
     cache.v.copy_(S.to_device(vc, dev))
     qkv = O.f32_to_bf16(rng.standard_normal((B, QKV)).astype(np.float32) * 2)
@@ -46,9 +46,13 @@ def oracle_rows(kc, vc, qkv, P):
     return out, k, v
 
 
-@pytest.mark.parametrize("P,B", [(0, 1), (0, 3), (5, 1), (63, 3), (64, 2), (2047, 3), (2300, 4)])
-def test_attention_matches_oracle(dev, P, B):
-    cache, kc, vc, qkv, pos = setup(dev, 100 + P + B, P, B)
+@pytest.mark.parametrize("P,B,smax", [(0, 1, SMAX), (0, 3, SMAX), (5, 1, SMAX), (63, 3, SMAX), (64, 2, SMAX),
+                                      (2047, 3, SMAX), (2300, 4, SMAX), (4094, 3, 8192),
+                                      (5000, 3, 8192), (8190, 2, 8192)])
+def test_attention_matches_oracle(dev, P, B, smax):
+    """Contexts past 4096 keys (more than 64 chunks of 64) take the combine's second
+    load phase; P = 4094, B = 3 puts the third row's last key in chunk 64."""
+    cache, kc, vc, qkv, pos = setup(dev, 100 + P + B, P, B, smax)
     out = nn.attention(S.to_device(qkv, dev), cache, pos, n_heads=HQ, n_kv_heads=HKV)
     ref, k, v = oracle_rows(kc, vc, qkv, P)
     got = out.float().cpu().numpy()
@@ -61,12 +65,12 @@ def test_attention_matches_oracle(dev, P, B):
     assert np.array_equal(kh[:, P + B:], O.bf16_to_f32(kc)[:, P + B:])
 
 
-@pytest.mark.parametrize("P", [0, 62, 700])
-def test_verify_rows_equal_single_rows(dev, P):
-    cache, kc, vc, qkv, pos = setup(dev, 200 + P, P, 3)
+@pytest.mark.parametrize("P,smax", [(0, SMAX), (62, SMAX), (700, SMAX), (4094, 8192), (6143, 8192)])
+def test_verify_rows_equal_single_rows(dev, P, smax):
+    cache, kc, vc, qkv, pos = setup(dev, 200 + P, P, 3, smax)
     qd = S.to_device(qkv, dev)
     out3 = nn.attention(qd, cache, pos, n_heads=HQ, n_kv_heads=HKV)
-    cache1, _, _, _, pos1 = setup(dev, 200 + P, P, 3)
+    cache1, _, _, _, pos1 = setup(dev, 200 + P, P, 3, smax)
     for r in range(3):
         o1 = nn.attention(qd[r:r + 1], cache1, pos1, n_heads=HQ, n_kv_heads=HKV)
         assert torch.equal(o1.view(torch.int16), out3[r:r + 1].view(torch.int16)), f"row {r}"
