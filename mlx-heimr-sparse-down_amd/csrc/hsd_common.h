@@ -94,6 +94,46 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// The maximum of a 64-bit key over each 16-lane row, in every lane of the row: DPP
+// quad_perm xor 1, xor 2, row_half_mirror, row_mirror (no LDS). Needs the row's lanes
+// active.
+__device__ __forceinline__ uint64_t row16_max_u64(uint64_t k) {
+  k = max_u64(k, dpp_u64<0xB1>(k));
+  k = max_u64(k, dpp_u64<0x4E>(k));
+  k = max_u64(k, dpp_u64<0x141>(k));
+  k = max_u64(k, dpp_u64<0x140>(k));
+  return k;
+}
+
+// The maximum of a 64-bit key over the 64 lanes, in every lane: the row maxima, then
+// v_permlane16_swap and v_permlane32_swap (each lane then holds its value and that of lane
+// l ^ 16, then l ^ 32, in some order). No LDS; needs every lane active.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  k = row16_max_u64(k);
+  {
+    const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    k = max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
+  }
+  {
+    const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    k = max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
+  }
+  return k;
+}
+
 // silu(x) = x / (1 + e^-x), with the hardware exponential and reciprocal (a few ulp;
 // the IEEE division and the libm exponential are long dependent sequences).
 __device__ __forceinline__ float silu_f32(float x) {

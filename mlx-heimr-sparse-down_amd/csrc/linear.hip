@@ -689,12 +689,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
         const uint16_t lb = f32_to_bf16_bits(v);
         uint64_t key = live ? argmax_key(lb, o) : 0;
         if (a.y && live) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + o] = lb;
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) {       // the best of the 16 lanes of token row m
-          const uint64_t ok = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), off, 64) << 32) |
-                              (uint32_t)__shfl_xor((int)(uint32_t)key, off, 64);
-          key = ok > key ? ok : key;
-        }
+        key = row16_max_u64(key);                      // the best of the 16 lanes of token row m
         best = key > best ? key : best;
       } else if (live) {
         const int64_t yi = m * a.y_ld + o;
@@ -750,12 +745,7 @@ __global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict
     const uint64_t v = keys[b * key_ld + i];
     k = v > k ? v : k;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
-                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
-    k = o > k ? o : k;
-  }
+  k = wave_max_u64(k);
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = k;
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -85,16 +85,6 @@ __device__ __forceinline__ uint32_t ordered_bits(float c) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
-                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
-    k = o > k ? o : k;
-  }
-  return k;
-}
-
 // Token row b's experts e[0..topk) and gains g[0..topk) (every lane gets them); every lane
 // of one wavefront calls it.
 __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, int topk, int lane,
@@ -123,12 +113,12 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
 #pragma unroll
       for (int i = 1; i < 4; ++i) m = key[i] > m ? key[i] : m;
       m = wave_max_u64(m);
-      const int e = (int)~(uint32_t)m;
+      const int e = __builtin_amdgcn_readfirstlane((int)~(uint32_t)m);  // the same in every lane
 #pragma unroll
       for (int i = 0; i < 4; ++i) key[i] = key[i] == m ? 0 : key[i];
       const int ii = e >> 6;
       const float own = ii == 0 ? sg[0] : ii == 1 ? sg[1] : ii == 2 ? sg[2] : sg[3];
-      const float s = __shfl(own, e & 63, 64);
+      const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), e & 63));
       e_out[r] = e;
       sc[r] = s;
       ssum += s;

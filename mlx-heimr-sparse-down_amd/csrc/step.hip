@@ -144,13 +144,7 @@ __device__ int wave_argmax_keys(const uint64_t* keys, int slots, int lane) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) k = v[i] > k ? v[i] : k;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), off, 64) << 32) |
-                       (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
-    k = o > k ? o : k;
-  }
-  return (int)~(uint32_t)k;
+  return (int)~(uint32_t)wave_max_u64(k);
 }
 
 // A plain decode step's end: tok = argmax; out_tokens[n] = tok (if n < cap); n += 1;
