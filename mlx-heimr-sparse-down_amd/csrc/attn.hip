@@ -262,8 +262,7 @@ __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   if (d < 64) {
     float M = -INFINITY;
     for (int c = d; c < nc; c += 64) M = fmaxf(M, mw[c]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    M = wave_max_f32(M);
     if (d == 0) red[0] = M;
   }
   __syncthreads();

@@ -134,6 +134,21 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
   return k;
 }
 
+// The maximum of a float over the 64 lanes, in every lane (fmaxf: a NaN loses to a
+// number), by the same moves as wave_max_u64. Needs every lane active.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const uint32_t b = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  const uint32_t c = __float_as_uint(v);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+}
+
 // silu(x) = x / (1 + e^-x), with the hardware exponential and reciprocal (a few ulp;
 // the IEEE division and the libm exponential are long dependent sequences).
 __device__ __forceinline__ float silu_f32(float x) {
