@@ -8,8 +8,7 @@
 // 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
 //   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
 //      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
-//      share of its 4 rows' 16-byte pieces (4 D/32 pieces dealt over the 64 lanes in
-//      turn, so every lane has the same count but the last round);
+//      4 rows' 16-byte pieces (16 lanes per row, D/32 pieces per row dealt over them);
 //   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
 //      and the sum of x over every 32-input piece;
 //   3. per piece: a shift, a mask and an OR with bf16 1.0 put each nibble in the top four
@@ -18,8 +17,9 @@
 //      u += 16 s * acc + (b - 16 s) * sum(x): the affine dequantisation W = s q + b folded
 //      per piece. (An offset of 1 against q/16 <= 15/16 keeps the cancellation in
 //      acc - sum(x) small: 128 + q, exact as well, lost about four more bits.)
-//   4. the 64 lanes' partials of each row: DPP sums inside 16-lane rows, then the four
-//      rows' totals in a fixed order; h = square(relu(bf16(u))) rounded to bf16.
+//   4. the 16 lanes' partials of each row: a DPP sum inside the 16-lane row (a lane's
+//      row never changes, so it keeps one partial and the x words it reads are those of
+//      the other three rows' lanes); h = square(relu(bf16(u))) rounded to bf16.
 // Bytes per token: every row of the 7 selected matrices (D/2 + 4 D/64 bytes per row),
 // 22.45 MB at the reference shape: an HBM-bound batched GEMV.
 #include "hsd_common.h"
@@ -201,18 +201,15 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   const int nsc = kUpBlk * NGD / 8;
   const int sc_i = tid < nsc ? tid : min(tid - nsc, nsc - 1);
   const uint4 scv = reinterpret_cast<const uint4*>((tid < nsc ? sb : bb) + row0 * NGD)[sc_i];
-  // pieces: index p = lane + 64 it over the wave's 4 rows x NP pieces
-  constexpr int kIt = (kUpRows * kUpMaxP + 63) / 64;
-  const int npw = kUpRows * NP, nit = (npw + 63) / 64;
+  // pieces: lanes 16 i .. 16 i + 15 take row i of the wave's 4, lane l its pieces
+  // j = l % 16 + 16 it (it < NP / 16 rounded up)
+  constexpr int kIt = (kUpMaxP + 15) / 16;
+  const int rw = lane >> 4, jl = lane & 15, nit = (NP + 15) / 16;
   uint4 q[kIt];
-  int prow[kIt], pj[kIt];
+  {
+    const uint4* wr = reinterpret_cast<const uint4*>(wb + (row0 + kUpRows * wave + rw) * NW);
 #pragma unroll
-  for (int it = 0; it < kIt; ++it) {
-    const int p = min(lane + 64 * it, npw - 1);
-    prow[it] = p / NP;
-    pj[it] = p - prow[it] * NP;
-    const uint4* wr = reinterpret_cast<const uint4*>(wb + (row0 + kUpRows * wave + prow[it]) * NW);
-    q[it] = wr[pj[it]];  // rounds past nit re-read the last piece, unused
+    for (int it = 0; it < kIt; ++it) q[it] = wr[min(jl + 16 * it, NP - 1)];  // past NP: re-read, unused
   }
 
   // ---- x pairs and piece sums into LDS: word t = tid + 256 i holds inputs 8t .. 8t+7
@@ -241,20 +238,21 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   if (tid < 2 * nsc) *reinterpret_cast<uint4*>((tid < nsc ? sl : bl) + 8 * sc_i) = scv;
   lds_barrier();
 
-  // ---- the lane's pieces into its 4 row partials, then per row the 64-lane sum
-  float pr[kUpRows];
-#pragma unroll
-  for (int i = 0; i < kUpRows; ++i) pr[i] = 0.0f;
+  // ---- the lane's pieces into its row partial, then the row's 16-lane sum
+  float pr = 0.0f;
+  const int rl = kUpRows * wave + rw;                 // row within the block
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
     if (it < nit) {  // uniform
-      const int j = pj[it], rl = kUpRows * wave + prow[it];  // piece, row within the block
-      const bool use = lane + 64 * it < npw;
+      const int j = jl + 16 * it;
+      const bool use = j < NP;
+      const int jc = use ? j : NP - 1;
       const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
       float acc = 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[4 * (m * NP + j)]);
+        // the four rows' lanes read the same words (one LDS access serves all four)
+        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[4 * (m * NP + jc)]);
         const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
         // nibble n (bits 4n..4n+3 of each half) to bits 3..6: a left shift by 3 for n = 0,
         // right shifts by 1, 5, 9 for the others
@@ -264,38 +262,25 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
         acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
         acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
       }
-      const float sc = bf16_bits_to_f32(sl[rl * NGD + j / 2]), bi = bf16_bits_to_f32(bl[rl * NGD + j / 2]);
-      const float t = use ? fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[j]) : 0.0f;
-#pragma unroll
-      for (int i = 0; i < kUpRows; ++i) pr[i] += prow[it] == i ? t : 0.0f;
+      const float sc = bf16_bits_to_f32(sl[rl * NGD + jc / 2]), bi = bf16_bits_to_f32(bl[rl * NGD + jc / 2]);
+      pr += use ? fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[jc]) : 0.0f;
     }
   }
-  float u[kUpRows];
-#pragma unroll
-  for (int i = 0; i < kUpRows; ++i) {
-    float part = pr[i];
-    // 16-lane sums (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then the four
-    // 16-lane totals in lane order
-    part += dpp_f32<0xB1>(part);
-    part += dpp_f32<0x4E>(part);
-    part += dpp_f32<0x141>(part);
-    part += dpp_f32<0x140>(part);
-    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
-    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16));
-    const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32));
-    const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48));
-    u[i] = ok ? ((t0 + t1) + t2) + t3 : 0.0f;
-  }
+  // 16-lane sum (quad_perm xor 1, xor 2, row_half_mirror, row_mirror): every lane of a row
+  // ends with the row's total
+  pr += dpp_f32<0xB1>(pr);
+  pr += dpp_f32<0x4E>(pr);
+  pr += dpp_f32<0x141>(pr);
+  pr += dpp_f32<0x140>(pr);
+  const float ui = ok ? pr : 0.0f;
 
-  // ---- h = square(relu(bf16(u))) in bf16; lanes 0..3 write the wave's 4 rows
-  float ui = u[0];
-#pragma unroll
-  for (int i = 1; i < kUpRows; ++i) ui = lane == i ? u[i] : ui;
+  // ---- h = square(relu(bf16(u))) in bf16; lane 16 i writes row i of the wave
   const float ub = bf16_bits_to_f32(f32_to_bf16_bits(ui));
   const float r = ub != ub ? ub : fmaxf(ub, 0.0f);
   const uint16_t hb = f32_to_bf16_bits(r * r);
-  if (lane < kUpRows) hcat[(size_t)b * NR + r0 + kUpRows * wave + lane] = hb;
-  const uint32_t lb = (uint32_t)(__ballot(lane < kUpRows && (hb & 0x7FFFu) != 0) & ((1u << kUpRows) - 1u));
+  if (jl == 0) hcat[(size_t)b * NR + r0 + kUpRows * wave + rw] = hb;
+  const uint64_t lv = __ballot(jl == 0 && (hb & 0x7FFFu) != 0);  // bits 0, 16, 32, 48
+  const uint32_t lb = (uint32_t)((lv & 1u) | ((lv >> 15) & 2u) | ((lv >> 30) & 4u) | ((lv >> 45) & 8u));
   if (lane == 0) nib[wave] = (int)lb;
   if (live_out) {
     lds_barrier();
