@@ -15,13 +15,16 @@
 // Work split: a workgroup (4 wavefronts) owns 16 consecutive output rows (4-bit: 4 per
 // wavefront) or 4 (bf16: 1 per wavefront) and loops over row blocks strided by the grid
 // (as many workgroups as are resident at once, so the prologue is paid once per
-// workgroup). Lane l owns the 16-byte pieces l, l + 64, ... of every row of its wavefront:
-// an x piece read from LDS serves all the wavefront's rows (at three token rows, reading x
-// once per row and piece made LDS the bound of lm_head). The next block's pieces are loaded
-// while the current one is computed. 4-bit pieces are turned into bf16 pairs (1 + q/16)
-// with a shift, a mask and an OR, and v_dot2_f32_bf16 accumulates x (1 + q/16); per
-// 32-input piece u += 16 s acc + (b - 16 s) sum(x) (the affine dequantisation folded per
-// piece). A row's 64 lane partials are summed with DPP in a fixed order.
+// workgroup; every 4-bit projection of the model is one block per workgroup).
+// 4-bit: the lanes of half-wavefront h own rows 2h and 2h + 1, lane l the 16-byte pieces
+// l % 32, l % 32 + 32, ... of both: an x piece read from LDS serves two rows, and a lane
+// adds into one partial per (row, token row) with no selects (VALU-bound at three token
+// rows: 253 -> 150 VGPRs and 3 workgroups per CU for in_proj). The pieces become bf16 pairs
+// (1 + q/16) with a shift, a mask and an OR, and v_dot2_f32_bf16 accumulates x (1 + q/16);
+// per 32-input piece u += 16 s acc + (b - 16 s) sum(x) (the affine dequantisation folded per
+// piece). A row's 32 lane partials are summed with DPP and v_permlane16_swap in a fixed
+// order. bf16: lane l owns the pieces l, l + 64, ... of the wavefront's row; the next
+// block's pieces are loaded while the current one is computed.
 // 4-bit projections of more 16-row blocks than one grid (lm_head) run on the matrix cores
 // instead (k_linear_q4 below): at several token rows the per-row dot products above bound
 // them.
@@ -34,6 +37,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 namespace hsd {
 namespace {
@@ -262,9 +266,13 @@ struct XIn {
 // blocks per workgroup, the next block in flight: lm_head took 49 against 59 us here before
 // it moved to the matrix cores) are faster with the registers of two.
 template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM>
-__global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void k_linear(LinArgs a) {
+__global__ __launch_bounds__(kLT, WF == HSD_W_Q4 ? (IMAX == 3072 && NB < 4 ? 3 : 2) : (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2)
+void k_linear(LinArgs a) {
   using T = WTraits<WF>;
+  constexpr bool Q4 = WF == HSD_W_Q4;
+  static_assert(!Q4 || RW == 4, "4-bit weights: 4 rows per wavefront, two per half-wavefront");
   constexpr int kRW = RW;
+  constexpr int kIt32 = (IMAX / 32 + 31) / 32;          // 4-bit: pieces per lane and row (max)
   constexpr int kFull = (IMAX / T::kIn) / 64 > 0 ? (IMAX / T::kIn) / 64 : 1;  // full passes (max)
   constexpr int kRP = REM ? (kRW * 63 + 63) / 64 : 1;  // remainder passes (max; none without REM)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
@@ -281,11 +289,14 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nblk = (O + kRows - 1) / kRows;            // the last block may be partial
   const int NPr = I / T::kIn;                          // pieces per row
-  // pieces 0 .. 64 nfull - 1 of every row: lane l owns pieces l + 64 it of each of the
+  // 4-bit: lanes 32 h .. 32 h + 31 take rows 2 h and 2 h + 1 of the wavefront's 4, lane l
+  // pieces l % 32 + 32 it of both (84 pieces a row at I = 2688: 3 each, the last taken by
+  // 20 lanes of a half): an x piece read from LDS serves two rows, and a lane's rows never
+  // change, so it keeps one partial per (row, token row).
+  const int hw = lane >> 5, jl = lane & 31, nit32 = (NPr + 31) / 32;
+  // bf16: pieces 0 .. 64 nfull - 1 of every row: lane l owns pieces l + 64 it of each of the
   // wavefront's kRW rows; the nrem pieces left of each row are dealt as (row, piece) pairs
-  // over the lanes, so no pass runs with most lanes idle (84 pieces a row at I = 2688: one
-  // full pass and two pair passes instead of two full passes with 20 lanes busy in the
-  // second)
+  // over the lanes, so no pass runs with most lanes idle
   const int nfull = NPr / 64, nrem = REM ? NPr - 64 * nfull : 0;
   const int npair = kRW * nrem, npass = (npair + 63) / 64;
   int prr[kRP], prj[kRP];                              // a pair's row and piece
@@ -298,12 +309,17 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
 
   // ---- weight pieces of a block (rows past O re-read row O-1, pieces past the row re-read
   // its last piece; unused)
-  struct Blk {
+  struct BlkQ4 {
+    uint4 q[kIt32][2];
+    uint32_t s[kIt32][2];
+  };
+  struct BlkBf {
     uint4 q[kRW][kFull];
     uint32_t s[kRW][kFull];
     uint4 qr[kRP];
     uint32_t sr[kRP];
   };
+  using Blk = typename std::conditional<Q4, BlkQ4, BlkBf>::type;
   auto load_piece = [&](int row, int j, uint4& qq, uint32_t& sq) {
     if constexpr (WF == HSD_W_Q4) {
       const uint32_t* wr = reinterpret_cast<const uint32_t*>(a.w) + (size_t)row * NW;
@@ -318,15 +334,23 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
   };
   auto load_block = [&](int blk, Blk& bk) {
     const int r0 = blk * kRows + kRW * wave;
+    if constexpr (Q4) {
 #pragma unroll
-    for (int r = 0; r < kRW; ++r) {
-      const int row = min(r0 + r, O - 1);
+      for (int it = 0; it < kIt32; ++it)
 #pragma unroll
-      for (int it = 0; it < kFull; ++it) load_piece(row, min(lane + 64 * it, NPr - 1), bk.q[r][it], bk.s[r][it]);
-    }
-    if constexpr (REM) {
+        for (int i = 0; i < 2; ++i)
+          load_piece(min(r0 + 2 * hw + i, O - 1), min(jl + 32 * it, NPr - 1), bk.q[it][i], bk.s[it][i]);
+    } else {
 #pragma unroll
-      for (int ps = 0; ps < kRP; ++ps) load_piece(min(r0 + prr[ps], O - 1), prj[ps], bk.qr[ps], bk.sr[ps]);
+      for (int r = 0; r < kRW; ++r) {
+        const int row = min(r0 + r, O - 1);
+#pragma unroll
+        for (int it = 0; it < kFull; ++it) load_piece(row, min(lane + 64 * it, NPr - 1), bk.q[r][it], bk.s[r][it]);
+      }
+      if constexpr (REM) {
+#pragma unroll
+        for (int ps = 0; ps < kRP; ++ps) load_piece(min(r0 + prr[ps], O - 1), prj[ps], bk.qr[ps], bk.sr[ps]);
+      }
     }
   };
 
@@ -341,44 +365,17 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
   xin.template finish<32>(a, xp, xh, wsum, tid, lane, wave);
   __syncthreads();
 
-  // one 16-byte piece j of a row against the token rows: the partial of each token row
-  auto piece_terms = [&](int j, const uint4& qv, uint32_t sq, float (&t)[NB]) {
-    if constexpr (WF == HSD_W_Q4) {
-      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-      uint32_t wc[4][4];
+  // bf16: one 16-byte piece j of a row against the token rows: the partial of each token row
+  auto piece_terms = [&](int j, const uint4& qv, float (&t)[NB]) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
-        wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
-        wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
-        wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
-      }
-      const float sv = lo_f(sq), bv = hi_f(sq);
-      const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
-          acc = dot2_bf16(xq.x, wc[m][0], acc);
-          acc = dot2_bf16(xq.y, wc[m][1], acc);
-          acc = dot2_bf16(xq.z, wc[m][2], acc);
-          acc = dot2_bf16(xq.w, wc[m][3], acc);
-        }
-        t[b] = fmaf(s16, acc, bo * xh[b * (I / 32) + j]);
-      }
-    } else {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
-        float acc = 0.0f;
-        acc = dot2_bf16(xq.x, qv.x, acc);
-        acc = dot2_bf16(xq.y, qv.y, acc);
-        acc = dot2_bf16(xq.z, qv.z, acc);
-        acc = dot2_bf16(xq.w, qv.w, acc);
-        t[b] = acc;
-      }
+    for (int b = 0; b < NB; ++b) {
+      const uint4 xq = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + 4 * j]);
+      float acc = 0.0f;
+      acc = dot2_bf16(xq.x, qv.x, acc);
+      acc = dot2_bf16(xq.y, qv.y, acc);
+      acc = dot2_bf16(xq.z, qv.z, acc);
+      acc = dot2_bf16(xq.w, qv.w, acc);
+      t[b] = acc;
     }
   };
 
@@ -387,28 +384,32 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
   auto do_block = [&](int blk_, const Blk& bk) {
-    float pr[NB][kRW];
+    float outv = 0.0f;
+    int ob, orr;
+    bool lane_out;
+    if constexpr (Q4) {
+      // the lane's pieces of its two rows against every token row, then the 32-lane sums
+      float pq[NB][2];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NB; ++b) pq[b][0] = pq[b][1] = 0.0f;
 #pragma unroll
-      for (int r = 0; r < kRW; ++r) pr[b][r] = 0.0f;
-    if constexpr (WF == HSD_W_Q4) {
-      // full passes: the x piece read once from LDS serves the wavefront's kRW rows
-#pragma unroll
-      for (int it = 0; it < kFull; ++it) {
-        if (it < nfull) {                                // uniform
-          const int j = lane + 64 * it;
+      for (int it = 0; it < kIt32; ++it) {
+        if (it < nit32) {                                // uniform
+          const int j = jl + 32 * it;
+          const bool use = j < NPr;
+          const int jc = use ? j : NPr - 1;
+          // the token rows' x words of piece jc (the two half-wavefronts read the same)
           uint4 xq[NB][4];
           float xs[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) xq[b][m] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + j) * 4]);
-            xs[b] = xh[b * (I / 32) + j];
+            for (int m = 0; m < 4; ++m) xq[b][m] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + jc) * 4]);
+            xs[b] = xh[b * (I / 32) + jc];
           }
 #pragma unroll
-          for (int r = 0; r < kRW; ++r) {
-            const uint32_t qw[4] = {bk.q[r][it].x, bk.q[r][it].y, bk.q[r][it].z, bk.q[r][it].w};
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t qw[4] = {bk.q[it][i].x, bk.q[it][i].y, bk.q[it][i].z, bk.q[it][i].w};
             uint32_t wc[4][4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
               wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
               wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
             }
-            const float sv = lo_f(bk.s[r][it]), bv = hi_f(bk.s[r][it]);
+            const float sv = lo_f(bk.s[it][i]), bv = hi_f(bk.s[it][i]);
             const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -429,12 +430,39 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
                 acc = dot2_bf16(xq[b][m].z, wc[m][2], acc);
                 acc = dot2_bf16(xq[b][m].w, wc[m][3], acc);
               }
-              pr[b][r] += fmaf(s16, acc, bo * xs[b]);
+              pq[b][i] += use ? fmaf(s16, acc, bo * xs[b]) : 0.0f;
             }
           }
         }
       }
+      // 32-lane sums: DPP inside each 16-lane row (quad_perm xor 1, xor 2, row_half_mirror,
+      // row_mirror), then v_permlane16_swap puts the even and the odd row's totals side by
+      // side and they are added in that order; lane 32 h + 2 b + i keeps (token row b, row
+      // 2 h + i)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          float v = pq[b][i];
+          v += dpp_f32<0xB1>(v);
+          v += dpp_f32<0x4E>(v);
+          v += dpp_f32<0x141>(v);
+          v += dpp_f32<0x140>(v);
+          const uint32_t vb = __float_as_uint(v);
+          const auto pv = __builtin_amdgcn_permlane16_swap(vb, vb, false, false);
+          const float u = __uint_as_float(pv[0]) + __uint_as_float(pv[1]);
+          outv = jl == 2 * b + i ? u : outv;
+        }
+      }
+      ob = jl >> 1;
+      orr = 2 * hw + (jl & 1);
+      lane_out = jl < 2 * NB;
     } else {
+      float pr[NB][kRW];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < kRW; ++r) pr[b][r] = 0.0f;
 #pragma unroll
       for (int it = 0; it < kFull; ++it) {
         if (it < nfull) {                                // uniform
@@ -456,42 +484,43 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
           }
         }
       }
-    }
-    // pair passes: lane l's pair p = l + 64 ps is piece prj of row prr of the wavefront
+      // pair passes: lane l's pair p = l + 64 ps is piece prj of row prr of the wavefront
 #pragma unroll
-    for (int ps = 0; ps < kRP; ++ps) {
-      if (REM && ps < npass) {                           // uniform
-        const bool use = lane + 64 * ps < npair;
-        float t[NB];
-        piece_terms(prj[ps], bk.qr[ps], bk.sr[ps], t);
+      for (int ps = 0; ps < kRP; ++ps) {
+        if (REM && ps < npass) {                         // uniform
+          const bool use = lane + 64 * ps < npair;
+          float t[NB];
+          piece_terms(prj[ps], bk.qr[ps], t);
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+          for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int r = 0; r < kRW; ++r) pr[b][r] += (use && prr[ps] == r) ? t[b] : 0.0f;
+            for (int r = 0; r < kRW; ++r) pr[b][r] += (use && prr[ps] == r) ? t[b] : 0.0f;
+        }
       }
-    }
-    // row sums: lane b*kRW + r ends with row r of token row b
-    float outv = 0.0f;
+      // row sums: lane b*kRW + r ends with row r of token row b
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+      for (int b = 0; b < NB; ++b) {
 #pragma unroll
-      for (int r = 0; r < kRW; ++r) {
-        float v = pr[b][r];
-        v += dpp_f32<0xB1>(v);
-        v += dpp_f32<0x4E>(v);
-        v += dpp_f32<0x141>(v);
-        v += dpp_f32<0x140>(v);
-        const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-        const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-        const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-        const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-        const float u = ((t0 + t1) + t2) + t3;
-        outv = lane == b * kRW + r ? u : outv;
+        for (int r = 0; r < kRW; ++r) {
+          float v = pr[b][r];
+          v += dpp_f32<0xB1>(v);
+          v += dpp_f32<0x4E>(v);
+          v += dpp_f32<0x141>(v);
+          v += dpp_f32<0x140>(v);
+          const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+          const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+          const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+          const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+          const float u = ((t0 + t1) + t2) + t3;
+          outv = lane == b * kRW + r ? u : outv;
+        }
       }
+      ob = lane / kRW;
+      orr = lane - ob * kRW;
+      lane_out = lane < NB * kRW;
     }
-    const int ob = lane / kRW, orr = lane - ob * kRW;
     const int o = blk_ * kRows + kRW * wave + orr;
-    const bool live = lane < NB * kRW && o < O;
+    const bool live = lane_out && o < O;
     if constexpr (YK == HSD_Y_ARGMAX) {
       const uint16_t lb = f32_to_bf16_bits(outv);
       const uint64_t key = live ? argmax_key(lb, o) : 0;
@@ -501,8 +530,9 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
         uint64_t kb = 0;
 #pragma unroll
         for (int r = 0; r < kRW; ++r) {
-          const uint64_t kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), b * kRW + r) << 32) |
-                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, b * kRW + r);
+          const int ln = Q4 ? 32 * (r >> 1) + 2 * b + (r & 1) : b * kRW + r;  // (token row b, row r)
+          const uint64_t kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), ln) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, ln);
           kb = kr > kb ? kr : kb;
         }
         best[b] = kb > best[b] ? kb : best[b];
@@ -522,6 +552,17 @@ __global__ __launch_bounds__(kLT, (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2) void 
 
   if ((int)gridDim.x >= nblk) {
     do_block(blk, cur);                                // one block per workgroup
+  } else if constexpr (Q4) {
+    // several blocks, one after the other: a second block's registers in flight would
+    // cost the occupancy that makes every projection of the model one block per workgroup
+    // (in_proj: 644 blocks, 768 resident workgroups)
+    for (;;) {
+      do_block(blk, cur);
+      blk += (int)gridDim.x;
+      if (blk >= nblk) break;
+      __builtin_amdgcn_sched_barrier(0);
+      load_block(blk, cur);
+    }
   } else {
     // several blocks: the next block's pieces are in flight while one is computed; the
     // load is unconditional (the last block re-reads its own lines), so the compiler's
