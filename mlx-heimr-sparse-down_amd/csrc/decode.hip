@@ -13,7 +13,9 @@
 //       1. one round trip: the slot's expert id and gain, and the group's 64 activations
 //          (4 per lane); the group's 16-byte scale and bias vectors follow as soon as the
 //          id is in, overlapping the activations' latency; 4 wave ballots give the live
-//          mask and an ascending live-row list in LDS (+-0 dead, NaN live);
+//          mask and an ascending live-row list in LDS (+-0 dead, NaN live), each entry of
+//          a 16-bit activation carrying its bits beside the row index (64 VGPRs, 8
+//          wavefronts per SIMD: at three token rows the 2016 workgroups are one round);
 //       2. one round trip: the live rows' words (4 B per lane), up to 16 rows per team;
 //       3. acc[t] = sum h_i q_{i,t}, hsum = sum h_i (fp32); term = s*acc + b*hsum (the
 //          group factorisation of decode.py:125-128);
@@ -79,7 +81,8 @@ template <> __device__ __forceinline__ bool live_bits<HSD_DT_F16>(uint16_t v) { 
 template <> __device__ __forceinline__ bool live_bits<HSD_DT_F32>(float v) { return !(v == 0.0f); }
 
 template <int HDT>
-__global__ __launch_bounds__(kThreads) void k_sparse_down_part(
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 ? 7 : 8))) void k_sparse_down_part(
     const typename Elem<HDT>::T* __restrict__ h, const int32_t* __restrict__ sel,
     const float* __restrict__ gains, const uint32_t* __restrict__ pw,
     const uint16_t* __restrict__ ps, const uint16_t* __restrict__ pb,
@@ -91,8 +94,13 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   // the four teams of a wavefront (16 lanes each) write different LDS banks.
   constexpr int kHP = 64 + 64 / (int)sizeof(HT);
   constexpr int kRedP = 8 * kWPC + 16;
-  __shared__ HT hs[kGPW * kRS][kHP];                // per team: the group's activations
-  __shared__ uint8_t lst[kGPW * kRS][64];           // per team: the group's live rows, ascending
+  // 16-bit activations: each list entry carries the row's activation bits beside its index
+  // ((bits << 16) | row), so one LDS read per row gives both and a lane holds one register
+  // per row instead of two (64 VGPRs: 8 wavefronts per SIMD); fp32: index list + table
+  constexpr bool kPack = sizeof(HT) == 2;
+  __shared__ HT hs[kPack ? 1 : kGPW * kRS][kHP];    // per team: the group's activations
+  __shared__ uint8_t lst[kPack ? 1 : kGPW * kRS][64];  // per team: the group's live rows, ascending
+  __shared__ uint32_t lsp[kPack ? kGPW * kRS : 1][64];  // the same with the activation bits
   __shared__ float red[kGPW * kRS][kRedP];          // per team: group terms [t][word]
   __shared__ float sum2[kDC][kL1 + 1];
 
@@ -153,9 +161,14 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
     const uint32_t mnz = (uint32_t)(__ballot(nz) >> sh) & 0xFFFFu;
     const uint32_t muse = (uint32_t)(__ballot(use) >> sh) & 0xFFFFu;
     live |= (uint64_t)mnz << (16 * v);
-    if (use) lst[team][cnt + __popc(muse & ((1u << l) - 1u))] = (uint8_t)(16 * v + l);
+    const int pos = cnt + __popc(muse & ((1u << l) - 1u));
+    if constexpr (kPack) {
+      if (use) lsp[team][pos] = ((uint32_t)hv[v] << 16) | (uint32_t)(16 * v + l);
+    } else {
+      if (use) lst[team][pos] = (uint8_t)(16 * v + l);
+      hs[team][16 * v + l] = hv[v];
+    }
     cnt += __popc(muse);
-    hs[team][16 * v + l] = hv[v];
   }
   if (live_out && c == 0 && phase == 0 && l == 0 && jv)
     live_out[(size_t)b * g.ngt + (routed ? k * g.gpr : g.topk * g.gpr) + grp] = live;
@@ -177,25 +190,40 @@ __global__ __launch_bounds__(kThreads) void k_sparse_down_part(
   const int nmax = max(max(__builtin_amdgcn_readlane(nmine, 0), __builtin_amdgcn_readlane(nmine, 16)),
                        max(__builtin_amdgcn_readlane(nmine, 32), __builtin_amdgcn_readlane(nmine, 48)));
   for (int r0 = 0; r0 < nmax; r0 += kRB) {            // one batch unless > 16 live rows
-    int idx[kRB];
+    // ent[r]: the row index in the low bits (16-bit activations: the activation bits above)
+    uint32_t ent[kRB];
 #pragma unroll
-    for (int r = 0; r < kRB; ++r) idx[r] = r0 + r < nmine ? (int)lst[team][r0 + r] : -1;
+    for (int r = 0; r < kRB; ++r) {
+      if constexpr (kPack)
+        ent[r] = r0 + r < nmine ? lsp[team][r0 + r] : 0u;
+      else
+        ent[r] = r0 + r < nmine ? (uint32_t)lst[team][r0 + r] : 0u;
+    }
     uint32_t q[kRB];
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
       q[r] = 0u;
-      if (idx[r] >= 0)
+      if (r0 + r < nmine)
         q[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(wb) +
-                                                  (size_t)(row0 + (uint32_t)idx[r] * (uint32_t)g.NW) * 4u);
+                                                  (size_t)(row0 + (ent[r] & 63u) * (uint32_t)g.NW) * 4u);
     }
-    HT hr[kRB];
+    float hx[kPack ? 1 : kRB];
+    if constexpr (!kPack) {
 #pragma unroll
-    for (int r = 0; r < kRB; ++r) hr[r] = hs[team][idx[r] < 0 ? 0 : idx[r]];
+      for (int r = 0; r < kRB; ++r) hx[r] = Elem<HDT>::load(&hs[team][ent[r] & 63u], 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
       if (r0 + r < nmax) {                            // wave-uniform bound
-        const float x = idx[r] >= 0 ? Elem<HDT>::load(&hr[r], 0) : 0.0f;
+        float x;
+        if constexpr (kPack) {
+          const HT hb = (HT)(ent[r] >> 16);
+          x = Elem<HDT>::load(&hb, 0);
+        } else {
+          x = hx[r];
+        }
+        x = r0 + r < nmine ? x : 0.0f;
         hsum += x;
         const uint32_t lo = q[r] & 0x0F0F0F0Fu, hi = (q[r] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
