@@ -35,7 +35,7 @@ enum {
 enum { HSD_DT_BF16 = 0, HSD_DT_F16 = 1, HSD_DT_F32 = 2 };
 
 /* hsd_linear: what x holds, the weight format, and what is written. */
-enum { HSD_X_BF16 = 0, HSD_X_RMS = 1, HSD_X_GATED = 2 };
+enum { HSD_X_BF16 = 0, HSD_X_RMS = 1, HSD_X_GATED = 2, HSD_X_GATED_Z = 3 };
 enum { HSD_W_Q4 = 0, HSD_W_BF16 = 1 };
 enum { HSD_Y_BF16 = 0, HSD_Y_F32 = 1, HSD_Y_RESID = 2, HSD_Y_ARGMAX = 3 };
 
@@ -197,7 +197,10 @@ int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* sel, const 
  *                      (mx.fast.rms_norm, the block pre-norm, model.py:114, mamba.py:25);
  *          HSD_X_GATED: x = y [B, I] f32, z = x * silu(gate) (gate bf16, stride gate_ld),
  *                      per group of 512: xn = bf16(bf16(z * rsqrt(mean(z^2) + eps)) * norm_w)
- *                      (the Mamba-2 gated RMSNorm, mamba.py:43).
+ *                      (the Mamba-2 gated RMSNorm, mamba.py:43);
+ *          HSD_X_GATED_Z: the same norm from hsd_mamba_ssm_gated's rows: x [B, I + I/16] f32
+ *                      holds z, then the sums of z^2 over every 16 channels (x_ld >= I + I/16);
+ *                      a group's sum is its 32 partials added in order (gate unused).
  *   y_kind HSD_Y_BF16 / HSD_Y_F32: y [B, O] (stride y_ld);
  *          HSD_Y_RESID: y = bf16(res + bf16(x W^T)) (res bf16, stride res_ld; y may be res:
  *                      the residual add `x + mixer(x)` of every block);
@@ -206,7 +209,8 @@ int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* sel, const 
  *                      for hsd_argmax_keys; y, when non-null, receives the bf16 outputs.
  *   xn_out (nullable): receives xn (bf16 [B, I], stride xn_ld).
  * Instantiated pairs (x_kind, y_kind): 4-bit -- (RMS, BF16), (RMS, F32), (RMS, ARGMAX),
- * (GATED, RESID), (BF16, RESID), (BF16, BF16); bf16 weights -- (RMS, BF16), (BF16, BF16).
+ * (GATED, RESID), (GATED_Z, RESID), (BF16, RESID), (BF16, BF16); bf16 weights -- (RMS,
+ * BF16), (BF16, BF16).
  * Requirements: O a multiple of 8 (4-bit) or 4 (bf16); I <= 6144, a multiple of 64 (4-bit)
  * or 8 (bf16), of 512 for the gated norm; x, gate, norm_w, w, xn_out 16-byte aligned with
  * row strides of whole 16-byte pieces. A token row's arithmetic does not depend on B. */
@@ -382,13 +386,27 @@ int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t
                      int32_t* dev_status, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The conv + SSM half of hsd_mamba_verify without the gated norm: y [L, H*P] f32 =
- * sum_n S C + D x per row, the per-row checkpoints written to the ring as above. The
- * model's Mamba block feeds y to out_proj through hsd_linear's HSD_X_GATED prologue. */
+ * sum_n S C + D x per row, the per-row checkpoints written to the ring as above, for
+ * hsd_linear's HSD_X_GATED prologue. (The model's Mamba block takes hsd_mamba_ssm_gated
+ * and HSD_X_GATED_Z.) */
 int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
                   const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log,
                   const float* dt_bias, const float* Dp, float* ssm_slabs, uint16_t* conv_slabs,
                   const int32_t* cur, int64_t nslab, float* y, int64_t L, int64_t H, int64_t P,
                   int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream);
+
+/* hsd_mamba_ssm with the gate of the gated norm applied (the first half of mamba.py:43):
+ * z [L, z_ld] f32 with z_ld >= H*P + H*P/16: columns 0 .. H*P-1 hold z = y * silu(gate)
+ * (gate [L, H*P] bf16, stride gate_ld), column H*P + k the sum of z^2 over channels
+ * 16k .. 16k+15 (in channel order), for hsd_linear's HSD_X_GATED_Z prologue (the model's
+ * out_proj then does no silu and loads no gate). A ring index outside [0, nslab) makes
+ * both NaN and sets HSD_STATUS_BAD_STATE. */
+int hsd_mamba_ssm_gated(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
+                        const uint16_t* gate, int64_t gate_ld, const uint16_t* conv_w, const uint16_t* conv_b,
+                        const float* A_log, const float* dt_bias, const float* Dp, float* ssm_slabs,
+                        uint16_t* conv_slabs, const int32_t* cur, int64_t nslab, float* z, int64_t z_ld,
+                        int64_t L, int64_t H, int64_t P, int64_t N, int64_t G, float dt_lo, float dt_hi,
+                        int32_t* dev_status, void* stream);
 
 /* Replaces hsd/mamba.py:47-56 `mamba_rollback(records, n_keep)` and the cache half of
  * model.py:348-356: the state after the first n_keep rows of the last verify is its

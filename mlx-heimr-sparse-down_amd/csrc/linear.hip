@@ -118,8 +118,10 @@ __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0
 // on their way. Words t = tid + 256 i hold inputs 8t .. 8t+7.
 template <int WF, int NB, int XK, int XIT>
 struct XIn {
-  uint4 xv[NB][XIT];
-  float4 yv0[XK == HSD_X_GATED ? NB : 1][XIT], yv1[XK == HSD_X_GATED ? NB : 1][XIT];
+  static constexpr bool kF32 = XK == HSD_X_GATED || XK == HSD_X_GATED_Z;  // x is f32
+  uint4 xv[XK == HSD_X_GATED_Z ? 1 : NB][XIT];
+  float4 yv0[kF32 ? NB : 1][XIT], yv1[kF32 ? NB : 1][XIT];
+  float zp[XK == HSD_X_GATED_Z ? NB : 1][XIT];   // HSD_X_GATED_Z: a partial of the group's sum
   uint4 nwv[XIT];
 
   __device__ __forceinline__ void load(const LinArgs& a, int tid) {
@@ -129,11 +131,15 @@ struct XIn {
       const int tc = min(tid + kLT * i, NW - 1);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        if constexpr (XK == HSD_X_GATED) {
-          const float4* yr = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + b * a.x_ld);
+        if constexpr (kF32) {
+          const float* xr = reinterpret_cast<const float*>(a.x) + b * a.x_ld;
+          const float4* yr = reinterpret_cast<const float4*>(xr);
           yv0[b][i] = yr[2 * tc];
           yv1[b][i] = yr[2 * tc + 1];
-          xv[b][i] = reinterpret_cast<const uint4*>(a.gate + b * a.gate_ld)[tc];
+          if constexpr (XK == HSD_X_GATED)
+            xv[b][i] = reinterpret_cast<const uint4*>(a.gate + b * a.gate_ld)[tc];
+          else  // the group of word tc (64 words) has partials 32 (tc / 64) .. + 31
+            zp[b][i] = xr[a.I + 32 * (tc >> 6) + (tid & 31)];
         } else {
           xv[b][i] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + b * a.x_ld)[tc];
         }
@@ -184,6 +190,33 @@ struct XIn {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const uint32_t t = pack_bf16x2(lo_f(xw[c]) * inv, hi_f(xw[c]) * inv);
+            xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
+          }
+        }
+      }
+    } else if constexpr (XK == HSD_X_GATED_Z) {
+      // a wavefront's 64 words of iteration i are one 512-element group; its 32 partials
+      // (in lanes 0-31, repeated in 32-63) summed with DPP inside 16-lane rows, then the
+      // lower row's total plus the upper's (v_permlane16_swap)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int i = 0; i < XIT; ++i) {
+          float g = zp[b][i];
+          g += dpp_f32<0xB1>(g);
+          g += dpp_f32<0x4E>(g);
+          g += dpp_f32<0x141>(g);
+          g += dpp_f32<0x140>(g);
+          const uint32_t gb = __float_as_uint(g);
+          const auto pg = __builtin_amdgcn_permlane16_swap(gb, gb, false, false);
+          g = __uint_as_float(pg[0]) + __uint_as_float(pg[1]);
+          const float inv = __builtin_amdgcn_rsqf(g / 512.0f + a.eps);
+          const float z[8] = {yv0[b][i].x, yv0[b][i].y, yv0[b][i].z, yv0[b][i].w,
+                              yv1[b][i].x, yv1[b][i].y, yv1[b][i].z, yv1[b][i].w};
+          const uint32_t nw4[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t t = pack_bf16x2(z[2 * c] * inv, z[2 * c + 1] * inv);
             xo[b][i][c] = pack_bf16x2(lo_f(t) * lo_f(nw4[c]), hi_f(t) * hi_f(nw4[c]));
           }
         }
@@ -817,7 +850,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (!x || !w || (y_kind != HSD_Y_ARGMAX && !y)) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (w_kind == HSD_W_Q4 && (!scales || !biases)) return set_error(HSD_ERR_ARG, "%s: 4-bit weights need scales and biases", fn);
   if (w_kind != HSD_W_Q4 && w_kind != HSD_W_BF16) return set_error(HSD_ERR_DTYPE, "%s: w_kind %d", fn, w_kind);
-  if (x_kind != HSD_X_BF16 && x_kind != HSD_X_RMS && x_kind != HSD_X_GATED)
+  if (x_kind != HSD_X_BF16 && x_kind != HSD_X_RMS && x_kind != HSD_X_GATED && x_kind != HSD_X_GATED_Z)
     return set_error(HSD_ERR_DTYPE, "%s: x_kind %d", fn, x_kind);
   if (y_kind < HSD_Y_BF16 || y_kind > HSD_Y_ARGMAX) return set_error(HSD_ERR_DTYPE, "%s: y_kind %d", fn, y_kind);
   if (x_kind != HSD_X_BF16 && !norm_w) return set_error(HSD_ERR_ARG, "%s: the normalisation needs norm_w", fn);
@@ -831,8 +864,12 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (I <= 0 || I > kLMaxI || I % (w_kind == HSD_W_Q4 ? 64 : 8))
     return set_error(HSD_ERR_SHAPE, "%s: I must be a multiple of %d and at most %d", fn,
                      w_kind == HSD_W_Q4 ? 64 : 8, kLMaxI);
-  if (x_kind == HSD_X_GATED && I % 512) return set_error(HSD_ERR_SHAPE, "%s: the gated norm needs I %% 512 == 0", fn);
-  const int64_t xe = x_kind == HSD_X_GATED ? 4 : 2;   // x element bytes
+  const bool gated = x_kind == HSD_X_GATED || x_kind == HSD_X_GATED_Z;
+  if (gated && I % 512) return set_error(HSD_ERR_SHAPE, "%s: the gated norm needs I %% 512 == 0", fn);
+  if (x_kind == HSD_X_GATED_Z && x_ld < I + I / 16)
+    return set_error(HSD_ERR_SHAPE, "%s: HSD_X_GATED_Z rows hold I + I/16 values (x_ld >= %lld)", fn,
+                     (long long)(I + I / 16));
+  const int64_t xe = gated ? 4 : 2;                   // x element bytes
   if (x_ld < I || (x_ld * xe) % 16 || ((uintptr_t)x & 15u) || (norm_w && ((uintptr_t)norm_w & 15u)) ||
       ((uintptr_t)w & 15u) || (gate && (((uintptr_t)gate & 15u) || gate_ld % 8 || gate_ld < I)) ||
       (xn_out && (((uintptr_t)xn_out & 15u) || xn_ld % 8 || xn_ld < I)))
@@ -862,9 +899,10 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   const int pair = x_kind * 8 + y_kind;
   constexpr int kRB = HSD_X_RMS * 8 + HSD_Y_BF16, kRA = HSD_X_RMS * 8 + HSD_Y_ARGMAX,
                 kRF = HSD_X_RMS * 8 + HSD_Y_F32, kGR = HSD_X_GATED * 8 + HSD_Y_RESID,
+                kZR = HSD_X_GATED_Z * 8 + HSD_Y_RESID,
                 kBR = HSD_X_BF16 * 8 + HSD_Y_RESID, kBB = HSD_X_BF16 * 8 + HSD_Y_BF16;
   const bool ok = w_kind == HSD_W_Q4 ? (pair == kRB || pair == kRA || pair == kRF || pair == kGR ||
-                                        pair == kBR || pair == kBB)
+                                        pair == kZR || pair == kBR || pair == kBB)
                                      : (pair == kRB || pair == kBB);
   if (!ok)
     return set_error(HSD_ERR_SHAPE, "%s: unsupported combination x_kind %d, y_kind %d, w_kind %d", fn, x_kind,
@@ -898,6 +936,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
           case kRA: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_ARGMAX); break;      \
           case kRF: HSD_LIN_I(WF, NB, HSD_X_RMS, HSD_Y_F32); break;         \
           case kGR: HSD_LIN_I(WF, NB, HSD_X_GATED, HSD_Y_RESID); break;     \
+          case kZR: HSD_LIN_I(WF, NB, HSD_X_GATED_Z, HSD_Y_RESID); break;   \
           default: HSD_LIN_I(WF, NB, HSD_X_BF16, HSD_Y_RESID); break;      \
         }                                                                  \
       }                                                                    \
@@ -926,6 +965,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     case kRA: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_ARGMAX); break;            \
     case kRF: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_F32); break;               \
     case kGR: HSD_Q4_I(NB, HSD_X_GATED, HSD_Y_RESID); break;           \
+    case kZR: HSD_Q4_I(NB, HSD_X_GATED_Z, HSD_Y_RESID); break;         \
     default: HSD_Q4_I(NB, HSD_X_BF16, HSD_Y_RESID); break;             \
   }
   if (mfma) {

@@ -18,7 +18,10 @@
 //   (a lane's 8 products, then a butterfly over the row's 16 lanes), and writes each
 //   row's S to its checkpoint slab. HBM: read S once, write L checkpoints; all loads in
 //   two round trips (the ring index, then what depends on it).
-// The gated RMSNorm (groups of 512 = 8 heads) runs as a second small kernel.
+// The gated RMSNorm (groups of 512 = 8 heads) runs as a second small kernel
+// (hsd_mamba_verify), or in out_proj's prologue: hsd_mamba_ssm_gated has this kernel apply
+// the gate (z = y silu(gate)) and write, after each row's z, every 16-channel block's sum
+// of z^2, so the prologue only adds 32 partials per group (no silu, no gate loads).
 #include "hsd_common.h"
 
 namespace hsd {
@@ -35,9 +38,11 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     int64_t dt_ld, const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ conv_b,
     const float* __restrict__ A_log, const float* __restrict__ dt_bias,
     const float* __restrict__ Dp, float* __restrict__ ssm, uint16_t* __restrict__ convs,
-    const int32_t* __restrict__ cur_ptr, int nslab, float* __restrict__ y_pre, int L, int H,
-    int P, int G, float dt_lo, float dt_hi, int32_t* __restrict__ status) {
+    const int32_t* __restrict__ cur_ptr, int nslab, float* __restrict__ y_pre, int64_t y_ld,
+    const uint16_t* __restrict__ gate, int64_t gate_ld, int L, int H, int P, int G, float dt_lo,
+    float dt_hi, int32_t* __restrict__ status) {
   __shared__ float xs[kLMax][kPB];
+  __shared__ float zsq[kLMax][kPB];
   __shared__ __attribute__((aligned(16))) float Bs[kLMax][kN];
   __shared__ __attribute__((aligned(16))) float Cs[kLMax][kN];
   __shared__ float dtv[kLMax], dA[kLMax];
@@ -84,13 +89,22 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   const uint16_t b1 = conv_b[ch1], b2 = conv_b[ch2];
   const int rd = min(max(tid - 64, 0), L - 1);  // wave 1's first L lanes: dt and dA
   const uint16_t dtr = dt_raw[(size_t)rd * dt_ld + hh];
+  // the gate of this thread's output channel (state row p below) for every row: read from
+  // conv_in (in bounds, unused) when there is no gate, so the load is unconditional
+  const uint16_t* gsrc = gate ? gate : conv_in;
+  const int64_t gld = gate ? gate_ld : cin_ld;
+  const int pg = pblk * kPB + (tid >> 6) * (kPB / (kMT / 64)) + ((tid & 63) >> 4);
+  uint16_t gv[kLMax];
+#pragma unroll
+  for (int r = 0; r < kLMax; ++r) gv[r] = gsrc[(size_t)min(r, L - 1) * gld + (size_t)hh * P + pg];
   // D enters the recurrence rounded to bf16, as the reference passes m.D.astype(x.dtype)
   // to ssm_update (mamba.py:38)
   const float Alog = A_log[hh], dtb = dt_bias[hh], Dh = bf16_bits_to_f32(f32_to_bf16_bits(Dp[hh]));
   if ((unsigned)cur >= (unsigned)nslab) {
     // a corrupt ring index: no state is read or written; the rows' outputs become NaN and
     // the status word says why
-    if (tid < kPB * L) y_pre[(size_t)(tid / kPB) * (H * P) + (size_t)hh * P + pblk * kPB + tid % kPB] = __int_as_float(0x7FC00000);
+    if (tid < kPB * L) y_pre[(size_t)(tid / kPB) * y_ld + (size_t)hh * P + pblk * kPB + tid % kPB] = __int_as_float(0x7FC00000);
+    if (gate && tid < L) y_pre[(size_t)tid * y_ld + DI + (size_t)hh * npb + pblk] = __int_as_float(0x7FC00000);
     if (tid == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_STATE);
     return;
   }
@@ -195,7 +209,25 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
     y += dpp_f32<0x4E>(y);   // quad_perm [2, 3, 0, 1]
     y += dpp_f32<0x141>(y);  // row_half_mirror
     y += dpp_f32<0x140>(y);  // row_mirror
-    if (c8 == 0) y_pre[(size_t)r * DI + (size_t)hh * P + p] = y + x * Dh;
+    if (c8 == 0) {
+      float yo = y + x * Dh;
+      if (gate) {                                      // uniform
+        yo *= silu_f32(bf16_bits_to_f32(gv[r]));
+        zsq[r][pl] = yo * yo;
+      }
+      y_pre[(size_t)r * y_ld + (size_t)hh * P + p] = yo;
+    }
+  }
+  if (gate) {
+    // this block's sum of z^2 over its 16 channels (in channel order) per row, after the
+    // row's z values: the gated norm's group sums start from these partials
+    lds_barrier();
+    if (tid < L) {
+      float s = zsq[tid][0];
+#pragma unroll
+      for (int i = 1; i < kPB; ++i) s += zsq[tid][i];
+      y_pre[(size_t)tid * y_ld + DI + (size_t)hh * npb + pblk] = s;
+    }
   }
 }
 
@@ -358,8 +390,8 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
   float* y_pre = reinterpret_cast<float*>(workspace);
   hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, st, conv_in,
                      conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias, Dp, ssm_slabs,
-                     conv_slabs, cur, (int)nslab, y_pre, (int)L, (int)H, (int)P, (int)G, dt_lo,
-                     dt_hi, dev_status);
+                     conv_slabs, cur, (int)nslab, y_pre, (int64_t)DI, nullptr, (int64_t)0, (int)L, (int)H,
+                     (int)P, (int)G, dt_lo, dt_hi, dev_status);
   int rc = check_launch(fn);
   if (rc) return rc;
   const unsigned ngrid = (unsigned)(L * (DI / norm_group));
@@ -398,12 +430,12 @@ extern "C" int hsd_mamba_select_row(int32_t* cur, const int32_t* n_keep_dev, int
   return check_launch("hsd_mamba_select_row");
 }
 
-extern "C" int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
-                             const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log,
-                             const float* dt_bias, const float* Dp, float* ssm_slabs, uint16_t* conv_slabs,
-                             const int32_t* cur, int64_t nslab, float* y, int64_t L, int64_t H, int64_t P,
-                             int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream) {
-  const char* fn = "hsd_mamba_ssm";
+namespace {
+int launch_ssm(const char* fn, const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
+               const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log, const float* dt_bias,
+               const float* Dp, float* ssm_slabs, uint16_t* conv_slabs, const int32_t* cur, int64_t nslab, float* y,
+               int64_t y_ld, const uint16_t* gate, int64_t gate_ld, int64_t L, int64_t H, int64_t P, int64_t N,
+               int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream) {
   if (!conv_in || !dt_raw || !conv_w || !conv_b || !A_log || !dt_bias || !Dp || !ssm_slabs || !conv_slabs ||
       !cur || !y)
     return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
@@ -415,12 +447,38 @@ extern "C" int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const 
     return set_error(HSD_ERR_SHAPE, "%s: need P %% %d == 0 and H %% G == 0", fn, kPB);
   const int64_t DI = H * P, CD = DI + 2 * G * N;
   if (conv_in_ld < CD || dt_ld < H) return set_error(HSD_ERR_SHAPE, "%s: row strides smaller than the rows", fn);
+  if (y_ld < (gate ? DI + DI / kPB : DI) || (gate && gate_ld < DI))
+    return set_error(HSD_ERR_SHAPE, "%s: row strides smaller than the rows", fn);
   if ((uintptr_t)ssm_slabs & 15u) return set_error(HSD_ERR_ALIGN, "%s: ssm_slabs must be 16-byte aligned", fn);
   if (H * (P / kPB) > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
   hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, as_stream(stream), conv_in,
                      conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias, Dp, ssm_slabs, conv_slabs, cur,
-                     (int)nslab, y, (int)L, (int)H, (int)P, (int)G, dt_lo, dt_hi, dev_status);
+                     (int)nslab, y, y_ld, gate, gate_ld, (int)L, (int)H, (int)P, (int)G, dt_lo, dt_hi, dev_status);
   return check_launch(fn);
+}
+}  // namespace
+
+extern "C" int hsd_mamba_ssm(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw, int64_t dt_ld,
+                             const uint16_t* conv_w, const uint16_t* conv_b, const float* A_log,
+                             const float* dt_bias, const float* Dp, float* ssm_slabs, uint16_t* conv_slabs,
+                             const int32_t* cur, int64_t nslab, float* y, int64_t L, int64_t H, int64_t P,
+                             int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status, void* stream) {
+  return launch_ssm("hsd_mamba_ssm", conv_in, conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias, Dp,
+                    ssm_slabs, conv_slabs, cur, nslab, y, H * P, nullptr, 0, L, H, P, N, G, dt_lo, dt_hi,
+                    dev_status, stream);
+}
+
+extern "C" int hsd_mamba_ssm_gated(const uint16_t* conv_in, int64_t conv_in_ld, const uint16_t* dt_raw,
+                                   int64_t dt_ld, const uint16_t* gate, int64_t gate_ld, const uint16_t* conv_w,
+                                   const uint16_t* conv_b, const float* A_log, const float* dt_bias,
+                                   const float* Dp, float* ssm_slabs, uint16_t* conv_slabs, const int32_t* cur,
+                                   int64_t nslab, float* z, int64_t z_ld, int64_t L, int64_t H, int64_t P,
+                                   int64_t N, int64_t G, float dt_lo, float dt_hi, int32_t* dev_status,
+                                   void* stream) {
+  if (!gate) return set_error(HSD_ERR_ARG, "hsd_mamba_ssm_gated: null gate");
+  return launch_ssm("hsd_mamba_ssm_gated", conv_in, conv_in_ld, dt_raw, dt_ld, conv_w, conv_b, A_log, dt_bias,
+                    Dp, ssm_slabs, conv_slabs, cur, nslab, z, z_ld, gate, gate_ld, L, H, P, N, G, dt_lo, dt_hi,
+                    dev_status, stream);
 }
 
 extern "C" int hsd_greedy_accept(const void* logits, int dtype, int64_t k, int64_t V,

@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("HSD_LIB") or os.path.join(_PKG_ROOT, "libhsd.so")
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 STATUS_BAD_EXPERT, STATUS_BAD_STATE, STATUS_BAD_TOKEN = 1, 2, 4
-X_BF16, X_RMS, X_GATED = 0, 1, 2
+X_BF16, X_RMS, X_GATED, X_GATED_Z = 0, 1, 2, 3
 W_Q4, W_BF16 = 0, 1
 Y_BF16, Y_F32, Y_RESID, Y_ARGMAX = 0, 1, 2, 3
 # sequence state indices (include/hsd.h HSD_SEQ_*)
@@ -52,6 +52,8 @@ _SIGS = {
                          + [_c_i64] * 6 + [_c_float] * 3 + [_vp, _vp, _c_size, _vp]),
     "hsd_mamba_ssm": (_c_int, [_vp, _c_i64, _vp, _c_i64] + [_vp] * 8 + [_c_i64, _vp] + [_c_i64] * 5
                       + [_c_float] * 2 + [_vp, _vp]),
+    "hsd_mamba_ssm_gated": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64] + [_vp] * 8 + [_c_i64, _vp, _c_i64]
+                            + [_c_i64] * 5 + [_c_float] * 2 + [_vp, _vp]),
     "hsd_mamba_select_row": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "hsd_greedy_accept": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
     "hsd_moe_up_relu2": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]

@@ -110,11 +110,14 @@ def verify_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out_dtype=torch.bfl
     return y
 
 
-def ssm_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out=None, status=None):
+def ssm_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out=None, status=None, gated=False):
     """The conv + SSM update of L rows from the in_proj output proj [L, 2*H*P + 2*G*N + H]
     (gate | conv input | dt) with the per-row checkpoints written, without the gated norm:
     -> y [L, H*P] f32 (sum_n S C + D x), which out_proj consumes through nn.linear's gated
-    norm prologue (with the gate columns of proj)."""
+    norm prologue (with the gate columns of proj).
+    gated=True: the gate applied here (hsd_mamba_ssm_gated) -> z [L, H*P] f32 = y silu(gate),
+    a view of rows of H*P + H*P/16 values whose tail holds each 16 channels' sum of z^2;
+    out_proj then takes it with nn.linear(..., gated_z=True)."""
     if proj.dtype != torch.bfloat16:
         raise N.HSDError("the Mamba-2 update takes the bf16 in_proj output")
     L = proj.shape[0]
@@ -122,12 +125,24 @@ def ssm_rows(mixer: Mamba2Mixer, proj, cache: MambaCache, out=None, status=None)
     DI, CD = mixer.intermediate_size, mixer.conv_dim
     if proj.shape[1] < DI + CD + H or proj.stride(1) != 1:
         raise N.HSDError(f"proj needs {DI + CD + H} unit-stride columns")
-    y = out if out is not None else torch.empty((L, DI), dtype=torch.float32, device=proj.device)
     es = proj.element_size()
     import ctypes
     conv_p = ctypes.c_void_p(proj.data_ptr() + DI * es)
     dt_p = ctypes.c_void_p(proj.data_ptr() + (DI + CD) * es)
     lo, hi = mixer.time_step_limit
+    if gated:
+        zw = DI + DI // 16
+        if out is None:
+            out = torch.empty((L, zw), dtype=torch.float32, device=proj.device)
+        if out.dtype != torch.float32 or out.shape[0] < L or out.stride(1) != 1 or out.stride(0) < zw:
+            raise N.HSDError(f"ssm_rows(gated=True) needs f32 rows of at least {zw} values")
+        N.call("hsd_mamba_ssm_gated", conv_p, proj.stride(0), dt_p, proj.stride(0), N.ptr(proj), proj.stride(0),
+               N.ptr(N.contig(mixer.conv_w)), N.ptr(N.contig(mixer.conv_b)), N.ptr(N.contig(mixer.A_log)),
+               N.ptr(N.contig(mixer.dt_bias)), N.ptr(N.contig(mixer.D)), N.ptr(cache.ssm), N.ptr(cache.conv),
+               N.ptr(cache.cur), cache.nslab, N.ptr(out), out.stride(0), L, H, P, Nst, G, float(lo), float(hi),
+               N.ptr(status), N.stream(proj.device))
+        return out[:L, :DI]
+    y = out if out is not None else torch.empty((L, DI), dtype=torch.float32, device=proj.device)
     N.call("hsd_mamba_ssm", conv_p, proj.stride(0), dt_p, proj.stride(0), N.ptr(N.contig(mixer.conv_w)),
            N.ptr(N.contig(mixer.conv_b)), N.ptr(N.contig(mixer.A_log)), N.ptr(N.contig(mixer.dt_bias)),
            N.ptr(N.contig(mixer.D)), N.ptr(cache.ssm), N.ptr(cache.conv), N.ptr(cache.cur), cache.nslab, N.ptr(y), L,
@@ -151,7 +166,8 @@ def mamba_verify(block, x3, cache, records):
     if hasattr(block, "in_proj") and hasattr(block, "norm_w") and hasattr(block, "rows"):
         m = block.mixer
         buf = dict(proj=torch.empty((L, block.in_proj.O), dtype=torch.bfloat16, device=x.device),
-                   y_pre=torch.empty((L, m.intermediate_size), dtype=torch.float32, device=x.device))
+                   y_pre=torch.empty((L, m.intermediate_size + m.intermediate_size // 16), dtype=torch.float32,
+                                     device=x.device))
         out = x.clone()
         block.rows(out, buf, cache)
         records.append((cache, L))

@@ -5,8 +5,8 @@ then norm_f and lm_head, plus the optional one-layer MTP head (hsd/mtp.py). Weig
 affine 4-bit group 64 (mlx's QuantizedLinear / QuantizedEmbedding format) except the router
 gates and the MTP head's eh_proj (bf16). Every kernel is libhsd's:
 
-  Mamba-2 block   nn.linear (rms_norm fused) -> hsd_mamba_ssm -> nn.linear (gated norm +
-                  residual fused)                                       (mamba.py:19-44)
+  Mamba-2 block   nn.linear (rms_norm fused) -> hsd_mamba_ssm_gated (z and its 16-channel
+                  sums of squares) -> nn.linear (gated norm + residual fused)   (mamba.py:19-44)
   MoE block       nn.linear of the bf16 gate (rms_norm fused, the normed token kept) ->
                   the router's top-k fused into the up projections + ReLU^2 -> the sparse
                   down projection with the residual fused        (model.py:110-139)
@@ -143,9 +143,10 @@ class MambaBlock:
         """x [B, D] (updated in place)."""
         B = x.shape[0]
         proj = nn.linear(x, self.in_proj, norm=self.norm_w, eps=self.eps, out=buf["proj"][:B])
-        y = M.ssm_rows(self.mixer, proj, cache, out=buf["y_pre"][:B])
-        DI = self.mixer.intermediate_size
-        nn.linear(y, self.out_proj, norm=self.mixer.norm_w, eps=self.eps, gate=proj[:, :DI], residual=x, out=x)
+        # the gate applied in the SSM kernel, which also leaves each 16 channels' sum of z^2
+        # for out_proj's gated norm (no silu, no gate loads in its prologue)
+        z = M.ssm_rows(self.mixer, proj, cache, out=buf["y_pre"][:B], gated=True)
+        nn.linear(z, self.out_proj, norm=self.mixer.norm_w, eps=self.eps, gated_z=True, residual=x, out=x)
         return x
 
     def nbytes(self):
@@ -421,7 +422,7 @@ class NemotronModel:
         ws_down = N.lib().hsd_sparse_down_workspace_bytes(B, c.hidden, c.moe_inter, c.shared_inter, c.topk)
         ws_attn = N.lib().hsd_attn_workspace_bytes(B, c.attn_heads, c.max_seq)
         return dict(x=e(B, c.hidden), xn=e(B, c.hidden), proj=e(B, c.in_proj_dim),
-                    y_pre=e(B, c.mamba_inner, dt=torch.float32), qkv=e(B, c.qkv_dim),
+                    y_pre=e(B, c.mamba_inner + c.mamba_inner // 16, dt=torch.float32), qkv=e(B, c.qkv_dim),
                     att=e(B, c.attn_heads * c.head_dim), logits=e(B, c.n_experts),
                     hcat=e(B, c.topk * c.moe_inter + c.shared_inter), sel=e(B, c.topk, dt=torch.int32),
                     gains=e(B, c.topk + 1, dt=torch.float32),

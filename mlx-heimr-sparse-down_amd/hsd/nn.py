@@ -48,15 +48,19 @@ def argmax_slots(O, q4=True):
     return int(N.lib().hsd_linear_argmax_slots(O, N.W_Q4 if q4 else N.W_BF16))
 
 
-def linear(x, W: QWeight, *, norm=None, eps=1e-5, gate=None, residual=None, out=None, out_dtype=torch.bfloat16,
-           xn_out=None, argmax_keys=None):
+def linear(x, W: QWeight, *, norm=None, eps=1e-5, gate=None, gated_z=False, residual=None, out=None,
+           out_dtype=torch.bfloat16, xn_out=None, argmax_keys=None):
     """y = xn W^T for x [B, I] (B <= 4; longer inputs go 4 rows at a time).
     norm (bf16 [I]): xn = rms_norm(x, norm, eps) (mx.fast.rms_norm); with `gate` as well,
     x is the f32 SSM output and xn the Mamba-2 gated RMSNorm of x * silu(gate) per group of
-    512. residual: y = bf16(residual + bf16(xn W^T)) (out may be residual). argmax_keys
+    512; gated_z=True: x is mamba.ssm_rows(..., gated=True)'s z (its rows carry the
+    16-channel sums of z^2 past column I) and xn the same gated norm.
+    residual: y = bf16(residual + bf16(xn W^T)) (out may be residual). argmax_keys
     ([B, slots] int64): the greedy argmax's per-workgroup keys instead of y (y still
     written when out is given). xn_out: receives xn (bf16 [B, I])."""
     B = x.shape[0]
+    if B > MAX_ROWS and gated_z:
+        raise N.HSDError(f"the gated_z prologue takes at most {MAX_ROWS} rows")
     if B > MAX_ROWS:
         if argmax_keys is not None:
             raise N.HSDError(f"argmax takes at most {MAX_ROWS} rows")
@@ -69,7 +73,11 @@ def linear(x, W: QWeight, *, norm=None, eps=1e-5, gate=None, residual=None, out=
         return y
     if x.shape[1] != W.I:
         raise N.HSDError(f"linear: x has {x.shape[1]} columns, the weight {W.I} inputs")
-    if gate is not None:
+    if gated_z:
+        xk = N.X_GATED_Z
+        if x.dtype != torch.float32 or norm is None or gate is not None or x.stride(0) < W.I + W.I // 16:
+            raise N.HSDError("gated_z takes ssm_rows(gated=True)'s z (rows of I + I/16 values) and a norm weight")
+    elif gate is not None:
         xk = N.X_GATED
         if x.dtype != torch.float32 or norm is None:
             raise N.HSDError("the gated norm takes the f32 SSM output and a norm weight")

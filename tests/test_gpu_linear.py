@@ -46,8 +46,11 @@ def ulp_close(a_bits, b_bits):
     return np.all(np.abs(sa - sb) <= 1), float(np.mean(a == b))
 
 
-@pytest.mark.parametrize("I,O_", [(2688, 2688), (4096, 1024), (2688, 10304)])
+@pytest.mark.parametrize("I,O_", [(2688, 2688), (4096, 1024), (2688, 10304), (2688, 20480), (4096, 16384),
+                                  (1024, 96)])
 def test_rms_linear_matches_oracle(dev, I, O_):
+    """(2688, 20480) and (4096, 16384): more 16-row blocks than resident workgroups, so a
+    workgroup runs several blocks in turn; (1024, 96): 32 pieces a row, one pass."""
     (w, s, b), W = q4_weight(10 + I, O_, I, dev)
     rng = np.random.default_rng(20)
     nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))

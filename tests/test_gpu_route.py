@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from hsd import mamba as M, moe, synth as S
+from hsd import mamba as M, moe, synth as S, nn
 from oracle import hsd_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -88,6 +88,58 @@ def test_ssm_only_entry(dev):
     assert torch.equal(c1.conv.view(torch.int16), c2.conv.view(torch.int16))
 
 
+def test_ssm_gated_entry(dev):
+    """hsd_mamba_ssm_gated: z = y * silu(gate) against the plain entry's y (same state,
+    same checkpoints), the 16-channel sums of z^2 against float64 sums of the returned z,
+    and the out_proj prologue that consumes them (HSD_X_GATED_Z) against the oracle's
+    gated norm; a row of a 3-row call equals that row alone, bit for bit."""
+    p = S.mamba_params_np(13)
+    mixer = M.Mamba2Mixer(conv_w=S.to_device(p["conv_w"], dev), conv_b=S.to_device(p["conv_b"], dev),
+                          A_log=S.to_device(p["A_log"], dev), dt_bias=S.to_device(p["dt_bias"], dev),
+                          D=S.to_device(p["D"], dev), norm_w=S.to_device(p["norm_w"], dev))
+    rows = S.mamba_rows_np(np.random.default_rng(14), 3)
+    rd = S.to_device(rows, dev)
+    DI = 4096
+    fresh = lambda: M.MambaCache(mixer, dev, conv_state=S.to_device(p["conv_state"], dev),
+                                 ssm_state=torch.from_numpy(p["ssm_state"]).to(dev))
+    c1, c2 = fresh(), fresh()
+    y = M.ssm_rows(mixer, rd, c1).cpu().numpy().astype(np.float64)
+    zbuf = torch.full((3, DI + DI // 16 + 4), float("nan"), dtype=torch.float32, device=dev)  # strided rows
+    z = M.ssm_rows(mixer, rd, c2, out=zbuf, gated=True)
+    assert torch.equal(c1.ssm.view(torch.int32), c2.ssm.view(torch.int32))
+    assert torch.equal(c1.conv.view(torch.int16), c2.conv.view(torch.int16))
+    zh = z.cpu().numpy().astype(np.float64)
+    g = O.bf16_to_f32(rows[:, :DI]).astype(np.float64)
+    zref = y * O.silu(g)
+    assert np.all(np.abs(zh - zref) <= 1e-5 * np.abs(zref) + 1e-6 * np.abs(y))
+    part = zbuf[:, DI:DI + DI // 16].cpu().numpy().astype(np.float64)
+    pref = (zh * zh).reshape(3, DI // 16, 16).sum(-1)
+    assert np.all(np.abs(part - pref) <= 1e-5 * pref + 1e-30)
+    assert torch.isnan(zbuf[:, DI + DI // 16:]).all()          # nothing past the partials
+    # the consumer: out_proj's gated norm from z and the partials
+    I, O_ = DI, 2688
+    rng = np.random.default_rng(15)
+    w, s, b = S.down_proj_np(rng, (), O_, I)
+    W = nn.QWeight(S.to_device(w, dev), S.to_device(s, dev), S.to_device(b, dev))
+    nw = O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32))
+    res = torch.zeros((3, O_), dtype=torch.bfloat16, device=dev)
+    xn = torch.empty((3, I), dtype=torch.bfloat16, device=dev)
+    out = nn.linear(z, W, norm=S.to_device(nw, dev), gated_z=True, residual=res, xn_out=xn)
+    xn_h = S.to_host(xn)
+    want = O.gated_rms_norm_bf16(y, g, O.bf16_to_f32(nw), 1e-5)
+    a, bb = xn_h.astype(np.int32), want.astype(np.int32)
+    sa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+    sb = np.where(bb & 0x8000, -(bb & 0x7FFF), bb & 0x7FFF)
+    print(f"gated_z norm: identical {np.mean(a == bb):.4f}")
+    assert np.all(np.abs(sa - sb) <= 1) and np.mean(a == bb) >= 0.99
+    ref = O.linear_q4(O.bf16_to_f32(xn_h), w, s, b)
+    assert np.all(np.abs(out.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+    for r in range(3):
+        res1 = torch.zeros((1, O_), dtype=torch.bfloat16, device=dev)
+        o1 = nn.linear(z[r:r + 1], W, norm=S.to_device(nw, dev), gated_z=True, residual=res1)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
+
+
 def test_corrupt_ring_index_is_reported(dev):
     p = S.mamba_params_np(11)
     mixer = M.Mamba2Mixer(conv_w=S.to_device(p["conv_w"], dev), conv_b=S.to_device(p["conv_b"], dev),
@@ -100,6 +152,13 @@ def test_corrupt_ring_index_is_reported(dev):
     y = M.verify_rows(mixer, S.to_device(S.mamba_rows_np(np.random.default_rng(12), 2), dev), cache, status=status)
     assert int(status.item()) == 2
     assert torch.isnan(y.float()).all()
+    assert torch.equal(cache.ssm, before)
+    # the gated entry: z and its partial sums NaN, the same status bit
+    st1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    zbuf = torch.zeros((2, 4096 + 256), dtype=torch.float32, device=dev)
+    M.ssm_rows(mixer, S.to_device(S.mamba_rows_np(np.random.default_rng(12), 2), dev), cache, out=zbuf,
+               gated=True, status=st1)
+    assert int(st1.item()) == 2 and torch.isnan(zbuf).all()
     assert torch.equal(cache.ssm, before)
     # a device n_keep beyond the verify's rows leaves the ring where it is
     cache.cur.zero_()
