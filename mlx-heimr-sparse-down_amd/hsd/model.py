@@ -223,16 +223,17 @@ class MoEBlock:
         c = self.cfg
         xn = buf["xn"][:B]
         logits = nn.linear(x, self.gate, norm=self.norm_w, eps=c.eps, out=buf["logits"][:B], xn_out=xn)
-        if B == 1:
-            # one row: the router's top-k fused into the up projections (a wavefront of every
-            # routed workgroup ranks the experts), one launch fewer: 12.2 against 13.9 us
+        if B <= 3:
+            # the router's top-k fused into the up projections (a wavefront of every routed
+            # workgroup ranks the experts), one launch fewer: 12.2 against 13.9 us at one row;
+            # at three, since the top-k runs on DPP moves, the MTP-2 step takes 1.970 against
+            # 1.977 ms (it was 28.7 against 25.1 us per layer with LDS shuffles)
             hcat, sel, gains = route_up_relu2(xn, logits, self.e_bias, self.w1, self.s1, self.b1, self.sw1,
                                               self.ss1, self.sb1, topk=c.topk, routed_scale=c.routed_scale,
                                               norm_topk=c.norm_topk, out=buf["hcat"][:B], sel=buf["sel"][:B],
                                               gains=buf["gains"][:B])
         else:
-            # three rows: three times the ranking work in the fused form (28.7 us), so the
-            # router runs on its own first (25.1 us for both); same selection, same bits
+            # more rows: the router runs on its own first; same selection, same bits
             sel, gains = router_topk(logits, self.e_bias, topk=c.topk, routed_scale=c.routed_scale,
                                      norm_topk=c.norm_topk, sel=buf["sel"][:B], gains=buf["gains"][:B])
             hcat = up_relu2(xn, sel, self.w1, self.s1, self.b1, self.sw1, self.ss1, self.sb1, topk=c.topk,
