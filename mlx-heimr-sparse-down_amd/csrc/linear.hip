@@ -116,7 +116,9 @@ __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0
 // group). load() issues the loads; the caller issues its first weight loads next, so
 // finish() waits for x only (loads complete in issue order) while the weights are still
 // on their way. Words t = tid + 256 i hold inputs 8t .. 8t+7.
-template <int WF, int NB, int XK, int XIT>
+// PX (4-bit weights): the LDS pitch of a token row in 32-input pieces (the instance's
+// largest row), so that the readers' addresses are a lane base plus compile-time offsets.
+template <int WF, int NB, int XK, int XIT, int PX>
 struct XIn {
   static constexpr bool kF32 = XK == HSD_X_GATED || XK == HSD_X_GATED_Z;  // x is f32
   uint4 xv[XK == HSD_X_GATED_Z ? 1 : NB][XIT];
@@ -268,10 +270,11 @@ struct XIn {
           } else {
             pr.x = w[0]; pr.y = w[1]; pr.z = w[2]; pr.w = w[3];
           }
-          // 4-bit: word m of piece j at [m][j] (lanes holding consecutive pieces then read
-          // consecutive 16-byte words, free of bank conflicts); bf16: word t at t
-          const int slot = WF == HSD_W_Q4 ? (t & 3) * (I / 32) + (t >> 2) : t;
-          *reinterpret_cast<uint4*>(&xp[b * (I / 2) + 4 * slot]) = pr;
+          // 4-bit: word m of piece j at [m][j] with a row of PX pieces (lanes holding
+          // consecutive pieces then read consecutive 16-byte words, free of bank
+          // conflicts); bf16: word t at t
+          const int slot = WF == HSD_W_Q4 ? (t & 3) * PX + (t >> 2) : t;
+          *reinterpret_cast<uint4*>(&xp[b * (WF == HSD_W_Q4 ? 16 * PX : I / 2) + 4 * slot]) = pr;
           if (a.xn_out && blockIdx.x == 0)
             reinterpret_cast<uint4*>(a.xn_out + b * a.xn_ld)[t] = make_uint4(w[0], w[1], w[2], w[3]);
         }
@@ -283,7 +286,7 @@ struct XIn {
           s8 += dpp_f32<0x4E>(s8);
           if constexpr (PS == 64) s8 += dpp_f32<0x141>(s8);  // the other piece: row_half_mirror
           constexpr int kWS = PS / 8;                        // words per sum
-          if (t < NW && (t & (kWS - 1)) == 0) xs[b * (I / PS) + t / kWS] = s8;
+          if (t < NW && (t & (kWS - 1)) == 0) xs[b * (PX * 32 / PS) + t / kWS] = s8;
         }
       }
     }
@@ -318,7 +321,8 @@ void k_linear(LinArgs a) {
   __shared__ uint64_t kbest[4][NB];
   const int I = a.I, O = a.O, NW = I / 8;
   uint32_t* xp = lsm;
-  float* xh = reinterpret_cast<float*>(lsm + NB * (I / 2));
+  constexpr int PX = IMAX / 32;                        // 4-bit: LDS pitch of a token row in pieces
+  float* xh = reinterpret_cast<float*>(lsm + NB * (Q4 ? 16 * PX : I / 2));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nblk = (O + kRows - 1) / kRows;            // the last block may be partial
   const int NPr = I / T::kIn;                          // pieces per row
@@ -388,7 +392,7 @@ void k_linear(LinArgs a) {
   };
 
   // ---- prologue: this workgroup's copy of the NB input rows, normalised if asked
-  XIn<WF, NB, XK, XIT> xin;
+  XIn<WF, NB, XK, XIT, PX> xin;
   xin.load(a, tid);
   // the first block's weight pieces, issued after x: the prologue waits for x only (loads
   // complete in issue order), while the weights are still on their way
@@ -428,17 +432,16 @@ void k_linear(LinArgs a) {
 #pragma unroll
       for (int it = 0; it < kIt32; ++it) {
         if (it < nit32) {                                // uniform
-          const int j = jl + 32 * it;
-          const bool use = j < NPr;
-          const int jc = use ? j : NPr - 1;
-          // the token rows' x words of piece jc (the two half-wavefronts read the same)
+          const int j = jl + 32 * it;                    // < PX: inside the row's LDS pitch
+          const bool use = j < NPr;                      // past NPr: read, then dropped
+          // the token rows' x words of piece j (the two half-wavefronts read the same)
           uint4 xq[NB][4];
           float xs[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) xq[b][m] = *reinterpret_cast<const uint4*>(&xp[b * (I / 2) + (m * NPr + jc) * 4]);
-            xs[b] = xh[b * (I / 32) + jc];
+            for (int m = 0; m < 4; ++m) xq[b][m] = *reinterpret_cast<const uint4*>(&xp[b * 16 * PX + (m * PX + j) * 4]);
+            xs[b] = xh[b * PX + j];
           }
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
@@ -658,12 +661,13 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
   __shared__ float wsum[NB][4];
   __shared__ float red[2][4][NB][kQR];                 // [block parity][wavefront][token row][row]
-  const int I = a.I, O = a.O, G = I / 64, NPr = I / 32;
+  const int I = a.I, O = a.O, G = I / 64;
   // LDS: x pairs [NB][I/2] words, the group sums [NB][G], then per block parity the
   // (scale | bias << 16) words of the block's rows [2][G][16]
   uint32_t* xp = lsm;
-  float* xg = reinterpret_cast<float*>(lsm + NB * (I / 2));
-  uint32_t* sbl = lsm + NB * (I / 2) + NB * G;
+  constexpr int PX = IMAX / 32;                        // LDS pitch of a token row in pieces
+  float* xg = reinterpret_cast<float*>(lsm + NB * 16 * PX);
+  uint32_t* sbl = lsm + NB * 16 * PX + NB * (PX / 2);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, q = lane >> 4;
   const int nblk = (O + kQR - 1) / kQR;
@@ -705,7 +709,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   int blk = blockIdx.x;
   uint4 sv, bv;
   load_sc(blk, sv, bv);
-  XIn<HSD_W_Q4, NB, XK, XIT> xin;
+  XIn<HSD_W_Q4, NB, XK, XIT, PX> xin;
   xin.load(a, tid);
   Wq cur;
   load_w(blk, cur);
@@ -733,7 +737,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const uint32_t qw = i ? wb.w[it].y : wb.w[it].x;
-          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * (I / 2) + 4 * ((2 * (q & 1) + i) * NPr + p)]);
+          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + i) * PX + p)]);
           const uint4 wq = make_uint4(((qw << 3) & kNibHi) | kBfOne2, ((qw >> 1) & kNibHi) | kBfOne2,
                                       ((qw >> 5) & kNibHi) | kBfOne2, ((qw >> 9) & kNibHi) | kBfOne2);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
@@ -743,7 +747,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
         const float sv_ = lo_f(sq), bv_ = hi_f(sq);
         const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
 #pragma unroll
-        for (int r = 0; r < NB; ++r) y[r] += fmaf(s16, acc[r], bo * xg[r * G + g]);
+        for (int r = 0; r < NB; ++r) y[r] += fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
       }
     }
     // lanes 0..15 hold token rows 0..3 of output row n (acc[r]: token row 4 (l / 16) + r)
@@ -883,13 +887,12 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (B == 0) return HSD_OK;
   LinArgs a{x, x_ld, gate, gate_ld, norm_w, eps, w, scales, biases, y, y_ld, res, res_ld, xn_out, xn_ld,
             argmax_keys, key_ld, slots, (int)O, (int)I};
-  const size_t lds = (size_t)B * (I / 2) * 4 + (w_kind == HSD_W_Q4 ? (size_t)B * (I / 32) * 4 : 0);
+  const size_t lds = (size_t)B * (I / 2) * 4;          // bf16 weights (4-bit: per instance below)
   // 4-bit projections of more 16-row blocks than one grid (lm_head) take the MFMA kernel;
   // the choice depends on O only, so a token row is computed the same way at any B
   const bool mfma = w_kind == HSD_W_Q4 && (O + kQR - 1) / kQR > kLMaxGrid;
   if (mfma && (((uintptr_t)scales & 15u) || ((uintptr_t)biases & 15u)))
     return set_error(HSD_ERR_ALIGN, "%s: scales and biases must be 16-byte aligned", fn);
-  const size_t lds_q4 = (size_t)B * (I / 2) * 4 + (size_t)B * (I / 64) * 4 + (size_t)2 * kQR * (I / 64) * 4;
   hipStream_t st = as_stream(stream);
   // IMAX 3072 (pieces left over after full passes: dealt as pairs), 4096 for 4-bit rows of
   // exactly 128 pieces (no pairs), the maximum otherwise
@@ -911,8 +914,9 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   {                                                                                                   \
     constexpr bool REM = !(WF == HSD_W_Q4 && IM == kLSmallQ4);                                        \
     const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW, REM>);          \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds, kLMaxGrid)));          \
-    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), lds, st, a);      \
+    const size_t ldsx = WF == HSD_W_Q4 ? (size_t)B * 17 * (IM / 32) * 4 : lds;                        \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));         \
+    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), ldsx, st, a);     \
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                      \
   {                                                      \
@@ -951,8 +955,9 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
 #define HSD_Q4_R(NB, XK, YK, IM)                                                                  \
   {                                                                                               \
     const void* kf = reinterpret_cast<const void*>(&k_linear_q4<NB, XK, YK, IM>);                 \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, lds_q4, kLMaxGrid)));   \
-    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), lds_q4, st, a);         \
+    const size_t ldsq = (size_t)NB * (16 * (IM / 32) + IM / 64) * 4 + (size_t)2 * kQR * (I / 64) * 4; \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, ldsq, kLMaxGrid)));     \
+    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), ldsq, st, a);           \
   }
 #define HSD_Q4_I(NB, XK, YK)                                    \
   if (I <= 3072) HSD_Q4_R(NB, XK, YK, 3072)                     \
