@@ -7,7 +7,8 @@
 // 16-row block of hcat): 4 wavefronts x 4 rows, so a
 // 64-row mask group takes four workgroups (each writes its 16 bits of the group's mask).
 //   1. one round trip: the token's x, the block's expert id (a scalar load), the 16 rows'
-//      scales and biases (contiguous: one 16-byte load per thread, to LDS), and the wave's
+//      scales and biases (contiguous: 4 of each per thread, to LDS as the affine step's
+//      factors (16 s, b - 16 s) per row and group), and the wave's
 //      4 rows' 16-byte pieces (16 lanes per row, D/32 pieces per row dealt over them);
 //   2. x goes to LDS as bf16 pairs (x[i], x[i+4]) in the order of a word's nibble pairs,
 //      and the sum of x over every 32-input piece;
@@ -36,7 +37,7 @@ constexpr int kUpBlk = kUpRows * kUpWaves;      // rows per workgroup (an eighth
 constexpr int kUpMaxD = 4096;                   // inputs per token held in LDS (the larger instance)
 constexpr int kUpSmallD = 3072;                 // the smaller instance (the reference shape's 2688)
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
-              "a block is a quarter or an eighth of a mask group; one scale load per thread");
+              "a block is a quarter or an eighth of a mask group; 4 scales and biases per thread");
 // Two instances by the largest D: the register arrays (x words, the lane's weight pieces)
 // are sized for it, so D <= 3072 takes 72 VGPRs and runs 7 wavefronts per SIMD where the
 // 4096 instance takes 96 (5 per SIMD): at three token rows (11136 wavefronts) the MTP-2
@@ -142,8 +143,8 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   __shared__ __attribute__((aligned(16))) uint32_t xp[MAXD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
   __shared__ int nib[kUpWaves];
-  __shared__ __attribute__((aligned(16))) uint16_t sl[kUpBlk * (MAXD / 64)];  // [row][group]
-  __shared__ __attribute__((aligned(16))) uint16_t bl[kUpBlk * (MAXD / 64)];
+  // per (row, group) of the block: (16 s, b - 16 s), the factors of the affine step
+  __shared__ __attribute__((aligned(16))) float2 sbt[kUpBlk * (MAXD / 64)];  // [row][group]
   const int b = blockIdx.y, blk = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
@@ -196,11 +197,12 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   const uint32_t* wb = routed ? w1 : sw1;
   const uint16_t* sb = routed ? s1 : ss1;
   const uint16_t* bb = routed ? b1 : sb1;
-  // the block's scales and biases: kUpBlk NGD bf16 each, contiguous and 16-byte aligned;
-  // threads [0, nsc) load s, [nsc, 2 nsc) load b (2 nsc <= kUpThreads)
-  const int nsc = kUpBlk * NGD / 8;
-  const int sc_i = tid < nsc ? tid : min(tid - nsc, nsc - 1);
-  const uint4 scv = reinterpret_cast<const uint4*>((tid < nsc ? sb : bb) + row0 * NGD)[sc_i];
+  // the block's scales and biases: kUpBlk NGD bf16 each, contiguous; thread t < nsc loads
+  // entries 4t .. 4t+3 of both
+  const int nsc = kUpBlk * NGD / 4;
+  const int sc_i = min(tid, nsc - 1);
+  const uint2 sv2 = reinterpret_cast<const uint2*>(sb + row0 * NGD)[sc_i];
+  const uint2 bv2 = reinterpret_cast<const uint2*>(bb + row0 * NGD)[sc_i];
   // pieces: lanes 16 i .. 16 i + 15 take row i of the wave's 4, lane l its pieces
   // j = l % 16 + 16 it (it < NP / 16 rounded up)
   constexpr int kIt = (kUpMaxP + 15) / 16;
@@ -235,7 +237,20 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
     s8 += dpp_f32<0x4E>(s8);
     if (t < NW && (t & 3) == 0) xh[t >> 2] = s8;
   }
-  if (tid < 2 * nsc) *reinterpret_cast<uint4*>((tid < nsc ? sl : bl) + 8 * sc_i) = scv;
+  if (tid < nsc) {
+    const uint32_t sw[2] = {sv2.x, sv2.y}, bw[2] = {bv2.x, bv2.y};
+    float f[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float sc = bf16_bits_to_f32((c & 1) ? sw[c >> 1] >> 16 : sw[c >> 1] & 0xFFFFu);
+      const float bi = bf16_bits_to_f32((c & 1) ? bw[c >> 1] >> 16 : bw[c >> 1] & 0xFFFFu);
+      f[2 * c] = 16.0f * sc;
+      f[2 * c + 1] = fmaf(-16.0f, sc, bi);
+    }
+    float4* dst = reinterpret_cast<float4*>(&sbt[4 * sc_i]);
+    dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+    dst[1] = make_float4(f[4], f[5], f[6], f[7]);
+  }
   lds_barrier();
 
   // ---- the lane's pieces into its row partial, then the row's 16-lane sum
@@ -262,8 +277,8 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
         acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
         acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
       }
-      const float sc = bf16_bits_to_f32(sl[rl * NGD + jc / 2]), bi = bf16_bits_to_f32(bl[rl * NGD + jc / 2]);
-      pr += use ? fmaf(16.0f * sc, acc, fmaf(-16.0f, sc, bi) * xh[jc]) : 0.0f;
+      const float2 f = sbt[rl * NGD + jc / 2];
+      pr += use ? fmaf(f.x, acc, f.y * xh[jc]) : 0.0f;
     }
   }
   // 16-lane sum (quad_perm xor 1, xor 2, row_half_mirror, row_mirror): every lane of a row
