@@ -39,13 +39,15 @@ constexpr int kUpSmallD = 3072;                 // the smaller instance (the ref
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
               "a block is a quarter or an eighth of a mask group; 4 scales and biases per thread");
 // Two instances by the largest D: the register arrays (x words, the lane's weight pieces)
-// are sized for it, so D <= 3072 takes 72 VGPRs and runs 7 wavefronts per SIMD where the
-// 4096 instance takes 96 (5 per SIMD): at three token rows (11136 wavefronts) the MTP-2
-// step measured 2.196 against 2.221 ms; forcing 8 per SIMD spilled (2.433 ms).
+// are sized for it, so D <= 3072 takes 64 VGPRs and runs 8 wavefronts per SIMD where the
+// 4096 instance takes 74 (6 per SIMD). A single instance for D <= 4096 (96 VGPRs, 5 per
+// SIMD) had made the MTP-2 step 2.221 against 2.196 ms for 72 VGPRs and 7 per SIMD; 8 per
+// SIMD fit once the x rows in LDS took a compile-time pitch (no per-piece address
+// registers).
 template <int MAXD> struct UpShape {
   static constexpr int kMaxP = MAXD / 32;
   static constexpr int kXIt = (MAXD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
-  static constexpr int kWaves = MAXD <= kUpSmallD ? 7 : 5;               // per SIMD
+  static constexpr int kWaves = MAXD <= kUpSmallD ? 8 : 6;               // per SIMD
 };
 // 16-row workgroups (4 rows per wavefront): at three token rows 19.0 against 19.8 us per
 // call for 8-row ones (fewer rounds of workgroups), at one row the same. Small workgroups
@@ -138,7 +140,8 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
     const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
     uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
     int E, Router rt) {
-  // x pairs: piece j, word m, pair n at xp[4 (m NP + j) + n] = (x[32 j + 8 m + n], x[.. + 4])
+  // x pairs: piece j, word m, pair n at xp[4 (m kUpMaxP + j) + n] = (x[32 j + 8 m + n], x[.. + 4])
+  // (a row of kUpMaxP pieces: the readers' addresses are a lane base plus constant offsets)
   constexpr int kUpMaxP = UpShape<MAXD>::kMaxP, kUpXIt = UpShape<MAXD>::kXIt;
   __shared__ __attribute__((aligned(16))) uint32_t xp[MAXD / 2];
   __shared__ float xh[kUpMaxP];  // sum of x over each 32-input piece
@@ -228,7 +231,7 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
       pr.w = el(3) | (el(7) << 16);
       // word m of piece j at [m][j]: lanes holding consecutive pieces read consecutive
       // 16-byte words (no LDS bank conflicts)
-      *reinterpret_cast<uint4*>(&xp[4 * ((t & 3) * NP + (t >> 2))]) = pr;
+      *reinterpret_cast<uint4*>(&xp[4 * ((t & 3) * kUpMaxP + (t >> 2))]) = pr;
     }
     float s8 = 0.0f;
 #pragma unroll
@@ -259,15 +262,14 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
     if (it < nit) {  // uniform
-      const int j = jl + 16 * it;
-      const bool use = j < NP;
-      const int jc = use ? j : NP - 1;
+      const int j = jl + 16 * it;                      // < kUpMaxP: inside the LDS pitch
+      const bool use = j < NP;                         // past NP: read, then dropped
       const uint32_t qw[4] = {q[it].x, q[it].y, q[it].z, q[it].w};
       float acc = 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         // the four rows' lanes read the same words (one LDS access serves all four)
-        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[4 * (m * NP + jc)]);
+        const uint4 xq = *reinterpret_cast<const uint4*>(&xp[4 * (m * kUpMaxP + j)]);
         const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
         // nibble n (bits 4n..4n+3 of each half) to bits 3..6: a left shift by 3 for n = 0,
         // right shifts by 1, 5, 9 for the others
@@ -277,8 +279,8 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
         acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
         acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
       }
-      const float2 f = sbt[rl * NGD + jc / 2];
-      pr += use ? fmaf(f.x, acc, f.y * xh[jc]) : 0.0f;
+      const float2 f = sbt[rl * NGD + min(j, NP - 1) / 2];
+      pr += use ? fmaf(f.x, acc, f.y * xh[j]) : 0.0f;
     }
   }
   // 16-lane sum (quad_perm xor 1, xor 2, row_half_mirror, row_mirror): every lane of a row
