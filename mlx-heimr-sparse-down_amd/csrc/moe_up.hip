@@ -88,9 +88,10 @@ __device__ __forceinline__ uint32_t ordered_bits(float c) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Token row b's experts e[0..topk) and gains g[0..topk) (every lane gets them); every lane
-// of one wavefront calls it.
-__device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, int topk, int lane,
+// Token row b's experts e[0..rounds) in rank order, and with rounds == topk the gains
+// g[0..topk) (every lane gets them); every lane of one wavefront calls it. rounds < topk
+// stops after the first rounds experts (the gains are then not the selection's).
+__device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, int topk, int rounds, int lane,
                                                 int (&e_out)[kMaxTopk], float (&g_out)[kMaxTopk]) {
   uint64_t key[4];
   float sg[4];
@@ -111,7 +112,7 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
   for (int r = 0; r < kMaxTopk; ++r) {
     e_out[r] = 0;
     sc[r] = 0.0f;
-    if (r < topk) {                                    // uniform
+    if (r < rounds) {                                  // uniform
       uint64_t m = key[0];
 #pragma unroll
       for (int i = 1; i < 4; ++i) m = key[i] > m ? key[i] : m;
@@ -173,7 +174,9 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
       if (wave == 0) {
         int es[kMaxTopk];
         float gs[kMaxTopk];
-        route_topk_wave(rt, b, E, topk, lane, es, gs);
+        // the block's own slot needs the first k + 1 experts; block 0 writes the whole
+        // selection and the gains
+        route_topk_wave(rt, b, E, topk, blk == 0 ? topk : k + 1, lane, es, gs);
         int ek = es[0];
         float gk = gs[0];
 #pragma unroll
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(64) void k_router_topk(Router rt, int E, int topk) 
   const int b = blockIdx.x, lane = threadIdx.x;
   int es[kMaxTopk];
   float gs[kMaxTopk];
-  route_topk_wave(rt, b, E, topk, lane, es, gs);
+  route_topk_wave(rt, b, E, topk, topk, lane, es, gs);
   int ek = es[0];
   float gk = gs[0];
 #pragma unroll
