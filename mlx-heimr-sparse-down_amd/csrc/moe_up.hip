@@ -225,20 +225,22 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   for (int i = 0; i < kUpXIt; ++i) {
     const int t = tid + kUpThreads * i;
     const uint32_t w[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};  // bf16 pairs (x[8t+2c], x[8t+2c+1])
-    auto el = [&](int n) { return (n & 1) ? w[n >> 1] >> 16 : w[n >> 1] & 0xFFFFu; };
     if (t < NW) {
+      // pairs (x[8t+n], x[8t+n+4]): the low or high halves of words n/2 and n/2 + 2, one
+      // v_perm_b32 each
       uint4 pr;
-      pr.x = el(0) | (el(4) << 16);
-      pr.y = el(1) | (el(5) << 16);
-      pr.z = el(2) | (el(6) << 16);
-      pr.w = el(3) | (el(7) << 16);
+      pr.x = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+      pr.y = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+      pr.z = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+      pr.w = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
       // word m of piece j at [m][j]: lanes holding consecutive pieces read consecutive
       // 16-byte words (no LDS bank conflicts)
       *reinterpret_cast<uint4*>(&xp[4 * ((t & 3) * kUpMaxP + (t >> 2))]) = pr;
     }
+    // the word's 8 inputs summed by v_dot2_f32_bf16 against (1.0, 1.0)
     float s8 = 0.0f;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) s8 += bf16_bits_to_f32(el(n));
+    for (int c = 0; c < 4; ++c) s8 = dot2_bf16(w[c], kBfOne2, s8);
     s8 += dpp_f32<0xB1>(s8);  // the 4 words of a piece: quad_perm xor 1, xor 2
     s8 += dpp_f32<0x4E>(s8);
     if (t < NW && (t & 3) == 0) xh[t >> 2] = s8;
