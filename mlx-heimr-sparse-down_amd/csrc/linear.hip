@@ -812,6 +812,154 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   }
 }
 
+// lm_head at one token row (argmax keys, no logits written): k_linear_q4's arithmetic with
+// the weights streamed into LDS instead of registers. A workgroup keeps a ring of three
+// blocks in flight (direct global-to-LDS loads, no registers held), where the register form
+// holds one: 2 workgroups per CU x 3 blocks against 3 x 1 (LDS: 3 x 24 KB + x). Each ring
+// slot holds a block's 16 weight rows (a 16-byte pad after each, so the 16 rows of a read
+// fall in different banks), then its scales and biases, 24 loads of 1 KB (6 per wavefront:
+// every wavefront waits on the same counts). A row's instruction sequence, group order and
+// cross-wavefront sum are k_linear_q4's, so its bf16 logits (and argmax) are bit-identical to
+// that kernel's for any number of token rows.
+constexpr int kRingI = 2688;             // inputs per row the ring is sized for (the hidden size)
+constexpr int kRingChunks = 1536;        // 16-byte chunks per slot: 16 (I/32 + 1) + 2 I/32 <= 1536
+constexpr int kRingPerWave = kRingChunks / 64 / 4;  // 1-KB loads per wavefront and block
+static_assert(16 * (kRingI / 32 + 1) + 2 * (kRingI / 32) <= kRingChunks && kRingChunks % 256 == 0, "ring slot");
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int XK>
+__global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
+  constexpr int IMAX = kRingI, PX = IMAX / 32;
+  constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
+  constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
+  __shared__ __attribute__((aligned(16))) uint4 ring0[kRingChunks];
+  __shared__ __attribute__((aligned(16))) uint4 ring1[kRingChunks];
+  __shared__ __attribute__((aligned(16))) uint4 ring2[kRingChunks];
+  __shared__ __attribute__((aligned(16))) uint32_t xp[16 * PX];
+  __shared__ float xg[PX / 2];
+  __shared__ float wsum[1][4];
+  __shared__ float red[2][4][kQR];                     // [block parity][wavefront][row]
+  const int I = a.I, O = a.O, G = I / 64, NPr = I / 32, rowc = NPr + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, q = lane >> 4;
+  const int nblk = (O + kQR - 1) / kQR;
+  const int nmine = nblk > (int)blockIdx.x ? (nblk - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  // this lane's source of each of its ring loads for block k = 0, and the step to block
+  // k + 1: chunk c = 64 i + lane of a slot takes weight row c / rowc, chunk c % rowc (the pad
+  // chunk re-reads the row's last), then the block's scales, then its biases; chunks past
+  // those re-read the last bias chunk (O % 16 == 0: no row past O)
+  const char* src[kRingPerWave];
+  uint32_t step[kRingPerWave];
+#pragma unroll
+  for (int j = 0; j < kRingPerWave; ++j) {
+    const int c = 64 * (wave + 4 * j) + lane;
+    if (c < 16 * rowc) {
+      const int r = c / rowc, ch = min(c - r * rowc, NPr - 1);
+      src[j] = reinterpret_cast<const char*>(a.w) + (size_t)((int)blockIdx.x * kQR + r) * (I / 2) + 16 * ch;
+      step[j] = gridDim.x * 8u * (uint32_t)I;
+    } else {
+      const int k2 = c - 16 * rowc;
+      const bool isb = k2 >= NPr;
+      src[j] = reinterpret_cast<const char*>(isb ? a.bq : a.s) + (size_t)blockIdx.x * kQR * G * 2 +
+               16 * min(isb ? k2 - NPr : k2, NPr - 1);
+      step[j] = gridDim.x * 32u * (uint32_t)G;
+    }
+  }
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+  // the next block of this workgroup into a slot: 1-KB direct loads (M0 = the LDS address of
+  // the wavefront's 1 KB, one wait state before the load uses it); a block past the last
+  // re-reads the last. The loads are issued by inline assembly so that the ring's reads wait
+  // only on the explicit counts below (the compiler's own count would wait for every load in
+  // flight before any LDS read). M0 holds nothing of the compiler's in this kernel.
+  auto issue = [&](int k, uint4* slot) {
+    const uint32_t base = (uint32_t)(uintptr_t)(lds_void_t*)slot;
+#pragma unroll
+    for (int j = 0; j < kRingPerWave; ++j) {
+      const uint32_t m0 = base + 1024u * (wv + 4u * j);
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src[j])
+                   : "memory");
+      if (k + 1 < nmine) src[j] += step[j];
+    }
+  };
+
+  // ---- prologue: x, the first three blocks, x into LDS
+  XIn<HSD_W_Q4, 1, XK, XIT, PX> xin;
+  xin.load(a, tid);
+  issue(0, ring0);
+  issue(1, ring1);
+  issue(2, ring2);
+  xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
+
+  uint64_t best = 0;
+  // block k from a slot: the wavefront's groups, its partials to LDS, then wavefront 0 adds
+  // the four and keeps the best key; the slot is free after the barrier
+  auto do_block = [&](int k, const uint4* slot, int par) {
+    const int blk = (int)blockIdx.x + k * (int)gridDim.x;
+    const char* sl = reinterpret_cast<const char*>(slot);
+    const uint16_t* ss = reinterpret_cast<const uint16_t*>(sl + 16 * 16 * rowc);
+    const uint16_t* sbb = ss + 8 * NPr;
+    float y = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kGW; ++it) {
+      const int g = wave + 4 * it;
+      if (g < G) {                                     // uniform
+        const int p = 2 * g + (q >> 1);
+        const uint2 w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t qw = i ? w2.y : w2.x;
+          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + i) * PX + p)]);
+          const uint4 wq = make_uint4(((qw << 3) & kNibHi) | kBfOne2, ((qw >> 1) & kNibHi) | kBfOne2,
+                                      ((qw >> 5) & kNibHi) | kBfOne2, ((qw >> 9) & kNibHi) | kBfOne2);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
+                                                        acc, 0, 0, 0);
+        }
+        const float sv_ = bf16_bits_to_f32(ss[n * G + g]), bv_ = bf16_bits_to_f32(sbb[n * G + g]);
+        const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
+        y += fmaf(s16, acc[0], bo * xg[g]);
+      }
+    }
+    if (q == 0) red[par][wave][n] = y;
+    lds_barrier();
+    if (wave == 0) {
+      const int o = blk * kQR + n;
+      const bool live = q == 0 && o < O;
+      const float v = ((red[par][0][n] + red[par][1][n]) + red[par][2][n]) + red[par][3][n];
+      uint64_t key = live ? argmax_key(f32_to_bf16_bits(v), o) : 0;
+      key = row16_max_u64(key);
+      best = key > best ? key : best;
+    }
+  };
+  // waits: a wavefront's ring loads complete in issue order, 6 per block; block k is in when
+  // at most the loads of the blocks issued after it are outstanding
+  auto wait_for = [&](int k) {
+    if (k + 2 < nmine) __builtin_amdgcn_s_waitcnt(0x0F7C);        // vmcnt(12)
+    else if (k + 1 < nmine) __builtin_amdgcn_s_waitcnt(0x0F76);   // vmcnt(6)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
+    lds_barrier();                                                // every wavefront's part in
+  };
+  lds_barrier();                                       // x in LDS
+  for (int k = 0; k < nmine; k += 3) {
+    wait_for(k);
+    do_block(k, ring0, 0);
+    if (k + 3 < nmine) issue(k + 3, ring0);
+    if (k + 1 >= nmine) break;
+    wait_for(k + 1);
+    do_block(k + 1, ring1, 1);
+    if (k + 4 < nmine) issue(k + 4, ring1);
+    if (k + 2 >= nmine) break;
+    wait_for(k + 2);
+    do_block(k + 2, ring2, 0);
+    if (k + 5 < nmine) issue(k + 5, ring2);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);                  // no ring load outlives the workgroup
+  if (wave == 0 && n == 0 && q == 0) {
+    a.keys[blockIdx.x] = best;
+    for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[sl2] = 0;
+  }
+}
+
 // tok[b] = the index of the best key of row b (argmax with NaN first, then the larger
 // value, then the smaller index). One workgroup per row.
 __global__ __launch_bounds__(1024) void k_argmax_keys(const uint64_t* __restrict__ keys, int64_t key_ld,
@@ -973,7 +1121,13 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     case kZR: HSD_Q4_I(NB, HSD_X_GATED_Z, HSD_Y_RESID); break;         \
     default: HSD_Q4_I(NB, HSD_X_BF16, HSD_Y_RESID); break;             \
   }
-  if (mfma) {
+  // one token row of argmax keys with no logits (the decode step's lm_head): the LDS ring
+  const bool ring = mfma && B == 1 && pair == kRA && !y && I <= kRingI && O % kQR == 0;
+  if (ring) {
+    const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS>);
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, 0, kLMaxGrid)));
+    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS>), dim3(g), dim3(kLT), 0, st, a);
+  } else if (mfma) {
     switch (B) {
       case 1: HSD_Q4_P(1); break;
       case 2: HSD_Q4_P(2); break;

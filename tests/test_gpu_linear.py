@@ -125,6 +125,46 @@ def test_many_blocks_matrix_core_path(dev, I):
     assert torch.equal(out.view(torch.int16), (res.float() + yp.float()).to(torch.bfloat16).view(torch.int16))
 
 
+@pytest.mark.parametrize("I,O_", [(2688, 131072), (2688, 33024), (1024, 40960)])
+def test_one_row_argmax_ring(dev, I, O_):
+    """One token row of argmax keys with no logits (the decode step's lm_head) takes the
+    LDS-ring kernel: its token equals the first argmax of the same row's bf16 logits from
+    the register kernel (and of the oracle's), alone and among three rows; equal logits
+    give the smallest index; a NaN logit wins; xn_out equals the three-row call's."""
+    (w, s, b), W = q4_weight(71 + O_, O_, I, dev)
+    rng = np.random.default_rng(72)
+    nwd = S.to_device(O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32)), dev)
+    x, xd = bf16_rows(rng, 3, I, dev, 2.0)
+    slots = nn.argmax_slots(O_)
+    xn3 = torch.empty((3, I), dtype=torch.bfloat16, device=dev)
+    y3 = nn.linear(xd, W, norm=nwd, xn_out=xn3)                      # bf16 logits, 3 rows
+    keys3 = torch.empty((3, slots), dtype=torch.int64, device=dev)
+    nn.linear(xd, W, norm=nwd, argmax_keys=keys3)
+    tok3 = nn.argmax(keys3).cpu().numpy().tolist()
+    want = O.argmax_bf16(y3.float().cpu().numpy()).tolist()
+    assert tok3 == want
+    for r in range(3):
+        keys = torch.full((1, slots), -1, dtype=torch.int64, device=dev)
+        xn1 = torch.empty((1, I), dtype=torch.bfloat16, device=dev)
+        nn.linear(xd[r:r + 1], W, norm=nwd, argmax_keys=keys, xn_out=xn1)
+        assert int(nn.argmax(keys).item()) == want[r], f"row {r}"
+        assert torch.equal(xn1.view(torch.int16), xn3[r:r + 1].view(torch.int16))
+        assert int((keys == -1).sum().item()) == 0                  # every slot written
+    rows = slice(O_ - 1024, O_)
+    ref = O.linear_q4(O.bf16_to_f32(S.to_host(xn3)), w[rows], s[rows], b[rows])
+    assert np.abs(y3[:, rows].float().cpu().numpy() - ref).max() <= 2e-2 + 1e-2 * np.abs(ref).max()
+    # equal rows: the first index wins; a NaN scale in one row: that row wins
+    wt, st, bt = (np.broadcast_to(a[5:6], a.shape).copy() for a in (w, s, b))
+    Wt = nn.QWeight(S.to_device(wt, dev), S.to_device(st, dev), S.to_device(bt, dev))
+    keys = torch.empty((1, slots), dtype=torch.int64, device=dev)
+    nn.linear(xd[:1], Wt, norm=nwd, argmax_keys=keys)
+    assert int(nn.argmax(keys).item()) == 0
+    st[O_ - 3, 1] = 0x7FC0
+    Wt = nn.QWeight(S.to_device(wt, dev), S.to_device(st, dev), S.to_device(bt, dev))
+    nn.linear(xd[:1], Wt, norm=nwd, argmax_keys=keys)
+    assert int(nn.argmax(keys).item()) == O_ - 3
+
+
 def test_residual_epilogue(dev):
     I, O_ = 4096, 2688
     (w, s, b), W = q4_weight(41, O_, I, dev)
