@@ -9,10 +9,12 @@
 // written into the cache at P .. P+B-1; the cache is read only below P, so no kernel reads
 // what this launch writes.
 //
-//   k_attn_part: one workgroup per (kv head, 64-key chunk, 16 of the kv head's query
+//   k_attn_part: one workgroup per (kv head, 32-key chunk, 16 of the kv head's query
 //     heads: all of them in this model), a wavefront per query head, so a chunk's keys and
 //     values are loaded once (4 heads per 256-thread workgroup: the MTP-2 step 1.922
-//     against 1.915 ms, the decode step 1.075 against 1.064). The chunk's keys go to LDS
+//     against 1.915 ms, the decode step 1.075 against 1.064). 32-key chunks halve each
+//     thread's value sum for twice the workgroups and partials (against 64-key ones:
+//     1.907 against 1.915 ms, 1.061 against 1.067). The chunk's keys go to LDS
 //     (rows padded by 16 bytes against bank
 //     conflicts); lane j of wave w scores key j against query head w (a q.k dot in
 //     fp32 with v_dot2_f32_bf16 in four partial sums, times the scale); a wave's max and
@@ -31,7 +33,7 @@ namespace {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHD = 128;        // head dim
-constexpr int kCH = 64;         // keys per chunk
+constexpr int kCH = 32;         // keys per chunk (lanes kCH .. 63 of the scores idle)
 constexpr int kAMaxB = 4;
 constexpr int kHPW = 16;        // query heads per workgroup (one per wavefront)
 constexpr int kAT = 1024;
@@ -40,8 +42,9 @@ constexpr int kHW = kHPW / kAW; // query heads per wavefront in the scores
 constexpr int kTPH = kAT / kHPW;  // threads per head in the value sum
 constexpr int kDPT = 128 / kTPH;  // head dims per thread there
 constexpr int kKP = kHD / 2 + 4;  // padded K row in u32 (272 bytes)
-constexpr int kLI = kCH * 16 / kAT;  // 16-byte K (and V) pieces per thread
-static_assert(kHPW % kAW == 0 && kLI >= 1 && kCH * 16 % kAT == 0, "attention workgroup shape");
+constexpr int kLT = kCH * 16 < kAT ? kCH * 16 : kAT;  // threads loading K and V (16 bytes each)
+constexpr int kLI = kCH * 16 / kLT;  // 16-byte K (and V) pieces per loading thread
+static_assert(kHPW % kAW == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0, "attention workgroup shape");
 constexpr int kRec = kHD + 4;     // partial record: m, l, 2 unused, acc[128] (16-byte aligned)
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -91,7 +94,8 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
     const int piece = tid & 15;
 #pragma unroll
     for (int i = 0; i < kLI; ++i) {
-      const int jl = (tid >> 4) + (kAT / 16) * i, j = j0 + jl;
+      if (tid >= kLT) break;                     // whole wavefronts
+      const int jl = (tid >> 4) + (kLT / 16) * i, j = j0 + jl;
       const bool cached = j < P;
       const int r = min(max(j - P, 0), B - 1);
       const uint16_t* ksrc = cached ? a.kc + ((size_t)g * a.smax + j) * kHD
@@ -124,13 +128,13 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
     uint32_t kr[kHD / 2];
 #pragma unroll
     for (int i = 0; i < kHD / 8; ++i) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&ks[lane][4 * i]);
+      const uint4 v = *reinterpret_cast<const uint4*>(&ks[min(lane, kCH - 1)][4 * i]);
       kr[4 * i] = v.x; kr[4 * i + 1] = v.y; kr[4 * i + 2] = v.z; kr[4 * i + 3] = v.w;
     }
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r) {
       if (r < B) {                               // uniform
-        const bool vis = j <= P + r;
+        const bool vis = lane < kCH && j <= P + r;
 #pragma unroll
         for (int hi = 0; hi < kHW; ++hi) {
           const int h = kHW * wave + hi;
@@ -161,7 +165,7 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
           const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48));
           const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));  // finite: key j0 is visible
           const float p = vis ? __expf(s - M) : 0.0f;
-          ps[r][h][lane] = p;
+          if (lane < kCH) ps[r][h][lane] = p;
           m[r][hi] = M;
           l[r][hi] = wave_sum_dpp(p);
         }
@@ -232,8 +236,8 @@ __global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
   }
 }
 
-constexpr int kMaxCh = 256;      // chunks per row the combine stages in LDS (smax <= 16384)
-constexpr int kPre = 64;         // chunks whose values the combine loads up front (4096 keys)
+constexpr int kMaxCh = 512;      // chunks per row the combine stages in LDS (smax <= 16384)
+constexpr int kPre = 64;         // chunks whose values the combine loads up front (2048 keys)
 
 __global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
   __shared__ float mw[kMaxCh];    // the chunks' maxima, then their weights e^(m - M)
