@@ -14,11 +14,11 @@
 //     values are loaded once (4 heads per 256-thread workgroup: the MTP-2 step 1.922
 //     against 1.915 ms, the decode step 1.075 against 1.064). 32-key chunks halve each
 //     thread's value sum for twice the workgroups and partials (against 64-key ones:
-//     1.907 against 1.915 ms, 1.061 against 1.067). The chunk's keys go to LDS
-//     (rows padded by 16 bytes against bank
-//     conflicts); lane j of wave w scores key j against query head w (a q.k dot in
-//     fp32 with v_dot2_f32_bf16 in four partial sums, times the scale); a wave's max and
-//     sum over its 64 keys (DPP); then p = exp(s - m) times V (LDS) into acc[128] (even and
+//     1.907 against 1.915 ms, 1.061 against 1.067; 16-key ones: 1.997 and 1.085, the
+//     combine then past its up-front loads). The chunk's keys go to LDS
+//     (rows padded by 16 bytes against bank conflicts); lane j of wave w scores key j
+//     against query head w (a q.k dot in fp32 with v_dot2_f32_bf16 in four partial sums,
+//     times the scale); a wave's max and sum over the chunk's keys (DPP); then p = exp(s - m) times V (LDS) into acc[128] (even and
 //     odd keys in separate sums). Writes the chunk's (m, l, acc) per row and head.
 //   k_attn_combine: one workgroup per (row, query head): the chunks of keys 0 .. P+r in
 //     chunk order: M = max m, L = sum l e^(m-M), o = sum acc e^(m-M) / L, rounded to bf16.
