@@ -238,7 +238,7 @@ int hsd_argmax_keys(const uint64_t* argmax_keys, int64_t key_ld, int64_t slots, 
  *   out [B, HQ * HD] bf16: softmax(scale q k^T over keys 0 .. P+r) v per query head;
  *   query head h reads kv head h / (HQ / HKV).
  * P + B > smax: the call writes zeros and sets HSD_STATUS_BAD_STATE. Requirements:
- * HD == 128, (HQ / HKV) % 16 == 0, smax % 32 == 0, smax <= 16384. A row's arithmetic does not depend on
+ * HD == 128, (HQ / HKV) % 4 == 0, smax % 32 == 0, smax <= 16384. A row's arithmetic does not depend on
  * B. workspace: hsd_attn_workspace_bytes(B, HQ, smax). */
 size_t hsd_attn_workspace_bytes(int64_t B, int64_t HQ, int64_t smax);
 int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, uint16_t* k_cache,

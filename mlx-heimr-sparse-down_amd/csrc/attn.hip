@@ -10,7 +10,7 @@
 // what this launch writes.
 //
 //   k_attn_part: one workgroup per (kv head, 32-key chunk, 16 of the kv head's query
-//     heads: all of them in this model), a wavefront per query head, so a chunk's keys and
+//     heads: all of them in this model; 8 or 4 for other ratios), a wavefront per query head, so a chunk's keys and
 //     values are loaded once (4 heads per 256-thread workgroup: the MTP-2 step 1.922
 //     against 1.915 ms, the decode step 1.075 against 1.064). 32-key chunks halve each
 //     thread's value sum for twice the workgroups and partials (against 64-key ones:
@@ -36,16 +36,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kHD = 128;        // head dim
 constexpr int kCH = 32;         // keys per chunk (lanes kCH .. 63 of the scores idle)
 constexpr int kAMaxB = 4;
-constexpr int kHPW = 16;        // query heads per workgroup (one per wavefront)
-constexpr int kAT = 1024;
-constexpr int kAW = kAT / 64;   // wavefronts per workgroup
-constexpr int kHW = kHPW / kAW; // query heads per wavefront in the scores
-constexpr int kTPH = kAT / kHPW;  // threads per head in the value sum
-constexpr int kDPT = 128 / kTPH;  // head dims per thread there
 constexpr int kKP = kHD / 2 + 4;  // padded K row in u32 (272 bytes)
-constexpr int kLT = kCH * 16 < kAT ? kCH * 16 : kAT;  // threads loading K and V (16 bytes each)
-constexpr int kLI = kCH * 16 / kLT;  // 16-byte K (and V) pieces per loading thread
-static_assert(kHPW % kAW == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0, "attention workgroup shape");
+constexpr int kMaxHPW = 16;      // query heads per workgroup: 16, or 8 or 4 for other GQA ratios
 constexpr int kRec = kHD + 4;     // partial record: m, l, 2 unused, acc[128] (16-byte aligned)
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -67,7 +59,17 @@ struct AttnArgs {
   float scale;
 };
 
-__global__ __launch_bounds__(kAT) void k_attn_part(AttnArgs a) {
+template <int kHPW>  // query heads per workgroup, one wavefront each
+__global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
+  constexpr int kAT = 64 * kHPW;
+  constexpr int kAW = kAT / 64;     // wavefronts per workgroup
+  constexpr int kHW = kHPW / kAW;   // query heads per wavefront in the scores
+  constexpr int kTPH = kAT / kHPW;  // threads per head in the value sum
+  constexpr int kDPT = 128 / kTPH;  // head dims per thread there
+  constexpr int kLT = kCH * 16 < kAT ? kCH * 16 : kAT;  // threads loading K and V (16 bytes each)
+  constexpr int kLI = kCH * 16 / kLT;  // 16-byte K (and V) pieces per loading thread
+  static_assert(kHPW % kAW == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0 && kHPW <= kMaxHPW,
+                "attention workgroup shape");
   __shared__ __attribute__((aligned(16))) uint32_t ks[kCH][kKP];
   __shared__ __attribute__((aligned(16))) uint32_t vs[kCH][kHD / 2];
   __shared__ __attribute__((aligned(16))) uint32_t qs[kAMaxB][kHPW][kHD / 2];
@@ -326,8 +328,12 @@ extern "C" int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, u
   if (!qkv || !k_cache || !v_cache || !pos || !out) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
   if (HD != kHD) return set_error(HSD_ERR_SHAPE, "%s: head_dim must be %d", fn, kHD);
   if (B < 1 || B > kAMaxB) return set_error(HSD_ERR_SHAPE, "%s: B must be in [1, %d]", fn, kAMaxB);
-  if (HKV <= 0 || HQ <= 0 || HQ % HKV || (HQ / HKV) % kHPW)
-    return set_error(HSD_ERR_SHAPE, "%s: query heads per kv head must be a multiple of %d", fn, kHPW);
+  if (HKV <= 0 || HQ <= 0 || HQ % HKV || (HQ / HKV) % 4)
+    return set_error(HSD_ERR_SHAPE, "%s: query heads per kv head must be a multiple of 4", fn);
+  // heads per workgroup: all 16 of a kv head where the ratio allows (each chunk's keys and
+  // values loaded once), else 8 or 4
+  const int ratio = (int)(HQ / HKV);
+  const int hpw = ratio % 16 == 0 ? 16 : ratio % 8 == 0 ? 8 : 4;
   if (smax <= 0 || smax % kCH || smax > kCH * kMaxCh)
     return set_error(HSD_ERR_SHAPE, "%s: the cache length must be a multiple of %d and at most %d", fn, kCH,
                      kCH * kMaxCh);
@@ -341,9 +347,14 @@ extern "C" int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, u
   AttnArgs a{qkv, qkv_ld, k_cache, v_cache, smax, pos, reinterpret_cast<float*>(workspace), out, out_ld,
              dev_status, (int)B, (int)HQ, (int)HKV, nch, scale};
   hipStream_t st = as_stream(stream);
-  const int64_t nwg = HKV * nch * (HQ / HKV / kHPW);
+  const int64_t nwg = HKV * nch * (ratio / hpw);
   if (nwg > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
-  hipLaunchKernelGGL(k_attn_part, dim3((unsigned)nwg), dim3(kAT), 0, st, a);
+  if (hpw == 16)
+    hipLaunchKernelGGL(k_attn_part<16>, dim3((unsigned)nwg), dim3(64 * 16), 0, st, a);
+  else if (hpw == 8)
+    hipLaunchKernelGGL(k_attn_part<8>, dim3((unsigned)nwg), dim3(64 * 8), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_attn_part<4>, dim3((unsigned)nwg), dim3(64 * 4), 0, st, a);
   int rc = check_launch(fn);
   if (rc) return rc;
   hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)(B * HQ)), dim3(kHD), 0, st, a);

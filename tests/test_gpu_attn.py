@@ -21,27 +21,27 @@ QKV = (HQ + 2 * HKV) * HD
 SCALE = 1.0 / math.sqrt(HD)
 
 
-def setup(dev, seed, P, B, smax=SMAX):
+def setup(dev, seed, P, B, smax=SMAX, hkv=HKV):
     rng = np.random.default_rng(seed)
-    cache = nn.KVCache(HKV, smax, dev)
-    kc = O.f32_to_bf16(rng.standard_normal((HKV, smax, HD)).astype(np.float32))
-    vc = O.f32_to_bf16(rng.standard_normal((HKV, smax, HD)).astype(np.float32))
+    cache = nn.KVCache(hkv, smax, dev)
+    kc = O.f32_to_bf16(rng.standard_normal((hkv, smax, HD)).astype(np.float32))
+    vc = O.f32_to_bf16(rng.standard_normal((hkv, smax, HD)).astype(np.float32))
     cache.k.copy_(S.to_device(kc, dev))
     cache.v.copy_(S.to_device(vc, dev))
-    qkv = O.f32_to_bf16(rng.standard_normal((B, QKV)).astype(np.float32) * 2)
+    qkv = O.f32_to_bf16(rng.standard_normal((B, (HQ + 2 * hkv) * HD)).astype(np.float32) * 2)
     pos = torch.tensor([P], dtype=torch.int32, device=dev)
     return cache, kc, vc, qkv, pos
 
 
-def oracle_rows(kc, vc, qkv, P):
+def oracle_rows(kc, vc, qkv, P, hkv=HKV):
     B = qkv.shape[0]
     k = O.bf16_to_f32(kc).copy()
     v = O.bf16_to_f32(vc).copy()
     q = O.bf16_to_f32(qkv)
     out = np.zeros((B, HQ * HD))
     for r in range(B):
-        k[:, P + r] = q[r, HQ * HD:(HQ + HKV) * HD].reshape(HKV, HD)
-        v[:, P + r] = q[r, (HQ + HKV) * HD:].reshape(HKV, HD)
+        k[:, P + r] = q[r, HQ * HD:(HQ + hkv) * HD].reshape(hkv, HD)
+        v[:, P + r] = q[r, (HQ + hkv) * HD:].reshape(hkv, HD)
         out[r] = O.attention(q[r, :HQ * HD].reshape(HQ, HD), k[:, :P + r + 1], v[:, :P + r + 1], SCALE).reshape(-1)
     return out, k, v
 
@@ -50,8 +50,8 @@ def oracle_rows(kc, vc, qkv, P):
                                       (2047, 3, SMAX), (2300, 4, SMAX), (4094, 3, 8192),
                                       (5000, 3, 8192), (8190, 2, 8192)])
 def test_attention_matches_oracle(dev, P, B, smax):
-    """Contexts past 4096 keys (more than 64 chunks of 64) take the combine's second
-    load phase; P = 4094, B = 3 puts the third row's last key in chunk 64."""
+    """Contexts past 2048 keys (more than 64 chunks of 32) take the combine's second
+    load phase; P = 4094, B = 3 puts the third row's last key (4096) first in its chunk."""
     cache, kc, vc, qkv, pos = setup(dev, 100 + P + B, P, B, smax)
     out = nn.attention(S.to_device(qkv, dev), cache, pos, n_heads=HQ, n_kv_heads=HKV)
     ref, k, v = oracle_rows(kc, vc, qkv, P)
@@ -76,6 +76,23 @@ def test_verify_rows_equal_single_rows(dev, P, smax):
         assert torch.equal(o1.view(torch.int16), out3[r:r + 1].view(torch.int16)), f"row {r}"
         pos1 += 1
     assert torch.equal(cache1.k.view(torch.int16), cache.k.view(torch.int16))
+
+
+@pytest.mark.parametrize("hkv", [4, 8])
+def test_other_head_ratios(dev, hkv):
+    """8 and 4 query heads per kv head (the workgroups then hold 8 or 4 heads): against
+    the oracle, and a 3-row call equal to single rows."""
+    P = 1000
+    cache, kc, vc, qkv, pos = setup(dev, 400 + hkv, P, 3, hkv=hkv)
+    qd = S.to_device(qkv, dev)
+    out = nn.attention(qd, cache, pos, n_heads=HQ, n_kv_heads=hkv)
+    ref, _, _ = oracle_rows(kc, vc, qkv, P, hkv=hkv)
+    assert np.all(np.abs(out.float().cpu().numpy() - ref) <= 2e-2 + 1e-2 * np.abs(ref))
+    cache1, _, _, _, pos1 = setup(dev, 400 + hkv, P, 3, hkv=hkv)
+    for r in range(3):
+        o1 = nn.attention(qd[r:r + 1], cache1, pos1, n_heads=HQ, n_kv_heads=hkv)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
+        pos1 += 1
 
 
 def test_full_cache_is_refused_on_device(dev):
