@@ -16,9 +16,11 @@
 //     thread's value sum for twice the workgroups and partials (against 64-key ones:
 //     1.907 against 1.915 ms, 1.061 against 1.067; 16-key ones: 1.997 and 1.085, the
 //     combine then past its up-front loads). The chunk's keys go to LDS
-//     (rows padded by 16 bytes against bank conflicts); lane j of wave w scores key j
-//     against query head w (a q.k dot in fp32 with v_dot2_f32_bf16 in four partial sums,
-//     times the scale); a wave's max and sum over the chunk's keys (DPP); then
+//     (rows padded by 16 bytes against bank conflicts); lane 32 u + j of wave w scores
+//     key j against query head w + u HPW/2 (a q.k dot in fp32 with v_dot2_f32_bf16 in four
+//     partial sums, times the scale), so half the wavefronts score (one head per
+//     wavefront, lanes 32-63 idle: the MTP-2 step 1.913 against 1.901 ms); a
+//     half-wavefront's max and sum over the chunk's keys (DPP); then
 //     p = exp(s - m) times V (LDS) into acc[128] (even and odd keys in separate sums).
 //     Writes the chunk's (m, l, acc) per row and head.
 //   k_attn_combine: one workgroup per (row, query head): the chunks of keys 0 .. P+r in
@@ -63,12 +65,11 @@ template <int kHPW>  // query heads per workgroup, one wavefront each
 __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
   constexpr int kAT = 64 * kHPW;
   constexpr int kAW = kAT / 64;     // wavefronts per workgroup
-  constexpr int kHW = kHPW / kAW;   // query heads per wavefront in the scores
   constexpr int kTPH = kAT / kHPW;  // threads per head in the value sum
   constexpr int kDPT = 128 / kTPH;  // head dims per thread there
   constexpr int kLT = kCH * 16 < kAT ? kCH * 16 : kAT;  // threads loading K and V (16 bytes each)
   constexpr int kLI = kCH * 16 / kLT;  // 16-byte K (and V) pieces per loading thread
-  static_assert(kHPW % kAW == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0 && kHPW <= kMaxHPW,
+  static_assert(kHPW == kAW && kHPW % 2 == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0 && kHPW <= kMaxHPW,
                 "attention workgroup shape");
   __shared__ __attribute__((aligned(16))) uint32_t ks[kCH][kKP];
   __shared__ __attribute__((aligned(16))) uint32_t vs[kCH][kHD / 2];
@@ -124,54 +125,65 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- scores: lane = key j, wave w = heads kHW w .. kHW w + kHW - 1
-  const int j = j0 + lane;
-  float m[kAMaxB][kHW], l[kAMaxB][kHW];
-  {
+  // ---- scores: a half-wavefront per query head, lane 32 u + j on key j; wavefront w <
+  // kSW takes heads w and w + kSW (the other wavefronts wait at the barrier)
+  constexpr int kSW = kHPW / 2;                        // wavefronts that score
+  static_assert(kCH == 32, "a half-wavefront's 32 lanes are the chunk's keys");
+  const int half = lane >> 5, jk = lane & 31;
+  const int hs = wave + kSW * half;                    // this lane's query head
+  const int j = j0 + jk;
+  float m[kAMaxB], l[kAMaxB];
+  if (wave < kSW) {                                    // uniform
     uint32_t kr[kHD / 2];
 #pragma unroll
     for (int i = 0; i < kHD / 8; ++i) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&ks[min(lane, kCH - 1)][4 * i]);
+      const uint4 v = *reinterpret_cast<const uint4*>(&ks[jk][4 * i]);
       kr[4 * i] = v.x; kr[4 * i + 1] = v.y; kr[4 * i + 2] = v.z; kr[4 * i + 3] = v.w;
     }
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r) {
-      if (r < B) {                               // uniform
-        const bool vis = lane < kCH && j <= P + r;
+      if (r < B) {                                     // uniform
+        const bool vis = j <= P + r;
+        // four partial dot products (16-byte pieces i % 4), so that four dependency chains
+        // of 16 interleave instead of one of 64
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int hi = 0; hi < kHW; ++hi) {
-          const int h = kHW * wave + hi;
-          // four partial dot products (16-byte pieces i % 4), so that four dependency chains
-          // of 16 interleave instead of one of 64
-          float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int i = 0; i < kHD / 8; ++i) {
-            const uint4 qv = *reinterpret_cast<const uint4*>(&qs[r][h][4 * i]);
-            float t = s4[i & 3];
-            t = dot2(qv.x, kr[4 * i], t);
-            t = dot2(qv.y, kr[4 * i + 1], t);
-            t = dot2(qv.z, kr[4 * i + 2], t);
-            t = dot2(qv.w, kr[4 * i + 3], t);
-            s4[i & 3] = t;
-          }
-          float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-          s = vis ? s * a.scale : -INFINITY;
-          // wave max (DPP inside rows, then the four row maxima)
-          float mx = s;
-          mx = fmaxf(mx, dpp_f32<0xB1>(mx));
-          mx = fmaxf(mx, dpp_f32<0x4E>(mx));
-          mx = fmaxf(mx, dpp_f32<0x141>(mx));
-          mx = fmaxf(mx, dpp_f32<0x140>(mx));
-          const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0));
-          const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16));
-          const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32));
-          const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48));
-          const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));  // finite: key j0 is visible
-          const float p = vis ? __expf(s - M) : 0.0f;
-          if (lane < kCH) ps[r][h][lane] = p;
-          m[r][hi] = M;
-          l[r][hi] = wave_sum_dpp(p);
+        for (int i = 0; i < kHD / 8; ++i) {
+          const uint4 qv = *reinterpret_cast<const uint4*>(&qs[r][hs][4 * i]);
+          float t = s4[i & 3];
+          t = dot2(qv.x, kr[4 * i], t);
+          t = dot2(qv.y, kr[4 * i + 1], t);
+          t = dot2(qv.z, kr[4 * i + 2], t);
+          t = dot2(qv.w, kr[4 * i + 3], t);
+          s4[i & 3] = t;
         }
+        float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        s = vis ? s * a.scale : -INFINITY;
+        // the half-wavefront's max: DPP inside rows of 16, then its two row maxima
+        float mx = s;
+        mx = fmaxf(mx, dpp_f32<0xB1>(mx));
+        mx = fmaxf(mx, dpp_f32<0x4E>(mx));
+        mx = fmaxf(mx, dpp_f32<0x141>(mx));
+        mx = fmaxf(mx, dpp_f32<0x140>(mx));
+        const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0));
+        const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16));
+        const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32));
+        const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48));
+        const float M = half ? fmaxf(m2, m3) : fmaxf(m0, m1);  // finite: key j0 is visible
+        const float p = vis ? __expf(s - M) : 0.0f;
+        ps[r][hs][jk] = p;
+        m[r] = M;
+        // the half-wavefront's sum of p: DPP inside rows, then its two row sums
+        float v = p;
+        v += dpp_f32<0xB1>(v);
+        v += dpp_f32<0x4E>(v);
+        v += dpp_f32<0x141>(v);
+        v += dpp_f32<0x140>(v);
+        const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+        const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+        l[r] = half ? r2 + r3 : r0 + r1;
       }
     }
   }
@@ -223,17 +235,14 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
       }
     }
   }
-  // m and l of each (row, head): lane 0 of the wave that computed them
-  if (lane == 0) {
+  // m and l of each (row, head): the first lane of the half-wavefront that computed them
+  if (wave < kSW && jk == 0) {
 #pragma unroll
     for (int r = 0; r < kAMaxB; ++r) {
       if (r < B && j0 <= P + r) {
-#pragma unroll
-        for (int hi = 0; hi < kHW; ++hi) {
-          float* dst = a.part + (((size_t)r * HQ + hq0 + kHW * wave + hi) * a.nch + c) * kRec;
-          dst[0] = m[r][hi];
-          dst[1] = l[r][hi];
-        }
+        float* dst = a.part + (((size_t)r * HQ + hq0 + hs) * a.nch + c) * kRec;
+        dst[0] = m[r];
+        dst[1] = l[r];
       }
     }
   }
