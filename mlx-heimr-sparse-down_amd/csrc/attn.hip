@@ -19,7 +19,7 @@
 //     (rows padded by 16 bytes against bank conflicts); lane 32 u + j of wave w scores
 //     key j against query head w + u HPW/2 (a q.k dot in fp32 with v_dot2_f32_bf16 in four
 //     partial sums, times the scale), so half the wavefronts score (one head per
-//     wavefront, lanes 32-63 idle: the MTP-2 step 1.913 against 1.901 ms); a
+//     wavefront with lanes 32-63 idle had taken 1.913 against 1.901 ms); a
 //     half-wavefront's max and sum over the chunk's keys (DPP); then
 //     p = exp(s - m) times V (LDS) into acc[128] (even and odd keys in separate sums).
 //     Writes the chunk's (m, l, acc) per row and head.
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
   static_assert(kHPW == kAW && kHPW % 2 == 0 && kCH <= 64 && kCH * 16 % kLT == 0 && kLT % 64 == 0 && kHPW <= kMaxHPW,
                 "attention workgroup shape");
   __shared__ __attribute__((aligned(16))) uint32_t ks[kCH][kKP];
-  __shared__ __attribute__((aligned(16))) uint32_t vs[kCH][kHD / 2];
+  __shared__ __attribute__((aligned(16))) float vs[kCH][kHD];     // V in fp32 (converted once)
   __shared__ __attribute__((aligned(16))) uint32_t qs[kAMaxB][kHPW][kHD / 2];
   __shared__ float ps[kAMaxB][kHPW][kCH];
   const int nhalf = a.HQ / a.HKV / kHPW;       // workgroups per (kv head, chunk)
@@ -109,7 +109,17 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
       const uint4 kv = reinterpret_cast<const uint4*>(ksrc)[piece];
       const uint4 vv = reinterpret_cast<const uint4*>(vsrc)[piece];
       *reinterpret_cast<uint4*>(&ks[jl][4 * piece]) = kv;
-      *reinterpret_cast<uint4*>(&vs[jl][4 * piece]) = vv;
+      {
+        const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        float vf[8];
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          vf[2 * c2] = bf16_bits_to_f32(vw[c2] & 0xFFFFu);
+          vf[2 * c2 + 1] = bf16_bits_to_f32(vw[c2] >> 16);
+        }
+        *reinterpret_cast<float4*>(&vs[jl][8 * piece]) = make_float4(vf[0], vf[1], vf[2], vf[3]);
+        *reinterpret_cast<float4*>(&vs[jl][8 * piece + 4]) = make_float4(vf[4], vf[5], vf[6], vf[7]);
+      }
       // the new rows also go to the cache (hh == 0: one writer per position)
       if (!cached && j < P + B && hh == 0) {
         reinterpret_cast<uint4*>(a.kc + ((size_t)g * a.smax + j) * kHD)[piece] = kv;
@@ -204,11 +214,12 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
       float va[kDPT], vb[kDPT];
 #pragma unroll
       for (int e = 0; e < kDPT; e += 2) {
-        const uint32_t wa = vs[jl][d0 / 2 + e / 2], wb = vs[jl + 1][d0 / 2 + e / 2];
-        va[e] = bf16_bits_to_f32(wa & 0xFFFFu);
-        va[e + 1] = bf16_bits_to_f32(wa >> 16);
-        vb[e] = bf16_bits_to_f32(wb & 0xFFFFu);
-        vb[e + 1] = bf16_bits_to_f32(wb >> 16);
+        const float2 fa = *reinterpret_cast<const float2*>(&vs[jl][d0 + e]);
+        const float2 fb = *reinterpret_cast<const float2*>(&vs[jl + 1][d0 + e]);
+        va[e] = fa.x;
+        va[e + 1] = fa.y;
+        vb[e] = fb.x;
+        vb[e + 1] = fb.y;
       }
 #pragma unroll
       for (int r = 0; r < kAMaxB; ++r) {
