@@ -891,10 +891,8 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
   xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
 
   uint64_t best = 0;
-  // block k from a slot: the wavefront's groups, its partials to LDS, then wavefront 0 adds
-  // the four and keeps the best key; the slot is free after the barrier
-  auto do_block = [&](int k, const uint4* slot, int par) {
-    const int blk = (int)blockIdx.x + k * (int)gridDim.x;
+  // block k from a slot: the wavefront's groups, its partial sums into red[k & 1]
+  auto compute = [&](int k, const uint4* slot) {
     const char* sl = reinterpret_cast<const char*>(slot);
     const uint16_t* ss = reinterpret_cast<const uint16_t*>(sl + 16 * 16 * rowc);
     const uint16_t* sbb = ss + 8 * NPr;
@@ -920,38 +918,46 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
         y += fmaf(s16, acc[0], bo * xg[g]);
       }
     }
-    if (q == 0) red[par][wave][n] = y;
-    lds_barrier();
+    if (q == 0) red[k & 1][wave][n] = y;
+  };
+  // after block k's barrier: wavefront 0 adds the four partials of each row and keeps the
+  // best key, while the others go on to block k + 1 (which writes red[(k + 1) & 1])
+  auto epilogue = [&](int k) {
     if (wave == 0) {
-      const int o = blk * kQR + n;
+      const int o = ((int)blockIdx.x + k * (int)gridDim.x) * kQR + n;
       const bool live = q == 0 && o < O;
-      const float v = ((red[par][0][n] + red[par][1][n]) + red[par][2][n]) + red[par][3][n];
+      const float v = ((red[k & 1][0][n] + red[k & 1][1][n]) + red[k & 1][2][n]) + red[k & 1][3][n];
       uint64_t key = live ? argmax_key(f32_to_bf16_bits(v), o) : 0;
       key = row16_max_u64(key);
       best = key > best ? key : best;
     }
   };
-  // waits: a wavefront's ring loads complete in issue order, 6 per block; block k is in when
-  // at most the loads of the blocks issued after it are outstanding
-  auto wait_for = [&](int k) {
-    if (k + 2 < nmine) __builtin_amdgcn_s_waitcnt(0x0F7C);        // vmcnt(12)
-    else if (k + 1 < nmine) __builtin_amdgcn_s_waitcnt(0x0F76);   // vmcnt(6)
-    else __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
-    lds_barrier();                                                // every wavefront's part in
+  // the end of block k: this wavefront's loads of block k + 1 in (a wavefront's ring loads
+  // complete in issue order, 6 per block: at most block k + 2's may be outstanding, when it
+  // was issued), then one barrier: every wavefront's part of block k + 1 is in, the slot of
+  // block k is free and red[k & 1] complete
+  auto end_block = [&](int k) {
+    if (k + 2 <= 2 || k + 2 < nmine) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
+    lds_barrier();
   };
-  lds_barrier();                                       // x in LDS
+  __builtin_amdgcn_s_waitcnt(0x0F7C);                  // vmcnt(12): block 0 in
+  lds_barrier();                                       // x and block 0 in LDS
   for (int k = 0; k < nmine; k += 3) {
-    wait_for(k);
-    do_block(k, ring0, 0);
+    compute(k, ring0);
+    end_block(k);
     if (k + 3 < nmine) issue(k + 3, ring0);
+    epilogue(k);
     if (k + 1 >= nmine) break;
-    wait_for(k + 1);
-    do_block(k + 1, ring1, 1);
+    compute(k + 1, ring1);
+    end_block(k + 1);
     if (k + 4 < nmine) issue(k + 4, ring1);
+    epilogue(k + 1);
     if (k + 2 >= nmine) break;
-    wait_for(k + 2);
-    do_block(k + 2, ring2, 0);
+    compute(k + 2, ring2);
+    end_block(k + 2);
     if (k + 5 < nmine) issue(k + 5, ring2);
+    epilogue(k + 2);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);                  // no ring load outlives the workgroup
   if (wave == 0 && n == 0 && q == 0) {
