@@ -400,7 +400,7 @@ void k_linear(LinArgs a) {
   int blk = blockIdx.x;
   load_block(blk, cur);
   xin.template finish<32>(a, xp, xh, wsum, tid, lane, wave);
-  __syncthreads();
+  lds_barrier();                                       // x in LDS; the weights may still be in flight
 
   // bf16: one 16-byte piece j of a row against the token rows: the partial of each token row
   auto piece_terms = [&](int j, const uint4& qv, float (&t)[NB]) {
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   load_w(blk, cur);
   store_sc(0, blk, sv, bv);
   xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
-  __syncthreads();
+  lds_barrier();                                       // x and scales in LDS; weights may be in flight
 
   uint64_t best = 0;                                   // wavefront 0, lanes of token row l / 16
   const int arow = min(n, NB - 1);                     // the token row of this lane's A operand
