@@ -306,8 +306,9 @@ __global__ __launch_bounds__(kLT, WF == HSD_W_Q4 ? (IMAX == 3072 && NB < 4 ? 3 :
 void k_linear(LinArgs a) {
   using T = WTraits<WF>;
   constexpr bool Q4 = WF == HSD_W_Q4;
-  static_assert(!Q4 || RW == 4, "4-bit weights: 4 rows per wavefront, two per half-wavefront");
+  static_assert(!Q4 || RW == 4 || RW == 2, "4-bit weights: 4 or 2 rows per wavefront, 2 or 1 per half-wavefront");
   constexpr int kRW = RW;
+  constexpr int kRH = Q4 ? RW / 2 : 1;                 // 4-bit: rows per half-wavefront (each lane's)
   constexpr int kIt32 = (IMAX / 32 + 31) / 32;          // 4-bit: pieces per lane and row (max)
   constexpr int kFull = (IMAX / T::kIn) / 64 > 0 ? (IMAX / T::kIn) / 64 : 1;  // full passes (max)
   constexpr int kRP = REM ? (kRW * 63 + 63) / 64 : 1;  // remainder passes (max; none without REM)
@@ -347,8 +348,8 @@ void k_linear(LinArgs a) {
   // ---- weight pieces of a block (rows past O re-read row O-1, pieces past the row re-read
   // its last piece; unused)
   struct BlkQ4 {
-    uint4 q[kIt32][2];
-    uint32_t s[kIt32][2];
+    uint4 q[kIt32][kRH];
+    uint32_t s[kIt32][kRH];
   };
   struct BlkBf {
     uint4 q[kRW][kFull];
@@ -375,8 +376,8 @@ void k_linear(LinArgs a) {
 #pragma unroll
       for (int it = 0; it < kIt32; ++it)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          load_piece(min(r0 + 2 * hw + i, O - 1), min(jl + 32 * it, NPr - 1), bk.q[it][i], bk.s[it][i]);
+        for (int i = 0; i < kRH; ++i)
+          load_piece(min(r0 + kRH * hw + i, O - 1), min(jl + 32 * it, NPr - 1), bk.q[it][i], bk.s[it][i]);
     } else {
 #pragma unroll
       for (int r = 0; r < kRW; ++r) {
@@ -425,10 +426,12 @@ void k_linear(LinArgs a) {
     int ob, orr;
     bool lane_out;
     if constexpr (Q4) {
-      // the lane's pieces of its two rows against every token row, then the 32-lane sums
-      float pq[NB][2];
+      // the lane's pieces of its kRH rows against every token row, then the 32-lane sums
+      float pq[NB][kRH];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) pq[b][0] = pq[b][1] = 0.0f;
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < kRH; ++i) pq[b][i] = 0.0f;
 #pragma unroll
       for (int it = 0; it < kIt32; ++it) {
         if (it < nit32) {                                // uniform
@@ -444,7 +447,7 @@ void k_linear(LinArgs a) {
             xs[b] = xh[b * PX + j];
           }
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
+          for (int i = 0; i < kRH; ++i) {
             const uint32_t qw[4] = {bk.q[it][i].x, bk.q[it][i].y, bk.q[it][i].z, bk.q[it][i].w};
             uint32_t wc[4][4];
 #pragma unroll
@@ -478,7 +481,7 @@ void k_linear(LinArgs a) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kRH; ++i) {
           float v = pq[b][i];
           v += dpp_f32<0xB1>(v);
           v += dpp_f32<0x4E>(v);
@@ -487,12 +490,12 @@ void k_linear(LinArgs a) {
           const uint32_t vb = __float_as_uint(v);
           const auto pv = __builtin_amdgcn_permlane16_swap(vb, vb, false, false);
           const float u = __uint_as_float(pv[0]) + __uint_as_float(pv[1]);
-          outv = jl == 2 * b + i ? u : outv;
+          outv = jl == kRH * b + i ? u : outv;
         }
       }
-      ob = jl >> 1;
-      orr = 2 * hw + (jl & 1);
-      lane_out = jl < 2 * NB;
+      ob = jl / kRH;
+      orr = kRH * hw + jl % kRH;
+      lane_out = jl < kRH * NB;
     } else {
       float pr[NB][kRW];
 #pragma unroll
@@ -566,7 +569,7 @@ void k_linear(LinArgs a) {
         uint64_t kb = 0;
 #pragma unroll
         for (int r = 0; r < kRW; ++r) {
-          const int ln = Q4 ? 32 * (r >> 1) + 2 * b + (r & 1) : b * kRW + r;  // (token row b, row r)
+          const int ln = Q4 ? 32 * (r / kRH) + kRH * b + r % kRH : b * kRW + r;  // (token row b, row r)
           const uint64_t kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), ln) << 32) |
                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, ln);
           kb = kr > kb ? kr : kb;
@@ -1060,6 +1063,13 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
                 kRF = HSD_X_RMS * 8 + HSD_Y_F32, kGR = HSD_X_GATED * 8 + HSD_Y_RESID,
                 kZR = HSD_X_GATED_Z * 8 + HSD_Y_RESID,
                 kBR = HSD_X_BF16 * 8 + HSD_Y_RESID, kBB = HSD_X_BF16 * 8 + HSD_Y_BF16;
+  // one token row of 4-bit rows of 128 pieces with the residual epilogue (out_proj, o_proj)
+  // and fewer 16-row blocks than CUs: 2 rows per wavefront (one per half-wavefront), twice
+  // the workgroups. A row's pieces, their order and its 32-lane sum are those of 4 rows per
+  // wavefront, so its bits do not depend on the choice (the decode step 1.055 -> 1.051 ms;
+  // at three token rows the MTP-2 step was slower, 1.905 against 1.899 ms)
+  const bool rw2 = w_kind == HSD_W_Q4 && !mfma && B == 1 && I == kLSmallQ4 && y_kind == HSD_Y_RESID &&
+                   (O + 15) / 16 < 256;
   const bool ok = w_kind == HSD_W_Q4 ? (pair == kRB || pair == kRA || pair == kRF || pair == kGR ||
                                         pair == kZR || pair == kBR || pair == kBB)
                                      : (pair == kRB || pair == kBB);
@@ -1071,16 +1081,20 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     constexpr bool REM = !(WF == HSD_W_Q4 && IM == kLSmallQ4);                                        \
     const void* kf = reinterpret_cast<const void*>(&k_linear<WF, NB, XK, YK, IM, RW, REM>);          \
     const size_t ldsx = WF == HSD_W_Q4 ? (size_t)B * 17 * (IM / 32) * 4 : lds;                        \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));         \
+    const int gr = RW == 2 ? std::min((int)((O + 7) / 8), kLMaxGrid) : grid;                          \
+    const int g = std::max(1, std::min(gr, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));           \
     hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), ldsx, st, a);     \
   }
-#define HSD_LIN(WF, NB, XK, YK, IM)                      \
-  {                                                      \
-    if constexpr (WF == HSD_W_Q4) {                      \
-      HSD_LIN_R(WF, NB, XK, YK, IM, 4)                   \
-    } else {                                             \
-      HSD_LIN_R(WF, NB, XK, YK, IM, 1)                   \
-    }                                                    \
+#define HSD_LIN(WF, NB, XK, YK, IM)                                   \
+  {                                                                   \
+    if constexpr (WF == HSD_W_Q4 && NB == 1 && IM == kLSmallQ4 && YK == HSD_Y_RESID) { \
+      if (rw2) HSD_LIN_R(WF, NB, XK, YK, IM, 2)                       \
+      else HSD_LIN_R(WF, NB, XK, YK, IM, 4)                           \
+    } else if constexpr (WF == HSD_W_Q4) {                            \
+      HSD_LIN_R(WF, NB, XK, YK, IM, 4)                                \
+    } else {                                                          \
+      HSD_LIN_R(WF, NB, XK, YK, IM, 1)                                \
+    }                                                                 \
   }
 #define HSD_LIN_I(WF, NB, XK, YK)                          \
   if (isz == 0) HSD_LIN(WF, NB, XK, YK, 3072)              \

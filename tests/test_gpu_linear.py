@@ -178,6 +178,11 @@ def test_residual_epilogue(dev):
     nn.linear(xd, W, residual=out, out=out)                              # in place, as the model does
     want = (res.float() + y.float()).to(torch.bfloat16)
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    # one token row takes 2 rows per wavefront at this shape, three rows 4: the same bits
+    for r in range(3):
+        o1 = res[r:r + 1].clone()
+        nn.linear(xd[r:r + 1], W, residual=o1, out=o1)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
 
 
 def test_gated_norm_prologue(dev):
