@@ -1063,13 +1063,15 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
                 kRF = HSD_X_RMS * 8 + HSD_Y_F32, kGR = HSD_X_GATED * 8 + HSD_Y_RESID,
                 kZR = HSD_X_GATED_Z * 8 + HSD_Y_RESID,
                 kBR = HSD_X_BF16 * 8 + HSD_Y_RESID, kBB = HSD_X_BF16 * 8 + HSD_Y_BF16;
-  // one token row of 4-bit rows of 128 pieces with the residual epilogue (out_proj, o_proj)
-  // and fewer 16-row blocks than CUs: 2 rows per wavefront (one per half-wavefront), twice
-  // the workgroups. A row's pieces, their order and its 32-lane sum are those of 4 rows per
-  // wavefront, so its bits do not depend on the choice (the decode step 1.055 -> 1.051 ms;
-  // at three token rows the MTP-2 step was slower, 1.905 against 1.899 ms)
-  const bool rw2 = w_kind == HSD_W_Q4 && !mfma && B == 1 && I == kLSmallQ4 && y_kind == HSD_Y_RESID &&
-                   (O + 15) / 16 < 256;
+  // one token row of a 4-bit projection with a bf16 or residual output and fewer than 512
+  // 16-row blocks (out_proj, o_proj, q|k|v; not in_proj's 644): 2 rows per wavefront (one
+  // per half-wavefront), twice the workgroups. A row's pieces, their order and its 32-lane
+  // sum are those of 4 rows per wavefront, so its bits do not depend on the choice
+  // (out_proj and o_proj: the decode step 1.054 -> 1.050 ms; q|k|v too: the MTP-2 step
+  // 1.894 -> 1.889 ms; in_proj too: the decode step slower, 1.062 against 1.058 ms; at
+  // three token rows the MTP-2 step was slower, 1.905 against 1.899 ms)
+  const bool rw2 = w_kind == HSD_W_Q4 && !mfma && B == 1 && (y_kind == HSD_Y_RESID || y_kind == HSD_Y_BF16) &&
+                   (O + 15) / 16 < 512;
   const bool ok = w_kind == HSD_W_Q4 ? (pair == kRB || pair == kRA || pair == kRF || pair == kGR ||
                                         pair == kZR || pair == kBR || pair == kBB)
                                      : (pair == kRB || pair == kBB);
@@ -1087,7 +1089,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                                   \
   {                                                                   \
-    if constexpr (WF == HSD_W_Q4 && NB == 1 && IM == kLSmallQ4 && YK == HSD_Y_RESID) { \
+    if constexpr (WF == HSD_W_Q4 && NB == 1 && (YK == HSD_Y_RESID || YK == HSD_Y_BF16)) { \
       if (rw2) HSD_LIN_R(WF, NB, XK, YK, IM, 2)                       \
       else HSD_LIN_R(WF, NB, XK, YK, IM, 4)                           \
     } else if constexpr (WF == HSD_W_Q4) {                            \
