@@ -82,6 +82,9 @@ def test_rows_are_independent_and_epilogues_agree(dev):
     assert torch.equal(y3.view(torch.int32), y4[:3].view(torch.int32))
     yb = nn.linear(xd, W, norm=nw)                                      # bf16 epilogue
     assert torch.equal(yb.view(torch.int16), y4.to(torch.bfloat16).view(torch.int16))
+    for r in range(4):                      # one row: 2 rows per wavefront; four rows: 4
+        y1b = nn.linear(xd[r:r + 1], W, norm=nw)
+        assert torch.equal(y1b.view(torch.int16), yb[r:r + 1].view(torch.int16)), f"row {r}"
     # argmax epilogue: the first index of the largest bf16 output, per row
     slots = nn.argmax_slots(O_)
     keys = torch.empty((4, slots), dtype=torch.int64, device=dev)
