@@ -730,6 +730,128 @@ def cpu_baseline_e2e(model, sess, lm_rows=8192):
                                    lm_head=round(t_lm, 4)), **info)
 
 
+def graph_node_counts(model, fn):
+    """Node types of one captured step (a capture of fn() that is counted and dropped,
+    never replayed): {"kernel": launches per step, ...} from hipGraphGetNodes /
+    hipGraphNodeGetType on the HIP runtime torch has loaded."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    g = model._capture(fn, keep_graph=True)
+    raw = ctypes.c_void_p(g.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(raw, None, ctypes.byref(n)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * n.value)()
+    if hip.hipGraphGetNodes(raw, nodes, ctypes.byref(n)) != 0:
+        return None
+    names = {0: "kernel", 1: "memcpy", 2: "memset", 5: "empty"}
+    out = {}
+    for nd in nodes:
+        t = ctypes.c_int(-1)
+        hip.hipGraphNodeGetType(ctypes.c_void_p(nd), ctypes.byref(t))
+        k = names.get(t.value, f"type{t.value}")
+        out[k] = out.get(k, 0) + 1
+    del g
+    return out
+
+
+def empty_launch_us(dev, n, reps=50):
+    """One graph of n back-to-back one-element fills (the launch floor of an n-kernel
+    step, timed like the steps: the graph replayed reps times) -> us per launch."""
+    tiny = torch.zeros(1, device=dev)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        tiny.fill_(0.0)
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                tiny.fill_(float(i))
+    torch.cuda.current_stream(dev).wait_stream(s)
+    ms = time_graphs([g], reps, 5)
+    del g
+    return 1e3 * ms / (reps * n)
+
+
+def _q4(O, I):
+    """Bytes of a 4-bit group-64 projection: nibbles plus bf16 scale and bias per group."""
+    return O * I // 2 + O * (I // 64) * 4
+
+
+def pass_bytes(cfg, B, P, z):
+    """Algorithmic HBM bytes of one pass of B token rows (positions P .. P+B-1) through the
+    52 layers, by block kind: every weight byte the pass needs once, the Mamba states read
+    once and written once per row (the checkpoints), the attention keys and values of the
+    prefix read once and the rows' own written, and the MoE experts the rows select
+    (routed experts: the expected number of distinct ones among B rows' top-k; down
+    projection: live rows x D/2 + live 64-groups x 4D at zero fraction z, the shared
+    expert's rows counted once per live row of any row). Activations between kernels are
+    not counted (they are KB)."""
+    D, H, Pd, Ns, G = cfg.hidden, cfg.mamba_heads, cfg.mamba_head_dim, cfg.ssm_state, cfg.n_groups
+    CD, DI = cfg.conv_dim, cfg.mamba_inner
+    E, k, F, FS = cfg.n_experts, cfg.topk, cfg.moe_inter, cfg.shared_inter
+    state = H * Pd * Ns * 4
+    mamba = (_q4(cfg.in_proj_dim, D) + _q4(D, DI) + 2 * D + 2 * DI + CD * 5 * 2 + 3 * H * 4
+             + state + B * state + 3 * CD * 2 + B * 3 * CD * 2)
+    d = E * (1.0 - (1.0 - k / E) ** B)                          # distinct routed experts
+    up = d * _q4(F, D) + _q4(FS, D)
+    live_g = 1.0 - z ** 64
+    down = (D // 2) * (B * k * F * (1.0 - z) + FS * (1.0 - z ** B)) + 4 * D * live_g * (d * F // 64 + FS // 64)
+    moe = E * D * 2 + 2 * D + E * 4 + up + down
+    kv = cfg.kv_heads * cfg.head_dim * 2
+    attn = _q4(cfg.qkv_dim, D) + _q4(D, cfg.attn_heads * cfg.head_dim) + 2 * D + 2 * kv * P + 2 * kv * B
+    pat = cfg.pattern
+    return dict(mamba=pat.count("M") * mamba, moe=pat.count("E") * moe, attention=pat.count("*") * attn)
+
+
+def step_bytes(cfg, kind, P, z):
+    """Algorithmic bytes of one captured step at cache length P, by part. kind "decode":
+    the embedding row, the 52 layers at one row, lm_head (norm_f fused). kind "mtp": the
+    head's call over the three rows the last verify confirmed (eh_proj, its attention and
+    MoE blocks) and lm_head on the draft row, the chained call at one row with lm_head
+    again, then the 3-row verify through the 52 layers and lm_head at three rows: lm_head's
+    198 MB are read three times, as three dependent passes (each needs the previous one's
+    argmax)."""
+    D, V = cfg.hidden, cfg.vocab
+    lm = _q4(V, D) + 2 * D
+    emb_row = D // 2 + (D // 64) * 4
+    out = {}
+    if kind == "decode":
+        out.update(pass_bytes(cfg, 1, P, z))
+        out["embedding"] = emb_row
+        out["lm_head"] = lm
+    else:
+        p3 = pass_bytes(cfg, 3, P, z)
+        out.update(p3)
+        cfg1 = Mdl.ModelConfig(**{**cfg.__dict__, "pattern": "*E"})
+        h3, h1 = pass_bytes(cfg1, 3, P, z), pass_bytes(cfg1, 1, P, z)
+        eh = 2 * D * D * 2 + 2 * 2 * D
+        out["mtp_head"] = h3["attention"] + h3["moe"] + h1["attention"] + h1["moe"] + 2 * eh
+        out["embedding"] = 7 * emb_row                        # the head's 3 + 1 rows, the verify's 3
+        out["lm_head"] = 3 * lm
+    out["total"] = sum(out.values())
+    return out
+
+
+def e2e_roofline(model, kind, ms_per_step, P, launches, launch_us):
+    z = float(np.mean(model.zero_frac_measured))
+    b = step_bytes(model.cfg, kind, P, z)
+    gbs = b["total"] / (ms_per_step * 1e-3) / 1e9
+    floor_ms = launches * launch_us * 1e-3 if launches else None
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                traffic=None, bytes_per_step=int(b["total"]),
+                bytes_by_part={k: int(v) for k, v in b.items() if k != "total"},
+                ms_per_step=ms_per_step, roof_ms_per_step=round(b["total"] / HBM_PEAK_GBS / 1e9 * 1e3, 4),
+                cache_len=int(P), moe_zero_frac=round(z, 4), launches_per_step=launches,
+                empty_launch_us=round(launch_us, 3),
+                launch_floor_ms=None if floor_ms is None else round(floor_ms, 4),
+                launch_floor_frac_of_step=None if floor_ms is None else round(floor_ms / ms_per_step, 4),
+                note="bytes: every weight byte the step needs once (lm_head once per dependent pass), Mamba "
+                     "states read and checkpoints written, the attention prefix read, the selected experts' "
+                     "up rows and the down projection's live rows and groups; launch floor: the step's kernel "
+                     "launches (graph nodes) x the measured launch time of an empty kernel in a graph")
+
+
 def bench_e2e(args):
     dev = torch.device("cuda:0")
     cfg = Mdl.ModelConfig()
@@ -740,33 +862,46 @@ def bench_e2e(args):
     log(f"[e2e] model: {len(cfg.pattern)} layers + MTP head, {model.nbytes() / 1e9:.2f} GB, built and calibrated "
         f"in {init_s:.1f} s; MoE zero fractions {min(model.zero_frac_measured):.3f}..{max(model.zero_frac_measured):.3f}")
     prompt = np.random.default_rng(args.seed + 11).integers(0, cfg.vocab, args.prompt).astype(np.int32)
-    G, W = args.gen, max(args.warmup, 0)
-    runs = {}
+    T, G, W = len(prompt), args.gen, max(args.warmup, 0)
+    # out_tokens room for the warm-up and timed steps of an MTP run (up to 3 tokens each)
+    cap = max(G, 1 + 3 * (W + max(args.steps, 0))) + 8
+    runs, nodes = {}, {}
+
+    def finish(s, n_to):
+        """Untimed steps after the timed window until n_to tokens are emitted."""
+        while s.emitted() < n_to:
+            s.step(1)
 
     def plain(mode):
         model.set_mode(mode)
-        s = model.session(prompt, cap=G + 8)
+        s = model.session(prompt, cap=cap)
         s.step(W)
         n0 = s.emitted()
-        k = max(G + 4 - n0, 1)
+        k = args.steps if args.steps > 0 else max(G - n0, 1)
         sec = s.step(k)
         n1 = s.emitted()
-        toks = s.tokens(G + 4)
+        finish(s, G)
         r = dict(tok_s=round((n1 - n0) / sec, 2), ms_per_token=round(1e3 * sec / k, 4), steps=k, warmup=W,
-                 prompt_tok_s=round(len(prompt) / s.prompt_s, 1))
-        log(f"[e2e] {mode}: {r['tok_s']:.1f} tok/s decode ({r['ms_per_token']:.3f} ms/token), prefill "
-            f"{r['prompt_tok_s']:.0f} tok/s")
-        return r, toks, s
+                 timed_tokens=[n0, n1], cache_len_mid=T + (n0 + n1) // 2,
+                 generation_tok_s=round((s.emitted() - 1) / s.decode_s, 2), generation_tokens=s.emitted(),
+                 prompt_tok_s=round(T / s.prompt_s, 1))
+        log(f"[e2e] {mode}: {r['tok_s']:.1f} tok/s over tokens {n0}..{n1} ({r['ms_per_token']:.3f} ms/token), "
+            f"{r['generation_tok_s']:.1f} tok/s over the whole generation, prefill {r['prompt_tok_s']:.0f} tok/s")
+        return r, s
 
-    runs["dense"], dense_toks, _ = plain("dense")
-    runs["sparse"], sparse_toks, sess_sparse = plain("sparse")
-    runs["sparse"]["tokens_equal_dense"] = sparse_toks[:G] == dense_toks[:G]
-    cpu = cpu_baseline_e2e(model, sess_sparse) if args.cpu_budget > 0 else None
-    del sess_sparse
+    runs["dense"], s = plain("dense")
+    dense_toks = s.tokens(G)
+    del s
+    runs["sparse"], s = plain("sparse")
+    runs["sparse"]["tokens_equal_dense"] = s.tokens(G) == dense_toks
+    runs["sparse"]["tokens_compared"] = G
+    nodes["decode"] = graph_node_counts(model, s.step_fn)
+    cpu = cpu_baseline_e2e(model, s) if args.cpu_budget > 0 else None
+    del s
     model.set_mode("sparse")
     for name, probs in (("mtp2_prose", (0.2, 0.34, 0.46)), ("mtp2_code", (0.06, 0.2, 0.74))):
         acc = mtp.scripted_accepts(8192, probs, seed=args.seed + 5)
-        s = model.session(prompt, mtp=True, cap=G + 8, script=dense_toks, accepts=acc)
+        s = model.session(prompt, mtp=True, cap=cap, script=dense_toks, accepts=acc)
         s.step(W)
         n0, st0 = s.emitted(), s.state()
         if args.steps > 0:
@@ -779,16 +914,32 @@ def bench_e2e(args):
         sec = s.step(k)
         st1 = s.state()
         n1 = s.emitted()
+        finish(s, G)
         toks = s.tokens(G)
         acc_mean = (st1[N.SEQ_ACC_SUM] - st0[N.SEQ_ACC_SUM]) / k
         runs[name] = dict(tok_s=round((n1 - n0) / sec, 2), ms_per_step=round(1e3 * sec / k, 4), steps=k, warmup=W,
+                          timed_tokens=[n0, n1], cache_len_mid=T + (n0 + n1) // 2,
                           accepted_mean=round(acc_mean, 4), tokens_per_step=round((n1 - n0) / k, 4),
-                          scripted_probs=list(probs), tokens_equal_dense=toks == dense_toks[:G],
-                          prompt_tok_s=round(len(prompt) / s.prompt_s, 1))
-        log(f"[e2e] sparse + MTP-2 ({name}, mean accepted {acc_mean:.2f}): {runs[name]['tok_s']:.1f} tok/s, "
-            f"{runs[name]['ms_per_step']:.3f} ms/step, tokens equal dense: {runs[name]['tokens_equal_dense']}")
+                          scripted_probs=list(probs), tokens_equal_dense=toks == dense_toks, tokens_compared=G,
+                          generation_tok_s=round((s.emitted() - 1) / s.decode_s, 2), generation_tokens=s.emitted(),
+                          generation_steps=s.steps, prompt_tok_s=round(T / s.prompt_s, 1))
+        if "mtp" not in nodes:
+            nodes["mtp"] = graph_node_counts(model, s.step_fn)
+        log(f"[e2e] sparse + MTP-2 ({name}, mean accepted {acc_mean:.2f}): {runs[name]['tok_s']:.1f} tok/s over "
+            f"tokens {n0}..{n1}, {runs[name]['ms_per_step']:.3f} ms/step; {runs[name]['generation_tok_s']:.1f} tok/s "
+            f"over the whole generation; {G} tokens equal dense: {runs[name]['tokens_equal_dense']}")
         del s
+    launch_us = empty_launch_us(dev, max(nodes["mtp"].get("kernel", 1) if nodes.get("mtp") else 200, 1))
     head = runs["mtp2_prose"]
+    e2e_roof = dict(
+        mtp2_step=e2e_roofline(model, "mtp", head["ms_per_step"], head["cache_len_mid"],
+                               (nodes.get("mtp") or {}).get("kernel"), launch_us),
+        decode_step=e2e_roofline(model, "decode", runs["sparse"]["ms_per_token"], runs["sparse"]["cache_len_mid"],
+                                 (nodes.get("decode") or {}).get("kernel"), launch_us))
+    for k_, r_ in e2e_roof.items():
+        log(f"[e2e] roofline {k_}: {r_['bytes_per_step'] / 1e9:.3f} GB per step, {r_['achieved']:.0f} GB/s "
+            f"({r_['frac']:.1%} of HBM); {r_['launches_per_step']} launches x {r_['empty_launch_us']:.2f} us = "
+            f"{r_['launch_floor_ms']} ms launch floor of {r_['ms_per_step']} ms")
     rec = dict(metric=METRIC, value=head["tok_s"], unit="tok/s", n_gpus=1, steps=head["steps"], warmup=W,
                ms_per_step=head["ms_per_step"], higher_is_better=True, scaling="weak", vs_baseline=None,
                dtype="f32 accumulate (4-bit weights, bf16 activations)", data="synthetic",
@@ -796,11 +947,14 @@ def bench_e2e(args):
                                     "128x top-6, 6 GQA 32/2) + 1-layer MTP head, 4-bit g64, vocab 131072; "
                                     "2048-token random prompt, 256 greedy tokens; sparse down + MTP-2, scripted "
                                     "acceptance at mean 1.26/2",
-                           prompt_tokens=len(prompt), gen_tokens=G, layers=len(cfg.pattern), hidden=cfg.hidden,
+                           prompt_tokens=T, gen_tokens=G, layers=len(cfg.pattern), hidden=cfg.hidden,
                            vocab=cfg.vocab, experts=cfg.n_experts, topk=cfg.topk,
                            weights_gb=round(model.nbytes() / 1e9, 2),
-                           moe_zero_frac=round(float(np.mean(model.zero_frac_measured)), 4)),
-               roofline=None, cpu_baseline=cpu, e2e=runs,
+                           moe_zero_frac=round(float(np.mean(model.zero_frac_measured)), 4),
+                           timed=f"{W} untimed warm-up steps, then {head['steps']} timed steps (tokens "
+                                 f"{head['timed_tokens'][0]}..{head['timed_tokens'][1]}); every run is then stepped "
+                                 f"on untimed to {G} tokens, and all {G} are compared with dense decode"),
+               roofline=None, e2e_roofline=e2e_roof, graph_nodes=nodes, cpu_baseline=cpu, e2e=runs,
                all_tokens_equal=all(r.get("tokens_equal_dense", True) for r in runs.values()),
                reference_published={"sparse+MTP2 tok/s, Apple M5 Pro, real checkpoint and text (README.md:19)": 153})
     del model

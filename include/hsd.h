@@ -211,8 +211,8 @@ int hsd_dense_down_decode(const void* h, int h_dtype, const int32_t* sel, const 
  * Instantiated pairs (x_kind, y_kind): 4-bit -- (RMS, BF16), (RMS, F32), (RMS, ARGMAX),
  * (GATED, RESID), (GATED_Z, RESID), (BF16, RESID), (BF16, BF16); bf16 weights -- (RMS,
  * BF16), (BF16, BF16).
- * Requirements: O a multiple of 8 (4-bit) or 4 (bf16); I <= 6144, a multiple of 64 (4-bit)
- * or 8 (bf16), of 512 for the gated norm; x, gate, norm_w, w, xn_out 16-byte aligned with
+ * Requirements: O a multiple of 8 (4-bit) or 4 (bf16); I a multiple of 64 and at most 4096
+ * (4-bit) or a multiple of 8 and at most 6144 (bf16), of 512 for the gated norm; x, gate, norm_w, w, xn_out 16-byte aligned with
  * row strides of whole 16-byte pieces. A token row's arithmetic does not depend on B. */
 int64_t hsd_linear_argmax_slots(int64_t O, int w_kind);
 int hsd_linear(const void* x, int64_t x_ld, int x_kind, const uint16_t* gate, int64_t gate_ld,

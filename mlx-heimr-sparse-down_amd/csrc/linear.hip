@@ -875,14 +875,19 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
   // the wavefront's 1 KB, one wait state before the load uses it); a block past the last
   // re-reads the last. The loads are issued by inline assembly so that the ring's reads wait
   // only on the explicit counts below (the compiler's own count would wait for every load in
-  // flight before any LDS read). M0 holds nothing of the compiler's in this kernel.
+  // flight before any LDS read). M0 is listed as clobbered; it is a reserved register, which
+  // the compiler only sets right before its own M0 users, and this kernel's generated code
+  // has none besides these loads (checked in its gfx950 assembly).
   auto issue = [&](int k, uint4* slot) {
     const uint32_t base = (uint32_t)(uintptr_t)(lds_void_t*)slot;
 #pragma unroll
     for (int j = 0; j < kRingPerWave; ++j) {
       const uint32_t m0 = base + 1024u * (wv + 4u * j);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src[j])
-                   : "memory");
+                   : "memory", "m0");
+#pragma clang diagnostic pop
       if (k + 1 < nmine) src[j] += step[j];
     }
   };
@@ -1024,9 +1029,12 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (B < 0 || B > kLMaxB) return set_error(HSD_ERR_SHAPE, "%s: B must be in [0, %d]", fn, kLMaxB);
   if (O <= 0 || O % rows || O > (1 << 28))
     return set_error(HSD_ERR_SHAPE, "%s: O must be a positive multiple of %d", fn, rows);
-  if (I <= 0 || I > kLMaxI || I % (w_kind == HSD_W_Q4 ? 64 : 8))
+  // 4-bit rows up to 4096 inputs (every 4-bit projection of the model; the register arrays
+  // of longer rows spill), bf16 rows up to 6144 (the MTP head's eh_proj: 5376)
+  const int imax = w_kind == HSD_W_Q4 ? kLSmallQ4 : kLMaxI;
+  if (I <= 0 || I > imax || I % (w_kind == HSD_W_Q4 ? 64 : 8))
     return set_error(HSD_ERR_SHAPE, "%s: I must be a multiple of %d and at most %d", fn,
-                     w_kind == HSD_W_Q4 ? 64 : 8, kLMaxI);
+                     w_kind == HSD_W_Q4 ? 64 : 8, imax);
   const bool gated = x_kind == HSD_X_GATED || x_kind == HSD_X_GATED_Z;
   if (gated && I % 512) return set_error(HSD_ERR_SHAPE, "%s: the gated norm needs I %% 512 == 0", fn);
   if (x_kind == HSD_X_GATED_Z && x_ld < I + I / 16)
@@ -1053,9 +1061,10 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (mfma && (((uintptr_t)scales & 15u) || ((uintptr_t)biases & 15u)))
     return set_error(HSD_ERR_ALIGN, "%s: scales and biases must be 16-byte aligned", fn);
   hipStream_t st = as_stream(stream);
-  // IMAX 3072 (pieces left over after full passes: dealt as pairs), 4096 for 4-bit rows of
-  // exactly 128 pieces (no pairs), the maximum otherwise
-  const int isz = I <= 3072 ? 0 : (w_kind == HSD_W_Q4 && I == kLSmallQ4) ? 1 : 2;
+  // IMAX 3072, then 4096 for 4-bit rows and 6144 for bf16 rows (bf16: pieces left over
+  // after full passes dealt as pairs). A 4-bit row's pieces, their order and its sums do not
+  // depend on IMAX.
+  const int isz = I <= 3072 ? 0 : 1;
   const int grid = slots;
   // the (x_kind, y_kind) pairs this library instantiates
   const int pair = x_kind * 8 + y_kind;
@@ -1098,9 +1107,9 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
       HSD_LIN_R(WF, NB, XK, YK, IM, 1)                                \
     }                                                                 \
   }
-#define HSD_LIN_I(WF, NB, XK, YK)                          \
-  if (isz == 0) HSD_LIN(WF, NB, XK, YK, 3072)              \
-  else if (WF == HSD_W_Q4 && isz == 1) HSD_LIN(WF, NB, XK, YK, kLSmallQ4) \
+#define HSD_LIN_I(WF, NB, XK, YK)                                       \
+  if (isz == 0) HSD_LIN(WF, NB, XK, YK, 3072)                           \
+  else if constexpr (WF == HSD_W_Q4) HSD_LIN(WF, NB, XK, YK, kLSmallQ4) \
   else HSD_LIN(WF, NB, XK, YK, kLMaxI)
 #define HSD_LIN_P(WF, NB)                                                  \
   switch (pair) {                                                          \
@@ -1133,8 +1142,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   }
 #define HSD_Q4_I(NB, XK, YK)                                    \
   if (I <= 3072) HSD_Q4_R(NB, XK, YK, 3072)                     \
-  else if (I <= kLSmallQ4) HSD_Q4_R(NB, XK, YK, kLSmallQ4)      \
-  else HSD_Q4_R(NB, XK, YK, kLMaxI)
+  else HSD_Q4_R(NB, XK, YK, kLSmallQ4)
 #define HSD_Q4_P(NB)                                                   \
   switch (pair) {                                                      \
     case kRB: HSD_Q4_I(NB, HSD_X_RMS, HSD_Y_BF16); break;              \

@@ -35,7 +35,8 @@ def sparse_down(h, sel, gains, pw, ps, pb, spw, sps, spb, *, F, FS, D, topk,
     sps/spb [FS/64, D] (hsd.layout.to_neuron_major).
 
     sl / unr / nds are the reference's Metal tuning knobs; the HIP kernel's geometry is
-    fixed (128-output chunks x 16-group parts), so they are accepted and ignored.
+    fixed (128-output chunks x 8-group parts, 32 parts per token row at the reference
+    shape), so they are accepted and ignored.
     dense=True: the dense-h control -- the same kernel reading every row (bit-identical
     result for finite inputs). live_masks: optional [B, topk*F/64 + FS/64] int64 tensor
     that receives the canonical live mask of every 64-group. status: optional int32 [1]

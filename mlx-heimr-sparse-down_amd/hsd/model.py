@@ -139,13 +139,13 @@ class MambaBlock:
                                    n_groups=cfg.n_groups, norm_group=cfg.mamba_inner // cfg.n_groups, eps=cfg.eps)
         self.eps = cfg.eps
 
-    def rows(self, x, buf, cache: M.MambaCache):
-        """x [B, D] (updated in place)."""
+    def rows(self, x, buf, cache: M.MambaCache, status=None):
+        """x [B, D] (updated in place). status: optional device int32 [1] (HSD_STATUS_*)."""
         B = x.shape[0]
         proj = nn.linear(x, self.in_proj, norm=self.norm_w, eps=self.eps, out=buf["proj"][:B])
         # the gate applied in the SSM kernel, which also leaves each 16 channels' sum of z^2
         # for out_proj's gated norm (no silu, no gate loads in its prologue)
-        z = M.ssm_rows(self.mixer, proj, cache, out=buf["y_pre"][:B], gated=True)
+        z = M.ssm_rows(self.mixer, proj, cache, out=buf["y_pre"][:B], gated=True, status=status)
         nn.linear(z, self.out_proj, norm=self.mixer.norm_w, eps=self.eps, gated_z=True, residual=x, out=x)
         return x
 
@@ -168,12 +168,12 @@ class AttnBlock:
         _zero_output_row0(w, s, b)
         self.o_proj = nn.QWeight(w, s, b)
 
-    def rows(self, x, buf, kv: nn.KVCache, pos):
+    def rows(self, x, buf, kv: nn.KVCache, pos, status=None):
         B = x.shape[0]
         c = self.cfg
         qkv = nn.linear(x, self.qkv, norm=self.norm_w, eps=c.eps, out=buf["qkv"][:B])
         o = nn.attention(qkv, kv, pos, n_heads=c.attn_heads, n_kv_heads=c.kv_heads, head_dim=c.head_dim,
-                         out=buf["att"][:B], workspace=buf["ws_attn"])
+                         out=buf["att"][:B], workspace=buf["ws_attn"], status=status)
         nn.linear(o, self.o_proj, residual=x, out=x)
         return x
 
@@ -218,7 +218,7 @@ class MoEBlock:
         self.spw, self.sps, self.spb = layout.to_neuron_major(sw, ss, sb)
         del w, s, b, sw, ss, sb
 
-    def rows(self, x, buf, dense=False):
+    def rows(self, x, buf, dense=False, status=None):
         B = x.shape[0]
         c = self.cfg
         xn = buf["xn"][:B]
@@ -244,7 +244,7 @@ class MoEBlock:
         N.call("hsd_sparse_down_residual", N.ptr(hcat), N.DT_BF16, N.ptr(sel), N.ptr(gains),
                N.ptr(N.as_words(self.pw)), N.ptr(self.ps), N.ptr(self.pb), N.ptr(N.as_words(self.spw)),
                N.ptr(self.sps), N.ptr(self.spb), N.ptr(x), N.ptr(x), B, c.hidden, c.moe_inter, c.shared_inter, c.topk,
-               c.n_experts, 1 if dense else 0, None, None, N.ptr(ws), ws.numel(), N.stream(x.device))
+               c.n_experts, 1 if dense else 0, None, N.ptr(status), N.ptr(ws), ws.numel(), N.stream(x.device))
         return x
 
     # ---- the reference's per-block call surface (model.py:110-175) on fresh buffers: any
@@ -357,6 +357,9 @@ class ModelCache:
     def __init__(self, model: "NemotronModel", cap=4096):
         c, dev = model.cfg, model.device
         self.seq = torch.zeros(N.SEQ_LEN, dtype=torch.int32, device=dev)
+        # HSD_STATUS_* bits the kernels OR in (an attention cache overflow, a corrupt ring
+        # index, a token or expert id out of range); checked after every prefill and step
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.cur = self.seq[N.SEQ_CUR:N.SEQ_CUR + 1]
         self.pos = self.seq[N.SEQ_POS:N.SEQ_POS + 1]
         self.head_pos = self.seq[N.SEQ_HEAD_POS:N.SEQ_HEAD_POS + 1]
@@ -375,6 +378,16 @@ class ModelCache:
 
     def state(self):
         return self.seq.cpu().tolist()
+
+    def check_status(self, where):
+        """Raises HSDError when a kernel has flagged this cache's status word (reads one
+        int back: call it after a synchronise, not inside a captured step)."""
+        st = int(self.status.item())
+        if st:
+            why = [n for bit, n in ((N.STATUS_BAD_EXPERT, "an expert id out of range"),
+                                    (N.STATUS_BAD_STATE, "an attention cache overflow or a corrupt Mamba ring index"),
+                                    (N.STATUS_BAD_TOKEN, "a token id out of range")) if st & bit]
+            raise N.HSDError(f"{where}: device status {st} ({'; '.join(why)})")
 
 
 # ------------------------------------------------------------------ the model
@@ -496,20 +509,21 @@ class NemotronModel:
         self.mode = mode
 
     # ---- pieces shared with the MTP head (model.py:222-230)
-    def embed(self, ids, out=None):
-        return nn.embed(ids, self.embedding, out=out)
+    def embed(self, ids, out=None, status=None):
+        return nn.embed(ids, self.embedding, out=out, status=status)
 
     # ---- the stack
     def layers(self, x, buf, cache: ModelCache):
         """x [B, D] through every block in place; rows at positions POS .. POS+B-1."""
         dense = self.mode == "dense"
+        st = cache.status
         for t, blk, lc in zip(self.cfg.pattern, self.blocks, cache.layers):
             if t == "M":
-                blk.rows(x, buf, lc)
+                blk.rows(x, buf, lc, status=st)
             elif t == "*":
-                blk.rows(x, buf, lc, cache.pos)
+                blk.rows(x, buf, lc, cache.pos, status=st)
             else:
-                blk.rows(x, buf, dense=dense)
+                blk.rows(x, buf, dense=dense, status=st)
         return x
 
     def head_keys(self, x, buf, keys, norm=None):
@@ -526,18 +540,18 @@ class NemotronModel:
         return out
 
     # ---- the MTP head forward (mtp.py:74-88)
-    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None):
+    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None, status=None):
         """Head rows: h [B, D] (the target's pre-norm hidden), toks [B] int32 (the token
         after each row's position) at positions pos .. pos+B-1 of the head's KV cache kv.
         Leaves the normed hidden rows in buf["hn"] and (with keys) the argmax keys of the
         head's logits."""
         B = h.shape[0]
         hd, c = self.mtp, self.cfg
-        e = self.embed(toks, out=buf["emb"][:B])
+        e = self.embed(toks, out=buf["emb"][:B], status=status)
         pair = nn.pair_norm(e, h, hd.enorm, hd.hnorm, eps=c.eps, out=buf["pair"][:B])
         x = nn.linear(pair, hd.eh_proj, out=buf["hx"][:B])
-        hd.attn.rows(x, buf, kv, pos)
-        hd.moe.rows(x, buf, dense=self.mode == "dense")
+        hd.attn.rows(x, buf, kv, pos, status=status)
+        hd.moe.rows(x, buf, dense=self.mode == "dense", status=status)
         if keys is not None:
             nn.linear(x, self.lm_head, norm=hd.final_norm, eps=c.eps, argmax_keys=keys, xn_out=buf["hn"][:B])
         return x
@@ -547,13 +561,13 @@ class NemotronModel:
         buf = self._bufs[3]
         ids = buf["ids"][:3]
         N.call("hsd_gather_tokens", N.ptr(prompt_dev), T, N.ptr(cache.seq), 0, 3, N.ptr(ids), N.stream(self.device))
-        x = self.embed(ids, out=buf["x"])
+        x = self.embed(ids, out=buf["x"], status=cache.status)
         self.layers(x, buf, cache)
         if with_head:
             pend = buf["pend"][:3]
             N.call("hsd_gather_tokens", N.ptr(prompt_dev), T, N.ptr(cache.seq), 1, 3, N.ptr(pend),
                    N.stream(self.device))
-            self.mtp_rows(x, pend, buf, cache.head_kv, cache.head_pos)
+            self.mtp_rows(x, pend, buf, cache.head_kv, cache.head_pos, status=cache.status)
         N.call("hsd_prefill_advance", N.ptr(cache.seq), T, 3, NSLAB, N.stream(self.device))
 
     def prefill(self, tokens, cache: ModelCache, with_head=None, graph=True):
@@ -565,6 +579,10 @@ class NemotronModel:
         prompt = torch.as_tensor(tokens, dtype=torch.int32).to(self.device)
         T = int(prompt.numel())
         nsteps = (T + 2) // 3
+        if T < 1 or 3 * nsteps > self.cfg.max_seq:
+            # the last 3-row step writes attention rows up to 3 * nsteps - 1
+            raise N.HSDError(f"a {T}-token prompt needs {3 * nsteps} attention cache rows (3-row prefill steps); "
+                             f"max_seq is {self.cfg.max_seq}")
         if graph and nsteps > 2:
             g = self._capture(lambda: self._prefill_step(prompt, T, cache, with_head))
             for _ in range(nsteps):
@@ -578,12 +596,13 @@ class NemotronModel:
         r = (T - 1) % 3
         return self._bufs[3]["x"][r:r + 1]
 
-    def _capture(self, fn):
+    def _capture(self, fn, keep_graph=False):
         """A graph of fn() (one step; it reads and advances the sequence state on the
         device, so it is captured without a warm-up run: every buffer is preallocated and
         nothing allocates inside). The graph is bound to the caches fn uses; the caller
-        keeps it only while they live."""
-        g = torch.cuda.CUDAGraph()
+        keeps it only while they live. keep_graph: the hipGraph_t stays readable
+        (raw_cuda_graph()) until the graph is instantiated."""
+        g = torch.cuda.CUDAGraph(keep_graph=keep_graph)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
@@ -595,7 +614,7 @@ class NemotronModel:
     # ---- plain decode (model.py:281-323)
     def _decode_step(self, cache):
         buf = self._bufs[1]
-        x = self.embed(cache.seq[N.SEQ_TOK:N.SEQ_TOK + 1], out=buf["x"])
+        x = self.embed(cache.seq[N.SEQ_TOK:N.SEQ_TOK + 1], out=buf["x"], status=cache.status)
         self.layers(x, buf, cache)
         self.head_keys(x, buf, buf["keys"])
         N.call("hsd_decode_advance", N.ptr(buf["keys"]), self.slots, N.ptr(cache.seq), N.ptr(cache.out_tokens),
@@ -672,20 +691,21 @@ class NemotronModel:
         st = N.stream(self.device)
         # the head over the rows the last verify confirmed (R of them valid); only row R-1's
         # prediction is a draft (model.py:408-411), so lm_head runs on that row alone
-        x3 = self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos)
+        x3 = self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos, status=cache.status)
         N.call("hsd_seq_select_row", N.ptr(x3), x3.stride(0), N.ptr(cache.seq), N.ptr(b1["x1"]), c.hidden, st)
         nn.linear(b1["x1"], self.lm_head, norm=self.mtp.final_norm, eps=c.eps, argmax_keys=b1["keys1"],
                   xn_out=b1["hn1"])
         N.call("hsd_mtp_chain", N.ptr(b1["keys1"]), 0, self.slots, N.ptr(b1["hn1"]), 0, c.hidden, N.ptr(cache.seq),
                N.ptr(b3["d1"]), N.ptr(b1["h2"]), st)
         # the chained call on its own normed hidden row (mtp.py, model.py:411-413)
-        self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"])
+        self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"],
+                      status=cache.status)
         ids = b3["ids"]
         N.call("hsd_draft_ids", N.ptr(b3["d1"]), N.ptr(b1["keys2"]), self.slots, 2, N.ptr(cache.seq),
                N.ptr(script), 0 if script is None else script.numel(), N.ptr(accepts),
                0 if accepts is None else accepts.numel(), c.vocab, N.ptr(ids), st)
         # verify [tok, d1, d2] in one pass of 3 rows, then accept and roll back on the device
-        x = self.embed(ids[:3], out=b3["x"])
+        x = self.embed(ids[:3], out=b3["x"], status=cache.status)
         self.layers(x, b3, cache)
         self.head_keys(x, b3, b3["keys"])
         N.call("hsd_spec_accept", N.ptr(b3["keys"]), b3["keys"].stride(0), self.slots, 2, N.ptr(ids),
@@ -731,10 +751,16 @@ class Session:
         dev = model.device
         if mtp and model.mtp is None:
             raise N.HSDError("an MTP session needs the model's MTP head")
+        self.prompt_len = T = len(prompt)
+        self.max_seq = model.cfg.max_seq
+        # attention cache rows: the prompt's (3-row prefill steps write up to 3 ceil(T / 3)),
+        # then one per generated token and the two draft rows of a verify beyond the last
+        if 3 * ((T + 2) // 3) > self.max_seq or T + cap + 2 > self.max_seq:
+            raise N.HSDError(f"a {T}-token prompt and {cap} generated tokens need {max(3 * ((T + 2) // 3), T + cap + 2)} "
+                             f"attention cache rows; max_seq is {self.max_seq}")
         self.cache = cache = model.make_cache(cap=cap + 4)
         self.script = None if script is None else torch.as_tensor(script, dtype=torch.int32).to(dev)
         self.accepts = None if accepts is None else torch.as_tensor(accepts, dtype=torch.int32).to(dev)
-        self.prompt_len = len(prompt)
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
         x_last = model.prefill(prompt, cache, with_head=mtp, graph=graph)
@@ -747,10 +773,13 @@ class Session:
             N.call("hsd_seq_add", N.ptr(cache.seq), N.SEQ_R, 1, N.stream(dev))
         torch.cuda.synchronize(dev)
         self.prompt_s = time.perf_counter() - t0
+        cache.check_status("prefill")
+        self.n_bound = 1                  # an upper bound of the emitted count (exact after emitted())
         if mtp:
             fn = lambda: model._mtp_step(cache, self.script, self.accepts)
         else:
             fn = lambda: model._decode_step(cache)
+        self.step_fn = fn
         self._run = model._capture(fn).replay if graph else fn
         self.decode_s = 0.0
         self.steps = 0
@@ -760,6 +789,14 @@ class Session:
         returns their seconds."""
         if n <= 0:
             return 0.0
+        per = 3 if self.mtp else 1
+        if self.prompt_len + self.n_bound + per * n + 1 > self.max_seq:
+            # a step's rows sit at POS = T + emitted - 1 onwards (up to 3 of them): refresh the
+            # bound from the device before refusing
+            self.emitted()
+            if self.prompt_len + self.n_bound + per * n + 1 > self.max_seq:
+                raise N.HSDError(f"{n} more steps could pass the attention cache's {self.max_seq} rows "
+                                 f"(prompt {self.prompt_len}, up to {self.n_bound} tokens emitted)")
         dev = self.m.device
         torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -771,13 +808,16 @@ class Session:
         sec = e0.elapsed_time(e1) * 1e-3
         self.decode_s += sec
         self.steps += n
+        self.n_bound += per * n
+        self.cache.check_status("decode step")
         return sec
 
     def state(self):
         return self.cache.state()
 
     def emitted(self):
-        return int(self.cache.seq[N.SEQ_N].item())
+        self.n_bound = int(self.cache.seq[N.SEQ_N].item())
+        return self.n_bound
 
     def tokens(self, limit=None):
         n = min(self.emitted(), self.cache.cap)

@@ -103,34 +103,45 @@ def test_python_layer_refuses_cpu_tensors():
         N.ptr(torch.zeros(4))
 
 
+BUNDLER = "/opt/rocm/llvm/bin/clang-offload-bundler"
+READELF = "/opt/rocm/llvm/bin/llvm-readelf"
+
+
+def device_code_objects(d):
+    """The gfx950 code objects of libhsd.so (one per source file), unbundled into dir d."""
+    import shutil
+    import subprocess
+    if not (os.path.exists(BUNDLER) and os.path.exists(READELF) and shutil.which("objcopy") and shutil.which("nm")):
+        pytest.skip("ROCm LLVM tools or binutils not installed")
+    fb = os.path.join(d, "fb.bin")
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", N.LIB_PATH, fb], check=True)
+    blob = open(fb, "rb").read()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts = [m.start() for m in re.finditer(re.escape(magic), blob)]
+    assert starts, "no offload bundle in libhsd.so"
+    out = []
+    for i, a in enumerate(starts):              # one bundle per object file
+        part, dev = os.path.join(d, f"b{i}.bin"), os.path.join(d, f"dev{i}.o")
+        with open(part, "wb") as f:
+            f.write(blob[a:starts[i + 1] if i + 1 < len(starts) else len(blob)])
+        subprocess.run([BUNDLER, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={part}",
+                        f"--output={dev}", "--unbundle"], check=True)
+        out.append(dev)
+    return out
+
+
 def test_every_kernel_handle_has_device_code():
     """Each kernel handle the host side of libhsd.so registers names a kernel of its gfx950
     code object. A launch through a handle without one aborts the process in the HIP
     runtime; a template argument whose type has no name (an unnamed enum) mangles
     differently in the host and device compilations and produced exactly that."""
-    import shutil
     import subprocess
     import tempfile
-    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
-    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
-    if not (os.path.exists(bundler) and os.path.exists(readelf) and shutil.which("objcopy") and shutil.which("nm")):
-        pytest.skip("ROCm LLVM tools or binutils not installed")
     so = N.LIB_PATH
     with tempfile.TemporaryDirectory() as d:
-        fb, dev = os.path.join(d, "fb.bin"), os.path.join(d, "dev.o")
-        subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", so, fb], check=True)
-        blob = open(fb, "rb").read()
-        magic = b"__CLANG_OFFLOAD_BUNDLE__"
-        starts = [m.start() for m in re.finditer(re.escape(magic), blob)]
-        assert starts, "no offload bundle in libhsd.so"
         devsyms = set()
-        for i, a in enumerate(starts):          # one bundle per object file
-            part = os.path.join(d, f"b{i}.bin")
-            with open(part, "wb") as f:
-                f.write(blob[a:starts[i + 1] if i + 1 < len(starts) else len(blob)])
-            subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={part}",
-                            f"--output={dev}", "--unbundle"], check=True)
-            devsyms |= {ln.split()[-1] for ln in subprocess.run([readelf, "-s", "-W", dev], check=True,
+        for dev in device_code_objects(d):
+            devsyms |= {ln.split()[-1] for ln in subprocess.run([READELF, "-s", "-W", dev], check=True,
                                                                capture_output=True, text=True).stdout.splitlines()
                         if ln.strip()}
     host = subprocess.run(["nm", so], check=True, capture_output=True, text=True).stdout.splitlines()
@@ -140,3 +151,36 @@ def test_every_kernel_handle_has_device_code():
     assert handles, "no kernel handles found in libhsd.so"
     missing = sorted(handles - devsyms)
     assert not missing, f"{len(missing)} kernel handles without device code, e.g. {missing[:3]}"
+
+
+def test_no_kernel_spills_to_scratch():
+    """No kernel of libhsd.so keeps registers in scratch memory: every instance's
+    private segment is empty (from the code objects' kernel metadata). A spilled
+    instance is a slow path a caller could fall onto with an unusual shape."""
+    import subprocess
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        kernels, spilled = 0, []
+        for dev in device_code_objects(d):
+            notes = subprocess.run([READELF, "--notes", dev], check=True, capture_output=True, text=True).stdout
+            for ent in notes.split("- .agpr_count")[1:]:
+                name = re.search(r"\.name:\s+(\S+)", ent).group(1)
+                priv = int(re.search(r"\.private_segment_fixed_size:\s+(\d+)", ent).group(1))
+                spill = int(re.search(r"\.vgpr_spill_count:\s+(\d+)", ent).group(1))
+                kernels += 1
+                if priv or spill:
+                    spilled.append((name, priv, spill))
+    assert kernels >= 100
+    assert not spilled, f"{len(spilled)} kernels use scratch, e.g. {spilled[:3]}"
+
+
+def test_linear_row_length_limits():
+    """hsd_linear refuses 4-bit rows longer than 4096 inputs and bf16 rows longer than 6144
+    (HSD_ERR_SHAPE, before any launch)."""
+    lib = N.lib()
+    d = ctypes.c_void_p(256)
+    def call(w_kind, I):
+        return lib.hsd_linear(d, I, 0, None, 0, None, 1e-5, d, d, d, w_kind, d, 64, 0, None, 0, None, 0, None, 0,
+                              1, 64, I, None)
+    assert call(0, 4160) == -2 and b"at most 4096" in lib.hsd_last_error()
+    assert call(1, 6152) == -2 and b"at most 6144" in lib.hsd_last_error()

@@ -46,7 +46,7 @@ def ulp_close(a_bits, b_bits):
     return np.all(np.abs(sa - sb) <= 1), float(np.mean(a == b))
 
 
-@pytest.mark.parametrize("I,O_", [(2688, 2688), (4096, 1024), (2688, 10304), (2688, 20480), (4096, 16384),
+@pytest.mark.parametrize("I,O_", [(2688, 2688), (4096, 1024), (3584, 512), (2688, 10304), (2688, 20480), (4096, 16384),
                                   (1024, 96)])
 def test_rms_linear_matches_oracle(dev, I, O_):
     """(2688, 20480) and (4096, 16384): more 16-row blocks than resident workgroups, so a

@@ -229,3 +229,23 @@ def test_mtp_head_call_surface(model):
     top = np.sort(lg)[::-1]
     if top[0] - top[1] > 6e-2 * np.abs(lg).max():
         assert int(pred[0]) == int(np.argmax(lg))
+
+
+def test_cache_bounds_are_checked(model):
+    """A prompt plus generation that would pass the attention caches' max_seq rows is
+    refused on the host before any kernel runs, and a step that would pass them is
+    refused before it is launched; a kernel's flag in the cache's status word raises."""
+    c = model.cfg
+    with pytest.raises(N.HSDError, match="max_seq"):
+        model.session(np.zeros(c.max_seq - 4, np.int32), cap=8)
+    with pytest.raises(N.HSDError, match="max_seq"):
+        # 3-row prefill steps: a max_seq-token prompt's last step would write 2 rows past it
+        model.prefill(np.zeros(c.max_seq, np.int32), model.make_cache(cap=4), graph=False)
+    s = model.session(PROMPT, cap=8)
+    with pytest.raises(N.HSDError, match="attention cache"):
+        s.step(c.max_seq)
+    s.step(2)
+    assert s.emitted() == 3
+    s.cache.status.fill_(N.STATUS_BAD_STATE)
+    with pytest.raises(N.HSDError, match="overflow"):
+        s.cache.check_status("test")
