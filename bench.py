@@ -16,12 +16,14 @@ decode sweep; `workloads` holds the decode sweep, the prefill grouped GEMM, the 
 verify + rollback over 23 Mamba-2 layers and the MoE front end, each with its roofline and
 its CPU baseline (the NumPy oracle on the host cores, a bounded sample).
 
---workload e2e|decode|prefill|mtp|up prints one of them alone; --workload step --mode
+--workload e2e|decode|prefill|mtp|up|proj prints one of them alone (proj: the step's projections
+and attention, each alone; calib: the counter calibration copy); --workload step --mode
 mtp|sparse|dense replays one captured step of the model (for per-kernel profiles).
 """
 from __future__ import annotations
 
 import argparse
+import math
 import json
 import os
 import platform
@@ -64,6 +66,19 @@ def pmc_traffic(workload):
     cal, kib = fields["cal"], fields["kib"]
     return int(1024 * (float(kib["fetch_kib"]) * float(cal["fetch_factor"])
                        + float(kib["write_kib"]) * float(cal["write_factor"])))
+def pmc_mfma_util(kernel):
+    """The kernel's matrix-core utilisation (MFMA busy cycles over SIMD cycles of the
+    dispatch) from the committed counter summary, or None."""
+    try:
+        for ln in open(os.path.join(ROOT, "profiles", "mfma_utilisation.txt")):
+            tok = ln.split()
+            if tok[:2] == ["mfma", kernel]:
+                return float(tok[2].split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 NL = 23                      # MoE layers
 D, F, FS, E, K = S.D, S.F, S.FS, S.E, S.TOPK
 NR = K * F + FS
@@ -499,7 +514,10 @@ def bench_prefill(args):
                             layers=nl, tt=tt, zero_frac=args.zero_frac),
                 roofline=dict(bound="mfma", achieved=round(tflops, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
                               frac=round(tflops / BF16_PEAK_TFLOPS, 4), traffic=pmc_traffic("prefill"),
-                              hbm_frac_dense_weights=round(wbytes / (ms_gemm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
+                              hbm_frac_dense_weights=round(wbytes / (ms_gemm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              mfma_busy_frac=pmc_mfma_util("k_gemm"),
+                              mfma_busy_note="k_gemm's MFMA busy cycles over its SIMD cycles, from rocprofv3 "
+                                             "counters (profiles/mfma_utilisation.txt)"),
                 cpu_baseline=cpu,
                 prefill_tok_s=round(T / (ms_all * 1e-3), 1), gflop_per_prompt=round(flops / 1e9, 2))
 
@@ -528,57 +546,109 @@ def cpu_baseline_mtp(args, per_layer, layers=4):
                 ms_per_layer_step=round(1e3 * sec / layers, 2), **info)
 
 
+def mamba_layer_bytes(cfg, L):
+    """Algorithmic bytes of one Mamba-2 layer-step of L rows. "ssm": the conv + SSM update
+    as the model runs it (hsd_mamba_ssm_gated): the fp32 state read once and written once
+    per row (the checkpoints), the conv window read and L checkpoints written, the conv
+    weights, the L rows' conv inputs, dt and gate read and z with its sums of squares
+    written. "block": that plus in_proj and out_proj (4-bit weights once, RMS norm and
+    gated-norm weights) and the residual row read and written."""
+    D, H, P, N_, G = cfg.hidden, cfg.mamba_heads, cfg.mamba_head_dim, cfg.ssm_state, cfg.n_groups
+    DI, CD = cfg.mamba_inner, cfg.conv_dim
+    state = H * P * N_ * 4
+    ssm = (state + L * state + 3 * CD * 2 + L * 3 * CD * 2 + CD * 5 * 2 + 3 * H * 4
+           + L * (CD + H + DI) * 2 + L * (DI + DI // 16) * 4)
+    block = ssm + _q4(cfg.in_proj_dim, D) + _q4(D, DI) + 2 * D + 2 * DI + 2 * L * D * 2
+    return dict(ssm=ssm, block=block)
+
+
 def bench_mtp(args):
+    """MTP verify + rollback over 23 Mamba-2 layers on the model's own path: each step runs
+    3 rows through every layer's block (in_proj with the RMS norm fused, the conv + SSM
+    update with the gate applied and every row's state checkpointed, out_proj with the
+    gated norm and the residual fused), then rolls the shared ring index back to the
+    scripted number of kept rows, P(0, 1, 2 drafts accepted) = (0.15, 0.35, 0.50). The
+    headline is the conv + SSM part (hsd_mamba_ssm_gated, the verify the survey's byte
+    model counts); the whole block is timed beside it."""
     dev = torch.device("cuda:0")
-    nl = NL
-    mixers, caches = [], []
+    cfg = Mdl.ModelConfig()
+    init = Mdl._Init(args.seed, dev)
+    blocks = [Mdl.MambaBlock(cfg, init) for _ in range(NL)]
     cur = torch.zeros(1, dtype=torch.int32, device=dev)
-    for l in range(nl):
+    caches = []
+    for l, b in enumerate(blocks):
         p = S.mamba_params_np(args.seed + l)
-        mixers.append(M.Mamba2Mixer(conv_w=S.to_device(p["conv_w"], dev), conv_b=S.to_device(p["conv_b"], dev),
-                                    A_log=S.to_device(p["A_log"], dev), dt_bias=S.to_device(p["dt_bias"], dev),
-                                    D=S.to_device(p["D"], dev), norm_w=S.to_device(p["norm_w"], dev)))
-        caches.append(M.MambaCache(mixers[-1], dev, nslab=4, cur=cur,
-                                   conv_state=S.to_device(p["conv_state"], dev),
+        caches.append(M.MambaCache(b.mixer, dev, nslab=Mdl.NSLAB, cur=cur, conv_state=S.to_device(p["conv_state"], dev),
                                    ssm_state=torch.from_numpy(p["ssm_state"]).to(dev)))
+    L, nsteps, D = 3, 64, cfg.hidden
     rng = np.random.default_rng(args.seed)
-    nsteps = 64
-    rows = S.to_device(np.stack([S.mamba_rows_np(rng, 3) for _ in range(nsteps)]), dev)   # [steps, 3, 10304]
+    xs = [S.to_device(S.bf16_bits(rng.standard_normal((L, D))), dev) for _ in range(nsteps)]
+    projs = [S.to_device(S.mamba_rows_np(rng, L), dev) for _ in range(NL)]
     accepts = mtp.scripted_accepts(nsteps, (0.15, 0.35, 0.50), args.seed)
     nkeep = torch.tensor(accepts + 1, dtype=torch.int32, device=dev)
-    ws = torch.empty(N.lib().hsd_mamba_workspace_bytes(3, 64, 64), dtype=torch.uint8, device=dev)
+    buf = dict(proj=torch.zeros((L, cfg.in_proj_dim), dtype=torch.bfloat16, device=dev),
+               y_pre=torch.zeros((L, cfg.mamba_inner + cfg.mamba_inner // 16), dtype=torch.float32, device=dev))
+    st = N.stream(dev)
 
-    def step(i):
-        recs = []
-        for l in range(nl):
-            M.verify_rows(mixers[l], rows[i], caches[l], workspace=ws)
-            recs.append((caches[l], 3))
-        M.mamba_rollback(recs[:1], 0, n_keep_dev=nkeep[i:i + 1])
+    def rollback(i):
+        N.call("hsd_mamba_select_row", N.ptr(cur), N.ptr(nkeep[i:i + 1]), 0, L, Mdl.NSLAB, None, st)
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step(0)
-    torch.cuda.current_stream().wait_stream(s)
-    graphs = []
-    for i in range(nsteps):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(i)
-        graphs.append(g)
-    ms = time_graphs(graphs, args.steps, args.warmup)
-    per_layer = 2097152 + 3 * 2097152 + 3 * 6144 * 2 + 3 * 3 * 6144 * 2 + 3 * 10304 * 2 + 3 * 4096 * 2
-    gbs = per_layer * nl * args.steps / (ms * 1e-3) / 1e9
-    log(f"[mtp] verify(3)+rollback, 23 Mamba-2 layers: {1e3 * ms / args.steps:.1f} us/step, {gbs:.0f} GB/s")
-    cpu = cpu_baseline_mtp(args, per_layer) if args.cpu_budget > 0 else None
-    return dict(metric="MTP-2 verify + rollback, 23 Mamba-2 layers: HBM GB/s", value=round(gbs, 2), unit="GB/s",
-                n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=round(ms / args.steps, 5),
+    def step_block(i):
+        for l in range(NL):
+            blocks[l].rows(xs[i], buf, caches[l])
+        rollback(i)
+
+    def step_ssm(i):
+        for l in range(NL):
+            M.ssm_rows(blocks[l].mixer, projs[l], caches[l], out=buf["y_pre"], gated=True)
+        rollback(i)
+
+    def capture(fn):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(0)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gs = []
+        for i in range(nsteps):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn(i)
+            gs.append(g)
+        return gs
+
+    g_ssm = capture(step_ssm)
+    ms = time_graphs(g_ssm, args.steps, args.warmup)
+    del g_ssm
+    g_blk = capture(step_block)
+    ms_blk = time_graphs(g_blk, args.steps, args.warmup)
+    del g_blk
+    lb = mamba_layer_bytes(cfg, L)
+    gbs = lb["ssm"] * NL * args.steps / (ms * 1e-3) / 1e9
+    gbs_blk = lb["block"] * NL * args.steps / (ms_blk * 1e-3) / 1e9
+    us, us_blk = 1e3 * ms / args.steps, 1e3 * ms_blk / args.steps
+    log(f"[mtp] verify(3)+rollback, 23 Mamba-2 layers: conv + SSM (hsd_mamba_ssm_gated) {us:.1f} us/step, "
+        f"{gbs:.0f} GB/s; whole block (in_proj, conv + SSM, out_proj) {us_blk:.1f} us/step, {gbs_blk:.0f} GB/s")
+    cpu = cpu_baseline_mtp(args, lb["ssm"]) if args.cpu_budget > 0 else None
+    roof_us = lb["ssm"] * NL / HBM_PEAK_GBS / 1e3
+    return dict(metric="MTP-2 verify + rollback, 23 Mamba-2 layers (conv + SSM update): HBM GB/s", value=round(gbs, 2),
+                unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=round(ms / args.steps, 5),
                 higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32 state, bf16 I/O",
                 data="synthetic",
-                config=dict(workload="MTP verify + rollback: 23 Mamba-2 layers, 3 rows, P(0,1,2)=(.15,.35,.5)"),
+                config=dict(workload="MTP verify + rollback: 23 Mamba-2 layers (64 heads x 64, state 128, 8 groups, "
+                                     "conv 4), 3 rows per step, P(0,1,2)=(.15,.35,.5); the model's path "
+                                     "(hsd_mamba_ssm_gated; the whole block beside it)"),
                 roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                               frac=round(gbs / HBM_PEAK_GBS, 4), traffic=pmc_traffic("mtp"),
-                              bytes_per_layer_step=per_layer),
+                              bytes_per_layer_step=lb["ssm"], us_per_step=round(us, 2),
+                              roof_us_per_step=round(roof_us, 2)),
+                block=dict(us_per_step=round(us_blk, 2), gbs=round(gbs_blk, 1),
+                           frac=round(gbs_blk / HBM_PEAK_GBS, 4), bytes_per_layer_step=lb["block"],
+                           traffic_per_layer_step=pmc_traffic("mtp_block"),
+                           roof_us_per_step=round(lb["block"] * NL / HBM_PEAK_GBS / 1e3, 2),
+                           note="in_proj (RMS norm fused) + hsd_mamba_ssm_gated + out_proj (gated norm and "
+                                "residual fused), 23 layers, then the rollback"),
                 cpu_baseline=cpu)
 
 
@@ -982,6 +1052,125 @@ def bench_step(args):
                                               prompt_tokens=len(prompt)))
 
 
+# ------------------------------------------------------------------ the step's other kernels
+def bench_proj(args):
+    """The other kernels of a decode / verify step, each on its own, timed like the decode
+    sweep (graphs of 23 calls, distinct weight sets rotated so that the calls read HBM, not
+    the 256 MB memory-side cache): every 4-bit and bf16 projection of the model with the
+    prologue and epilogue the model fuses into it, at one token row (a decode step) and
+    three (a verify step), and the attention over a 2100-key cache. Per kernel: us per
+    call, algorithmic bytes (weights once, inputs and outputs) and the fraction of the HBM
+    roof."""
+    from hsd import nn
+    dev = torch.device("cuda:0")
+    cfg = Mdl.ModelConfig()
+    init = Mdl._Init(args.seed, dev)
+    D, DI = cfg.hidden, cfg.mamba_inner
+    ncall = 23
+    steps, warm = max(args.steps, 10), max(args.warmup, 2)
+    out = []
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 7)
+
+    def rows(B, n, dt=torch.bfloat16, lo=-1.0, hi=1.0):
+        return (torch.rand((B, n), device=dev, generator=gen) * (hi - lo) + lo).to(dt)
+
+    def timed(name, key, B, nbytes, fn):
+        graphs = capture_steps(lambda t, l: fn(l), 2)
+        ms = time_graphs(graphs, steps, warm)
+        del graphs
+        us = 1e3 * ms / (steps * ncall)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append(dict(kernel=name, rows=B, us_per_call=round(us, 3), mb_per_call=round(nbytes / 1e6, 3),
+                        gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
+                        traffic=pmc_traffic(f"proj:{key}:{B}")))
+        log(f"[proj] {name:36s} rows {B}: {us:7.2f} us, {nbytes / 1e6:7.2f} MB, {gbs:6.0f} GB/s "
+            f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+
+    specs = [  # name, key, O, I, 4-bit, prologue, epilogue
+        ("Mamba in_proj (RMS norm)", "in_proj", cfg.in_proj_dim, D, True, "rms", "bf16"),
+        ("Mamba out_proj (gated norm, residual)", "out_proj", D, DI, True, "gated_z", "resid"),
+        ("attention q|k|v (RMS norm)", "qkv", cfg.qkv_dim, D, True, "rms", "bf16"),
+        ("attention o_proj (residual)", "o_proj", D, cfg.attn_heads * cfg.head_dim, True, "none", "resid"),
+        ("MoE router gate, bf16 (RMS norm)", "gate", cfg.n_experts, D, False, "rms", "bf16"),
+        ("MTP eh_proj, bf16", "eh_proj", D, 2 * D, False, "none", "bf16"),
+        ("lm_head (RMS norm, argmax)", "lm_head", cfg.vocab, D, True, "rms", "argmax"),
+    ]
+    for name, key, O, I, q4, pro, epi in specs:
+        wbytes = _q4(O, I) if q4 else O * I * 2
+        nsets = min(ncall, max(2, -(-700_000_000 // wbytes)))
+        Ws = [nn.QWeight(*init.q4(O, I, 1.0 / math.sqrt(I))) if q4 else nn.QWeight(init.bf16(O, I, std=I ** -0.5))
+              for _ in range(nsets)]
+        normw = init.uniform(I)
+        for B in (1, 3):
+            if pro == "gated_z":                          # z rows with their sums of squares past I
+                x = rows(B, I + I // 16, torch.float32, 0.1, 1.0)[:, :I]
+            else:
+                x = rows(B, I)
+            res = rows(B, O) if epi == "resid" else None
+            keys = torch.empty((B, nn.argmax_slots(O, q4)), dtype=torch.int64, device=dev) if epi == "argmax" else None
+            y = None if epi == "argmax" else torch.empty((B, O), dtype=torch.bfloat16, device=dev)
+            xn = torch.empty((B, I), dtype=torch.bfloat16, device=dev) if pro == "rms" and not q4 else None
+            io = B * I * (4 if pro == "gated_z" else 2) + B * O * 2 * (2 if epi == "resid" else 1) + \
+                (2 * I if pro != "none" else 0) + (B * keys.shape[1] * 8 if keys is not None else 0)
+
+            def call(l, W=Ws, x=x, res=res, keys=keys, y=y, xn=xn, pro=pro, epi=epi, normw=normw):
+                w = W[l % len(W)]
+                nn.linear(x, w, norm=normw if pro != "none" else None, eps=cfg.eps, gated_z=pro == "gated_z",
+                          residual=res if epi == "resid" else None, out=y if epi != "argmax" else None,
+                          argmax_keys=keys, xn_out=xn)
+            timed(name, key, B, wbytes + io, call)
+        del Ws
+        torch.cuda.empty_cache()
+    # attention over a 2100-key cache (6 layers' caches rotated)
+    P = 2100
+    kvs = [nn.KVCache(cfg.kv_heads, cfg.max_seq, dev, cfg.head_dim) for _ in range(6)]
+    for kv in kvs:
+        kv.k.normal_(generator=gen)
+        kv.v.normal_(generator=gen)
+    pos = torch.tensor([P], dtype=torch.int32, device=dev)
+    for B in (1, 3):
+        qkv = rows(B, cfg.qkv_dim)
+        o = torch.empty((B, cfg.attn_heads * cfg.head_dim), dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(N.lib().hsd_attn_workspace_bytes(B, cfg.attn_heads, cfg.max_seq), dtype=torch.uint8,
+                         device=dev)
+        nbytes = 2 * cfg.kv_heads * cfg.head_dim * 2 * (P + B) + B * cfg.qkv_dim * 2 + B * cfg.attn_heads * cfg.head_dim * 2
+
+        def att(l, qkv=qkv, o=o, ws=ws):
+            # the cache length stays P: the call writes rows P .. P+B-1 and a replay rewrites them
+            nn.attention(qkv, kvs[l % len(kvs)], pos, n_heads=cfg.attn_heads, n_kv_heads=cfg.kv_heads,
+                         head_dim=cfg.head_dim, out=o, workspace=ws)
+        timed(f"attention, {P} keys (part + combine)", "attention", B, nbytes, att)
+    return dict(metric="the step's projections and attention, each alone: HBM GB/s", value=None, unit="GB/s",
+                n_gpus=1, steps=steps, warmup=warm, ms_per_step=None, higher_is_better=True, scaling="weak",
+                vs_baseline=None, dtype="f32 accumulate (4-bit or bf16 weights, bf16 activations)", data="synthetic",
+                config=dict(workload="graphs of 23 calls over rotated weight sets, 1 and 3 token rows"),
+                kernels=out)
+
+
+def bench_calib(args):
+    """The counter calibration workload: a 268435456-byte device-to-device copy (torch
+    copy_), six times. Its FETCH_SIZE and WRITE_SIZE per dispatch against the 256 MiB read
+    and written give the factors that turn those counters into bytes."""
+    dev = torch.device("cuda:0")
+    n = 1 << 26
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(6):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 6
+    gbs = 2 * 4 * n / (ms * 1e-3) / 1e9
+    log(f"[calib] 256 MiB copy: {ms * 1e3:.1f} us, {gbs:.0f} GB/s read + write")
+    return dict(metric="256 MiB device copy (counter calibration)", value=round(gbs, 1), unit="GB/s", n_gpus=1,
+                steps=6, warmup=0, ms_per_step=round(ms, 4), higher_is_better=True, scaling="weak",
+                vs_baseline=None, dtype="f32", data="synthetic", config=dict(workload="copy", bytes=4 * n))
+
+
 def _sub(rec):
     """A workload's record inside the combined line (the fields the run record repeats dropped)."""
     drop = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "data")
@@ -1015,7 +1204,8 @@ def main():
     ap.add_argument("--steps", type=int, default=0,
                     help="timed steps (0: the workload's default; end to end: the steps that make 256 tokens)")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="all", choices=("all", "e2e", "decode", "prefill", "mtp", "up", "step"))
+    ap.add_argument("--workload", default="all",
+                    choices=("all", "e2e", "decode", "prefill", "mtp", "up", "step", "calib", "proj"))
     ap.add_argument("--mode", default="mtp", choices=("mtp", "sparse", "dense"), help="step: which step")
     ap.add_argument("--prompt", type=int, default=2048, help="end to end: prompt tokens")
     ap.add_argument("--gen", type=int, default=256, help="end to end: generated tokens")
@@ -1040,12 +1230,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    if args.workload not in ("all", "e2e", "step"):
+    if args.workload not in ("all", "e2e", "step", "calib", "proj"):
         defaults = dict(decode=(200, 20), prefill=(3, 1), mtp=(200, 20), up=(200, 20))[args.workload]
         if args.steps <= 0:
             args.steps, args.warmup = defaults
     fn = dict(all=bench_all, e2e=bench_e2e, decode=bench_decode, prefill=bench_prefill, mtp=bench_mtp,
-              up=bench_up, step=bench_step)[args.workload]
+              up=bench_up, step=bench_step, calib=bench_calib, proj=bench_proj)[args.workload]
     rec = fn(args)
     rec["device"] = torch.cuda.get_device_name(0)
     rec["torch"] = torch.__version__

@@ -72,3 +72,61 @@ def test_noalloc_rejects_rows_beyond_the_scratch(layer, dev):
         N.ptr(N.as_words(nm[3])), N.ptr(nm[4]), N.ptr(nm[5]), N.ptr(y), 2, B, D, F, FS, TOPK, nm[0].shape[0], 0,
         None, None, N.stream(dev))
     assert rc == -2 and b"static scratch" in N.lib().hsd_last_error()
+
+
+# The child process of test_noalloc_first_call_inside_graph_capture: its first
+# hsd_sparse_down_decode_noalloc call (the one that looks up the device's scratch address)
+# is made while a HIP graph is being captured; the graph is replayed three times with eager
+# calls of the workspace entry point in between, and every replay's output must equal that
+# entry point's bit for bit.
+CHILD = r'''
+import sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+from hsd import _native as N, layout, synth as S
+dev = torch.device("cuda:0")
+E, D, F, FS, K, B = 8, 256, 192, 384, 3, 3
+lay = S.moe_layer_np(5, n_experts=E, d=D, f=F, fs=FS)
+dv = {k: S.to_device(v, dev) for k, v in lay.items()}
+nm = layout.to_neuron_major(dv["w"], dv["s"], dv["b"]) + layout.to_neuron_major(dv["sw"], dv["ss"], dv["sb"])
+ins = []
+for i in range(3):
+    h, sel, gains = S.decode_inputs_np(40 + i, B=B, zero_frac=0.9, n_experts=E, f=F, fs=FS, topk=K)
+    ins.append([S.to_device(a, dev) for a in (h, sel, gains)])
+cur = [t.clone() for t in ins[0]]
+y = torch.empty((B, D), dtype=torch.float32, device=dev)
+ws = torch.empty(N.lib().hsd_sparse_down_workspace_bytes(B, D, F, FS, K), dtype=torch.uint8, device=dev)
+def args(h, sel, gains, out):
+    return [N.ptr(h), N.dtype_tag(h.dtype), N.ptr(sel), N.ptr(gains), N.ptr(N.as_words(nm[0])), N.ptr(nm[1]),
+            N.ptr(nm[2]), N.ptr(N.as_words(nm[3])), N.ptr(nm[4]), N.ptr(nm[5]), N.ptr(out), N.dtype_tag(out.dtype),
+            B, D, F, FS, K, E, 0, None, None]
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(s):
+    with torch.cuda.graph(g, stream=s):
+        N.call("hsd_sparse_down_decode_noalloc", *args(*cur, y), N.stream(dev))
+torch.cuda.current_stream().wait_stream(s)
+for i in range(3):
+    for c, t in zip(cur, ins[i]):
+        c.copy_(t)
+    g.replay()
+    ref = torch.empty_like(y)
+    N.call("hsd_sparse_down_decode", *args(*cur, ref), N.ptr(ws), ws.numel(), N.stream(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), ref.view(torch.int32)), f"replay {i} differs"
+    print(f"replay {i}: equal, max|y| {ref.abs().max().item():.4f}", flush=True)
+print("ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_inside_graph_capture(dev):
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", CHILD, root, os.path.join(root, "mlx-heimr-sparse-down_amd")],
+                       capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok")
