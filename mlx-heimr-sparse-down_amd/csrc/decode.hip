@@ -536,6 +536,7 @@ __global__ __launch_bounds__(64 * kDQWaves) void k_dense_down_q(
   }
   lds_barrier();
   // ---- the lane's pieces against its wavefront's outputs
+  const uint32_t nibm = opaque_vgpr(kNibHi);          // (w & nibm) | one: one v_and_or_b32
   float tot[kDQRW];
 #pragma unroll
   for (int r = 0; r < kDQRW; ++r) tot[r] = 0.0f;
@@ -552,10 +553,10 @@ __global__ __launch_bounds__(64 * kDQWaves) void k_dense_down_q(
       float acc = 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        acc = dot2_bf16(xq[m].x, ((qw[m] << 3) & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xq[m].y, ((qw[m] >> 1) & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xq[m].z, ((qw[m] >> 5) & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xq[m].w, ((qw[m] >> 9) & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].x, ((qw[m] << 3) & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].y, ((qw[m] >> 1) & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].z, ((qw[m] >> 5) & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xq[m].w, ((qw[m] >> 9) & nibm) | kBfOne2, acc);
       }
       const float sv = lo_bf16(sb[r][it]), bv = hi_bf16(sb[r][it]);
       const float u = fmaf(16.0f * sv, acc, fmaf(-16.0f, sv, bv) * xs);

@@ -87,6 +87,16 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// v in a vector register the compiler cannot see through. The 4-bit decodes build a bf16
+// pair as ((w >> k) & mask) | one: with both constants as literals that compiles to a
+// v_and_b32 and a v_or_b32 (the three-operand v_and_or_b32 takes no literal on this
+// target); with the mask in a register and the other constant in a scalar register it is one
+// v_and_or_b32. Call once per kernel, outside the loops.
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // v read from another lane of the same 16-lane row by a DPP control (quad_perm, row
 // mirrors: every source lane is inside the row)
 template <int CTRL>

@@ -325,6 +325,7 @@ void k_linear(LinArgs a) {
   constexpr int PX = IMAX / 32;                        // 4-bit: LDS pitch of a token row in pieces
   float* xh = reinterpret_cast<float*>(lsm + NB * (Q4 ? 16 * PX : I / 2));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t nibm = opaque_vgpr(kNibHi);         // (w & nibm) | one: one v_and_or_b32
   const int nblk = (O + kRows - 1) / kRows;            // the last block may be partial
   const int NPr = I / T::kIn;                          // pieces per row
   // 4-bit: lanes 32 h .. 32 h + 31 take rows 2 h and 2 h + 1 of the wavefront's 4, lane l
@@ -452,10 +453,10 @@ void k_linear(LinArgs a) {
             uint32_t wc[4][4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              wc[m][0] = ((qw[m] << 3) & kNibHi) | kBfOne2;
-              wc[m][1] = ((qw[m] >> 1) & kNibHi) | kBfOne2;
-              wc[m][2] = ((qw[m] >> 5) & kNibHi) | kBfOne2;
-              wc[m][3] = ((qw[m] >> 9) & kNibHi) | kBfOne2;
+              wc[m][0] = ((qw[m] << 3) & nibm) | kBfOne2;
+              wc[m][1] = ((qw[m] >> 1) & nibm) | kBfOne2;
+              wc[m][2] = ((qw[m] >> 5) & nibm) | kBfOne2;
+              wc[m][3] = ((qw[m] >> 9) & nibm) | kBfOne2;
             }
             const float sv = lo_f(bk.s[it][i]), bv = hi_f(bk.s[it][i]);
             const float s16 = 16.0f * sv, bo = fmaf(-16.0f, sv, bv);
@@ -671,7 +672,10 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   constexpr int PX = IMAX / 32;                        // LDS pitch of a token row in pieces
   float* xg = reinterpret_cast<float*>(lsm + NB * 16 * PX);
   uint32_t* sbl = lsm + NB * 16 * PX + NB * (PX / 2);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wavefront index as a scalar: the group loops below branch on it uniformly (a
+  // vector index made each group an exec-masked branch, serialising the groups)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nibm = opaque_vgpr(kNibHi);         // (w & nibm) | one: one v_and_or_b32
   const int n = lane & 15, q = lane >> 4;
   const int nblk = (O + kQR - 1) / kQR;
 
@@ -731,26 +735,31 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
 #pragma unroll
     for (int r = 0; r < NB; ++r) y[r] = 0.0f;
     const uint32_t* sb = sbl + par * kQR * G;
+    // the first 8 group slots unconditionally (a group past G re-reads group G - 1 and adds
+    // nothing: a select, not a branch), so their LDS reads, unpacking and MFMAs interleave;
+    // the slots after them stop at the row's last group (a uniform branch)
 #pragma unroll
     for (int it = 0; it < kGW; ++it) {
-      const int g = wave + 4 * it;
-      if (g < G) {                                     // uniform
-        const int p = 2 * g + (q >> 1);
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (it >= 8 && wave + 4 * it >= G) break;
+      const int g0 = wave + 4 * it, g = min(g0, G - 1);
+      const int p = 2 * g + (q >> 1);
+      floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const uint32_t qw = i ? wb.w[it].y : wb.w[it].x;
-          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + i) * PX + p)]);
-          const uint4 wq = make_uint4(((qw << 3) & kNibHi) | kBfOne2, ((qw >> 1) & kNibHi) | kBfOne2,
-                                      ((qw >> 5) & kNibHi) | kBfOne2, ((qw >> 9) & kNibHi) | kBfOne2);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
-                                                        acc, 0, 0, 0);
-        }
-        const uint32_t sq = sb[g * kQR + n];
-        const float sv_ = lo_f(sq), bv_ = hi_f(sq);
-        const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t qw = i ? wb.w[it].y : wb.w[it].x;
+        const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + i) * PX + p)]);
+        const uint4 wq = make_uint4(((qw << 3) & nibm) | kBfOne2, ((qw >> 1) & nibm) | kBfOne2,
+                                    ((qw >> 5) & nibm) | kBfOne2, ((qw >> 9) & nibm) | kBfOne2);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
+                                                      acc, 0, 0, 0);
+      }
+      const uint32_t sq = sb[g * kQR + n];
+      const float sv_ = lo_f(sq), bv_ = hi_f(sq);
+      const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
 #pragma unroll
-        for (int r = 0; r < NB; ++r) y[r] += fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
+      for (int r = 0; r < NB; ++r) {
+        const float yn = y[r] + fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
+        y[r] = g0 < G ? yn : y[r];
       }
     }
     // lanes 0..15 hold token rows 0..3 of output row n (acc[r]: token row 4 (l / 16) + r)
@@ -845,7 +854,10 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
   __shared__ float wsum[1][4];
   __shared__ float red[2][4][kQR];                     // [block parity][wavefront][row]
   const int I = a.I, O = a.O, G = I / 64, NPr = I / 32, rowc = NPr + 1;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wavefront index as a scalar: the group loops below branch on it uniformly (a
+  // vector index made each group an exec-masked branch, serialising the groups)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nibm = opaque_vgpr(kNibHi);         // (w & nibm) | one: one v_and_or_b32
   const int n = lane & 15, q = lane >> 4;
   const int nblk = (O + kQR - 1) / kQR;
   const int nmine = nblk > (int)blockIdx.x ? (nblk - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
@@ -907,26 +919,30 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
     const uint16_t* ss = reinterpret_cast<const uint16_t*>(sl + 16 * 16 * rowc);
     const uint16_t* sbb = ss + 8 * NPr;
     float y = 0.0f;
+    // the first 8 group slots unconditionally (a group past G re-reads group G - 1 and adds
+    // nothing: a select, not a branch), so their LDS reads, unpacking and MFMAs interleave;
+    // the slots after them stop at the row's last group (a uniform branch). The sum over the
+    // wavefront's groups keeps its order.
 #pragma unroll
     for (int it = 0; it < kGW; ++it) {
-      const int g = wave + 4 * it;
-      if (g < G) {                                     // uniform
-        const int p = 2 * g + (q >> 1);
-        const uint2 w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (it >= 8 && wave + 4 * it >= G) break;
+      const int g0 = wave + 4 * it, g = min(g0, G - 1);
+      const int p = 2 * g + (q >> 1);
+      const uint2 w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
+      floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const uint32_t qw = i ? w2.y : w2.x;
-          const uint4 xa = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + i) * PX + p)]);
-          const uint4 wq = make_uint4(((qw << 3) & kNibHi) | kBfOne2, ((qw >> 1) & kNibHi) | kBfOne2,
-                                      ((qw >> 5) & kNibHi) | kBfOne2, ((qw >> 9) & kNibHi) | kBfOne2);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
-                                                        acc, 0, 0, 0);
-        }
-        const float sv_ = bf16_bits_to_f32(ss[n * G + g]), bv_ = bf16_bits_to_f32(sbb[n * G + g]);
-        const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
-        y += fmaf(s16, acc[0], bo * xg[g]);
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t qw = i ? w2.y : w2.x;
+        const uint4 xa = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + i) * PX + p)]);
+        const uint4 wq = make_uint4(((qw << 3) & nibm) | kBfOne2, ((qw >> 1) & nibm) | kBfOne2,
+                                    ((qw >> 5) & nibm) | kBfOne2, ((qw >> 9) & nibm) | kBfOne2);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
+                                                      acc, 0, 0, 0);
       }
+      const float sv_ = bf16_bits_to_f32(ss[n * G + g]), bv_ = bf16_bits_to_f32(sbb[n * G + g]);
+      const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
+      const float yn = y + fmaf(s16, acc[0], bo * xg[g]);
+      y = g0 < G ? yn : y;
     }
     if (q == 0) red[k & 1][wave][n] = y;
   };

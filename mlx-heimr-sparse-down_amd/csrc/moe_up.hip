@@ -47,7 +47,12 @@ static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kU
 template <int MAXD> struct UpShape {
   static constexpr int kMaxP = MAXD / 32;
   static constexpr int kXIt = (MAXD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
-  static constexpr int kWaves = MAXD <= kUpSmallD ? 8 : 6;               // per SIMD
+  // per SIMD: 7 for D <= 3072 (72 VGPRs). With the nibble mask in a register (one
+  // v_and_or_b32 per bf16 pair instead of a v_and_b32 and a v_or_b32) the routed instance
+  // needs 65-68 VGPRs; at 8 wavefronts (64 VGPRs) it spilled. 7 wavefronts with the shorter
+  // decode: MTP-2 step 1.854 / 1.846 against 1.860 / 1.863 ms for 8 with the literal decode,
+  // sparse decode step 1.037 / 1.028 against 1.044 / 1.041 ms (alternating runs).
+  static constexpr int kWaves = MAXD <= kUpSmallD ? 7 : 6;
 };
 // 16-row workgroups (4 rows per wavefront): at three token rows 19.0 against 19.8 us per
 // call for 8-row ones (fewer rounds of workgroups), at one row the same. Small workgroups
@@ -262,6 +267,7 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   lds_barrier();
 
   // ---- the lane's pieces into its row partial, then the row's 16-lane sum
+  const uint32_t nibm = opaque_vgpr(kNibHi);         // (w & nibm) | one: one v_and_or_b32
   float pr = 0.0f;
   const int rl = kUpRows * wave + rw;                 // row within the block
 #pragma unroll
@@ -279,10 +285,10 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
         // nibble n (bits 4n..4n+3 of each half) to bits 3..6: a left shift by 3 for n = 0,
         // right shifts by 1, 5, 9 for the others
         const uint32_t w0 = qw[m] << 3, w1 = qw[m] >> 1, w2 = qw[m] >> 5, w3 = qw[m] >> 9;
-        acc = dot2_bf16(xw[0], (w0 & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xw[1], (w1 & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xw[2], (w2 & kNibHi) | kBfOne2, acc);
-        acc = dot2_bf16(xw[3], (w3 & kNibHi) | kBfOne2, acc);
+        acc = dot2_bf16(xw[0], (w0 & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xw[1], (w1 & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xw[2], (w2 & nibm) | kBfOne2, acc);
+        acc = dot2_bf16(xw[3], (w3 & nibm) | kBfOne2, acc);
       }
       const float2 f = sbt[rl * NGD + min(j, NP - 1) / 2];
       pr += use ? fmaf(f.x, acc, f.y * xh[j]) : 0.0f;
