@@ -735,6 +735,15 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
 #pragma unroll
     for (int r = 0; r < NB; ++r) y[r] = 0.0f;
     const uint32_t* sb = sbl + par * kQR * G;
+    // a group slot's x words (the lane's token row, 2 x 16 bytes), read for the next slot
+    // before the current slot's arithmetic so the LDS latency is off the chain of groups
+    auto ldx = [&](int it, uint4& xa0, uint4& xa1) {
+      const int p = 2 * min(wave + 4 * it, G - 1) + (q >> 1);
+      xa0 = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + 0) * PX + p)]);
+      xa1 = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + 1) * PX + p)]);
+    };
+    uint4 xa0n, xa1n;
+    ldx(0, xa0n, xa1n);
     // the first 8 group slots unconditionally (a group past G re-reads group G - 1 and adds
     // nothing: a select, not a branch), so their LDS reads, unpacking and MFMAs interleave;
     // the slots after them stop at the row's last group (a uniform branch)
@@ -742,16 +751,16 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
     for (int it = 0; it < kGW; ++it) {
       if (it >= 8 && wave + 4 * it >= G) break;
       const int g0 = wave + 4 * it, g = min(g0, G - 1);
-      const int p = 2 * g + (q >> 1);
+      const uint4 xa0 = xa0n, xa1 = xa1n;
+      if (it + 1 < kGW) ldx(it + 1, xa0n, xa1n);
       floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const uint32_t qw = i ? wb.w[it].y : wb.w[it].x;
-        const uint4 xa = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + i) * PX + p)]);
         const uint4 wq = make_uint4(((qw << 3) & nibm) | kBfOne2, ((qw >> 1) & nibm) | kBfOne2,
                                     ((qw >> 5) & nibm) | kBfOne2, ((qw >> 9) & nibm) | kBfOne2);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
-                                                      acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, i ? xa1 : xa0),
+                                                      __builtin_bit_cast(bf16x8, wq), acc, 0, 0, 0);
       }
       const uint32_t sq = sb[g * kQR + n];
       const float sv_ = lo_f(sq), bv_ = hi_f(sq);
@@ -919,25 +928,35 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
     const uint16_t* ss = reinterpret_cast<const uint16_t*>(sl + 16 * 16 * rowc);
     const uint16_t* sbb = ss + 8 * NPr;
     float y = 0.0f;
-    // the first 8 group slots unconditionally (a group past G re-reads group G - 1 and adds
-    // nothing: a select, not a branch), so their LDS reads, unpacking and MFMAs interleave;
-    // the slots after them stop at the row's last group (a uniform branch). The sum over the
-    // wavefront's groups keeps its order.
+    // a group slot's LDS words (its 8 weight bytes and the 2 x 16 bytes of x they meet); the
+    // next slot's are read before the current slot's arithmetic, so the LDS latency is not
+    // on the chain of one group after another
+    auto ld = [&](int it, uint2& w2, uint4& xa0, uint4& xa1) {
+      const int g = min(wave + 4 * it, G - 1);
+      const int p = 2 * g + (q >> 1);
+      w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
+      xa0 = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + 0) * PX + p)]);
+      xa1 = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + 1) * PX + p)]);
+    };
+    uint2 w2n;
+    uint4 xa0n, xa1n;
+    ld(0, w2n, xa0n, xa1n);
+    // every group slot (a slot past G re-reads group G - 1 and adds nothing: a select, not a
+    // branch); the sum over the wavefront's groups keeps its order
 #pragma unroll
     for (int it = 0; it < kGW; ++it) {
-      if (it >= 8 && wave + 4 * it >= G) break;
       const int g0 = wave + 4 * it, g = min(g0, G - 1);
-      const int p = 2 * g + (q >> 1);
-      const uint2 w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
+      const uint2 w2 = w2n;
+      const uint4 xa0 = xa0n, xa1 = xa1n;
+      if (it + 1 < kGW) ld(it + 1, w2n, xa0n, xa1n);
       floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const uint32_t qw = i ? w2.y : w2.x;
-        const uint4 xa = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + i) * PX + p)]);
         const uint4 wq = make_uint4(((qw << 3) & nibm) | kBfOne2, ((qw >> 1) & nibm) | kBfOne2,
                                     ((qw >> 5) & nibm) | kBfOne2, ((qw >> 9) & nibm) | kBfOne2);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, wq),
-                                                      acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, i ? xa1 : xa0),
+                                                      __builtin_bit_cast(bf16x8, wq), acc, 0, 0, 0);
       }
       const float sv_ = bf16_bits_to_f32(ss[n * G + g]), bv_ = bf16_bits_to_f32(sbb[n * G + g]);
       const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
@@ -946,10 +965,11 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
     }
     if (q == 0) red[k & 1][wave][n] = y;
   };
-  // after block k's barrier: wavefront 0 adds the four partials of each row and keeps the
-  // best key, while the others go on to block k + 1 (which writes red[(k + 1) & 1])
+  // after block k's barrier: wavefront k % 4 adds the four partials of each row and keeps the
+  // best key, while the others go on to block k + 1 (which writes red[(k + 1) & 1]); taking
+  // turns keeps one wavefront from running behind the others at every block's barrier
   auto epilogue = [&](int k) {
-    if (wave == 0) {
+    if (wave == (k & 3)) {                              // the wavefronts take turns
       const int o = ((int)blockIdx.x + k * (int)gridDim.x) * kQR + n;
       const bool live = q == 0 && o < O;
       const float v = ((red[k & 1][0][n] + red[k & 1][1][n]) + red[k & 1][2][n]) + red[k & 1][3][n];
@@ -986,8 +1006,15 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
     epilogue(k + 2);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);                  // no ring load outlives the workgroup
-  if (wave == 0 && n == 0 && q == 0) {
-    a.keys[blockIdx.x] = best;
+  // each wavefront's best key (lane 0 holds its blocks' best row), then their maximum
+  __shared__ uint64_t wbest[4];
+  if (lane == 0) wbest[wave] = best;
+  lds_barrier();
+  if (wave == 0 && lane == 0) {
+    uint64_t m = wbest[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = wbest[w] > m ? wbest[w] : m;
+    a.keys[blockIdx.x] = m;
     for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[sl2] = 0;
   }
 }
