@@ -1041,7 +1041,8 @@ def bench_step(args):
     model = Mdl.NemotronModel(cfg, mode="dense" if args.mode == "dense" else "sparse", seed=args.seed)
     prompt = np.random.default_rng(args.seed + 11).integers(0, cfg.vocab, args.prompt).astype(np.int32)
     K = args.steps if args.steps > 0 else 200
-    s = model.session(prompt, mtp=args.mode == "mtp", cap=4 * K + 16)
+    per = 3 if args.mode == "mtp" else 1               # tokens a step can emit
+    s = model.session(prompt, mtp=args.mode == "mtp", cap=per * (K + max(args.warmup, 0)) + 8)
     s.step(max(args.warmup, 0))
     sec = s.step(K)
     log(f"[step] {args.mode}: {1e3 * sec / K:.3f} ms per step over {K} steps after a {len(prompt)}-token prompt")
