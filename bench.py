@@ -172,7 +172,7 @@ def capture_steps(fn_layer, ntok):
     torch.cuda.synchronize()
     for t in range(ntok):
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with N.capture_guard(), torch.cuda.graph(g):
             for l in range(NL):
                 fn_layer(t, l)
         graphs.append(g)
@@ -613,7 +613,7 @@ def bench_mtp(args):
         gs = []
         for i in range(nsteps):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with N.capture_guard(), torch.cuda.graph(g):
                 fn(i)
             gs.append(g)
         return gs
@@ -832,7 +832,7 @@ def empty_launch_us(dev, n, reps=50):
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(s):
+    with torch.cuda.stream(s), N.capture_guard():
         tiny.fill_(0.0)
         with torch.cuda.graph(g, stream=s):
             for i in range(n):

@@ -6,7 +6,9 @@ or a call fails, an exception says so.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import gc
 import os
 
 import torch
@@ -23,6 +25,24 @@ Y_BF16, Y_F32, Y_RESID, Y_ARGMAX = 0, 1, 2, 3
 # sequence state indices (include/hsd.h HSD_SEQ_*)
 SEQ_POS, SEQ_CUR, SEQ_N, SEQ_TOK, SEQ_HEAD_POS, SEQ_R, SEQ_HEAD_POS2, SEQ_ACCEPT, SEQ_STEPS, SEQ_ACC_SUM = range(10)
 SEQ_LEN = 16
+
+
+@contextlib.contextmanager
+def capture_guard():
+    """Python's cyclic garbage collector runs one full pass, then stays off for the body
+    (a stream capture). A dead object that owns a captured graph (a torch CUDAGraph held in
+    a reference cycle) must not be freed while a capture runs: releasing its memory pool is
+    an API call that a global-mode capture prohibits, and the error, raised in a destructor,
+    aborts the process. torch.cuda.graph no longer collects on entry by default."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
 
 _c_int, _c_i64, _c_size, _c_float, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p
 

@@ -605,7 +605,7 @@ class NemotronModel:
         g = torch.cuda.CUDAGraph(keep_graph=keep_graph)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(s):
+        with torch.cuda.stream(s), N.capture_guard():
             with torch.cuda.graph(g, stream=s):
                 fn()
         torch.cuda.current_stream(self.device).wait_stream(s)
@@ -775,8 +775,12 @@ class Session:
         self.prompt_s = time.perf_counter() - t0
         cache.check_status("prefill")
         self.n_bound = 1                  # an upper bound of the emitted count (exact after emitted())
+        # the step closes over the model and the caches, not over the session: a session
+        # dropped by its caller (and the graph it owns) is freed at once, not by the cycle
+        # collector
         if mtp:
-            fn = lambda: model._mtp_step(cache, self.script, self.accepts)
+            script, accepts = self.script, self.accepts
+            fn = lambda: model._mtp_step(cache, script, accepts)
         else:
             fn = lambda: model._decode_step(cache)
         self.step_fn = fn

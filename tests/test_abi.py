@@ -184,3 +184,24 @@ def test_linear_row_length_limits():
                               1, 64, I, None)
     assert call(0, 4160) == -2 and b"at most 4096" in lib.hsd_last_error()
     assert call(1, 6152) == -2 and b"at most 6144" in lib.hsd_last_error()
+
+
+def test_capture_guard_pauses_the_collector():
+    """A stream capture runs with the cycle collector off (after one full pass), and the
+    collector's state is restored afterwards, also when the body raises."""
+    import gc
+    assert gc.isenabled()
+    with N.capture_guard():
+        assert not gc.isenabled()
+    assert gc.isenabled()
+    with pytest.raises(RuntimeError):
+        with N.capture_guard():
+            raise RuntimeError("capture failed")
+    assert gc.isenabled()
+    gc.disable()
+    try:
+        with N.capture_guard():
+            pass
+        assert not gc.isenabled()
+    finally:
+        gc.enable()

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from hsd import decode, layout, mamba as M, prefill, synth as S
+from hsd import _native as N, decode, layout, mamba as M, prefill, synth as S
 from hsd.moe import up_relu2
 
 pytestmark = pytest.mark.gpu
@@ -22,7 +22,7 @@ def capture(fn):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with N.capture_guard(), torch.cuda.graph(g):
         out = fn()
     return g, out
 
@@ -109,7 +109,7 @@ def test_mamba_verify_rollback_graph(dev):
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
+    with torch.cuda.stream(s), N.capture_guard():
         with torch.cuda.graph(g):
             yg = step(mg, cg)      # recorded, not run: the state is still the initial one
     torch.cuda.current_stream().wait_stream(s)

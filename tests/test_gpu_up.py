@@ -83,6 +83,28 @@ def test_up_relu2_matches_oracle(up, dev):
     assert np.array_equal(masks.cpu().numpy().view(np.uint64), masks_of(hb))
 
 
+def test_rows_do_not_depend_on_batch(up, dev):
+    """A token row's h and mask bits are the same in a call of 1, 3 or 6 rows (the shared
+    expert's blocks take tiles of up to 4 rows: at B = 6 a tile of 4 and one of 2)."""
+    lay, dv = up
+    x, sel = inputs(13, 6)
+    args = (dv["w1"], dv["s1"], dv["b1"], dv["sw1"], dv["ss1"], dv["sb1"])
+    nm = (K * F + FS) // 64
+
+    def run(lo, hi):
+        m = torch.zeros((hi - lo) * nm, dtype=torch.int64, device=dev)
+        h = up_relu2(S.to_device(x[lo:hi], dev), S.to_device(sel[lo:hi], dev), *args, topk=K, live_masks=m)
+        return h.view(torch.int16).cpu().numpy(), m.cpu().numpy()
+
+    h6, m6 = run(0, 6)
+    for lo, hi in [(0, 3), (3, 6), (2, 3), (5, 6), (0, 1)]:
+        h, m = run(lo, hi)
+        assert np.array_equal(h, h6[lo:hi]), (lo, hi)
+        assert np.array_equal(m, m6[lo * nm:hi * nm]), (lo, hi)
+    ref = O.up_relu2(x, sel, lay["w1"], lay["s1"], lay["b1"], lay["sw1"], lay["ss1"], lay["sb1"], F=F, FS=FS, topk=K)
+    check(h6.view(np.uint16), ref, x, sel, lay, F, FS, K)
+
+
 def test_bad_expert_id(up, dev):
     lay, dv = up
     x, sel = inputs(7, 1)
