@@ -25,7 +25,7 @@ def up(dev):
     return u, {k: S.to_device(v, dev) for k, v in u.items()}
 
 
-@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("B", [1, 3, 6])
 def test_router_topk_and_front_end(dev, up, B):
     u, ud = up
     rng = np.random.default_rng(40 + B)
