@@ -39,11 +39,10 @@ constexpr int kUpSmallD = 3072;                 // the smaller instance (the ref
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
               "a block is a quarter or an eighth of a mask group; 4 scales and biases per thread");
 // Two instances by the largest D: the register arrays (x words, the lane's weight pieces)
-// are sized for it, so D <= 3072 takes 64 VGPRs and runs 8 wavefronts per SIMD where the
-// 4096 instance takes 74 (6 per SIMD). A single instance for D <= 4096 (96 VGPRs, 5 per
-// SIMD) had made the MTP-2 step 2.221 against 2.196 ms for 72 VGPRs and 7 per SIMD; 8 per
-// SIMD fit once the x rows in LDS took a compile-time pitch (no per-piece address
-// registers).
+// are sized for it, so D <= 3072 runs 7 wavefronts per SIMD (at most 72 VGPRs) and the
+// 4096 instance 6. A single instance for D <= 4096 (96 VGPRs, 5 per SIMD) had made the
+// MTP-2 step 2.221 against 2.196 ms for 72 VGPRs and 7 per SIMD; the x rows in LDS sit at
+// a compile-time pitch (no per-piece address registers).
 template <int MAXD> struct UpShape {
   static constexpr int kMaxP = MAXD / 32;
   static constexpr int kXIt = (MAXD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
