@@ -835,10 +835,11 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
   }
 }
 
-// lm_head at one token row (argmax keys, no logits written): k_linear_q4's arithmetic with
-// the weights streamed into LDS instead of registers. A workgroup keeps a ring of three
-// blocks in flight (direct global-to-LDS loads, no registers held), where the register form
-// holds one: 2 workgroups per CU x 3 blocks against 3 x 1 (LDS: 3 x 24 KB + x). Each ring
+// lm_head at NB = 1 or 3 token rows (argmax keys, no logits written): k_linear_q4's
+// arithmetic with the weights streamed into LDS instead of registers. A workgroup keeps a
+// ring of blocks in flight (direct global-to-LDS loads, no registers held), where the
+// register form holds one: at one row 2 workgroups per CU x 3 slots (LDS: 3 x 24 KB + x), at
+// three rows (the verify) 2 x 2 slots, the x rows taking the third slot's LDS. Each ring
 // slot holds a block's 16 weight rows (a 16-byte pad after each, so the 16 rows of a read
 // fall in different banks), then its scales and biases, 24 loads of 1 KB (6 per wavefront:
 // every wavefront waits on the same counts). A row's instruction sequence, group order and
@@ -850,18 +851,18 @@ constexpr int kRingPerWave = kRingChunks / 64 / 4;  // 1-KB loads per wavefront 
 static_assert(16 * (kRingI / 32 + 1) + 2 * (kRingI / 32) <= kRingChunks && kRingChunks % 256 == 0, "ring slot");
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int XK>
+template <int XK, int NB>
 __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
   constexpr int IMAX = kRingI, PX = IMAX / 32;
   constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
-  __shared__ __attribute__((aligned(16))) uint4 ring0[kRingChunks];
-  __shared__ __attribute__((aligned(16))) uint4 ring1[kRingChunks];
-  __shared__ __attribute__((aligned(16))) uint4 ring2[kRingChunks];
-  __shared__ __attribute__((aligned(16))) uint32_t xp[16 * PX];
-  __shared__ float xg[PX / 2];
-  __shared__ float wsum[1][4];
-  __shared__ float red[2][4][kQR];                     // [block parity][wavefront][row]
+  constexpr int kSlots = NB == 1 ? 3 : 2;              // ring slots
+  static_assert(NB == 1 || NB == 3, "ring instances: one row (decode) and three (verify)");
+  __shared__ __attribute__((aligned(16))) uint4 ring[kSlots][kRingChunks];
+  __shared__ __attribute__((aligned(16))) uint32_t xp[NB * 16 * PX];
+  __shared__ float xg[NB * (PX / 2)];
+  __shared__ float wsum[NB][4];
+  __shared__ float red[2][4][NB][kQR];                 // [block parity][wavefront][token row][row]
   const int I = a.I, O = a.O, G = I / 64, NPr = I / 32, rowc = NPr + 1;
   // the wavefront index as a scalar: the group loops below branch on it uniformly (a
   // vector index made each group an exec-masked branch, serialising the groups)
@@ -913,21 +914,23 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
     }
   };
 
-  // ---- prologue: x, the first three blocks, x into LDS
-  XIn<HSD_W_Q4, 1, XK, XIT, PX> xin;
+  // ---- prologue: x, the first blocks (one per slot), x into LDS
+  XIn<HSD_W_Q4, NB, XK, XIT, PX> xin;
   xin.load(a, tid);
-  issue(0, ring0);
-  issue(1, ring1);
-  issue(2, ring2);
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) issue(k, ring[k]);
   xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
 
-  uint64_t best = 0;
+  uint64_t best = 0;                                   // lanes of token row l / 16
+  const int arow = min(n, NB - 1);                     // the token row of this lane's A operand
   // block k from a slot: the wavefront's groups, its partial sums into red[k & 1]
   auto compute = [&](int k, const uint4* slot) {
     const char* sl = reinterpret_cast<const char*>(slot);
     const uint16_t* ss = reinterpret_cast<const uint16_t*>(sl + 16 * 16 * rowc);
     const uint16_t* sbb = ss + 8 * NPr;
-    float y = 0.0f;
+    float y[NB];
+#pragma unroll
+    for (int r = 0; r < NB; ++r) y[r] = 0.0f;
     // a group slot's LDS words (its 8 weight bytes and the 2 x 16 bytes of x they meet); the
     // next slot's are read before the current slot's arithmetic, so the LDS latency is not
     // on the chain of one group after another
@@ -935,8 +938,8 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
       const int g = min(wave + 4 * it, G - 1);
       const int p = 2 * g + (q >> 1);
       w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
-      xa0 = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + 0) * PX + p)]);
-      xa1 = *reinterpret_cast<const uint4*>(&xp[4 * ((2 * (q & 1) + 1) * PX + p)]);
+      xa0 = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + 0) * PX + p)]);
+      xa1 = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + 1) * PX + p)]);
     };
     uint2 w2n;
     uint4 xa0n, xa1n;
@@ -960,10 +963,17 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
       }
       const float sv_ = bf16_bits_to_f32(ss[n * G + g]), bv_ = bf16_bits_to_f32(sbb[n * G + g]);
       const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
-      const float yn = y + fmaf(s16, acc[0], bo * xg[g]);
-      y = g0 < G ? yn : y;
+#pragma unroll
+      for (int r = 0; r < NB; ++r) {
+        const float yn = y[r] + fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
+        y[r] = g0 < G ? yn : y[r];
+      }
     }
-    if (q == 0) red[k & 1][wave][n] = y;
+    // lanes 0..15 hold token rows 0..3 of output row n (acc[r]: token row 4 (l / 16) + r)
+    if (q == 0) {
+#pragma unroll
+      for (int r = 0; r < NB; ++r) red[k & 1][wave][r][n] = y[r];
+    }
   };
   // after block k's barrier: wavefront k % 4 adds the four partials of each row and keeps the
   // best key, while the others go on to block k + 1 (which writes red[(k + 1) & 1]); taking
@@ -971,51 +981,49 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
   auto epilogue = [&](int k) {
     if (wave == (k & 3)) {                              // the wavefronts take turns
       const int o = ((int)blockIdx.x + k * (int)gridDim.x) * kQR + n;
-      const bool live = q == 0 && o < O;
-      const float v = ((red[k & 1][0][n] + red[k & 1][1][n]) + red[k & 1][2][n]) + red[k & 1][3][n];
+      const int m = min(q, NB - 1);                      // token row of this lane
+      const bool live = q < NB && o < O;
+      const float v = ((red[k & 1][0][m][n] + red[k & 1][1][m][n]) + red[k & 1][2][m][n]) + red[k & 1][3][m][n];
       uint64_t key = live ? argmax_key(f32_to_bf16_bits(v), o) : 0;
       key = row16_max_u64(key);
       best = key > best ? key : best;
     }
   };
   // the end of block k: this wavefront's loads of block k + 1 in (a wavefront's ring loads
-  // complete in issue order, 6 per block: at most block k + 2's may be outstanding, when it
-  // was issued), then one barrier: every wavefront's part of block k + 1 is in, the slot of
-  // block k is free and red[k & 1] complete
+  // complete in issue order, 6 per block; with three slots block k + 2's may be outstanding,
+  // when it was issued), then one barrier: every wavefront's part of block k + 1 is in, the
+  // slot of block k is free and red[k & 1] complete
   auto end_block = [&](int k) {
-    if (k + 2 <= 2 || k + 2 < nmine) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
-    else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
+    if (kSlots == 3 && (k + 2 <= 2 || k + 2 < nmine)) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                                             // vmcnt(0)
     lds_barrier();
   };
-  __builtin_amdgcn_s_waitcnt(0x0F7C);                  // vmcnt(12): block 0 in
+  if constexpr (kSlots == 3)
+    __builtin_amdgcn_s_waitcnt(0x0F7C);                // vmcnt(12): block 0 in
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F76);                // vmcnt(6): block 0 in
   lds_barrier();                                       // x and block 0 in LDS
-  for (int k = 0; k < nmine; k += 3) {
-    compute(k, ring0);
-    end_block(k);
-    if (k + 3 < nmine) issue(k + 3, ring0);
-    epilogue(k);
-    if (k + 1 >= nmine) break;
-    compute(k + 1, ring1);
-    end_block(k + 1);
-    if (k + 4 < nmine) issue(k + 4, ring1);
-    epilogue(k + 1);
-    if (k + 2 >= nmine) break;
-    compute(k + 2, ring2);
-    end_block(k + 2);
-    if (k + 5 < nmine) issue(k + 5, ring2);
-    epilogue(k + 2);
+  for (int k = 0; k < nmine; k += kSlots) {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      if (i > 0 && k + i >= nmine) break;
+      compute(k + i, ring[i]);
+      end_block(k + i);
+      if (k + i + kSlots < nmine) issue(k + i + kSlots, ring[i]);
+      epilogue(k + i);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);                  // no ring load outlives the workgroup
-  // each wavefront's best key (lane 0 holds its blocks' best row), then their maximum
-  __shared__ uint64_t wbest[4];
-  if (lane == 0) wbest[wave] = best;
+  // each wavefront's best key per token row (lane 16 m holds row m's), then their maximum
+  __shared__ uint64_t wbest[4][NB];
+  if (n == 0 && q < NB) wbest[wave][q] = best;
   lds_barrier();
-  if (wave == 0 && lane == 0) {
-    uint64_t m = wbest[0];
+  if (wave == 0 && lane < NB) {
+    uint64_t m = wbest[0][lane];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) m = wbest[w] > m ? wbest[w] : m;
-    a.keys[blockIdx.x] = m;
-    for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[sl2] = 0;
+    for (int w = 1; w < 4; ++w) m = wbest[w][lane] > m ? wbest[w][lane] : m;
+    a.keys[lane * a.key_ld + blockIdx.x] = m;
+    for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[lane * a.key_ld + sl2] = 0;
   }
 }
 
@@ -1196,12 +1204,21 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     case kZR: HSD_Q4_I(NB, HSD_X_GATED_Z, HSD_Y_RESID); break;         \
     default: HSD_Q4_I(NB, HSD_X_BF16, HSD_Y_RESID); break;             \
   }
-  // one token row of argmax keys with no logits (the decode step's lm_head): the LDS ring
-  const bool ring = mfma && B == 1 && pair == kRA && !y && I <= kRingI && O % kQR == 0;
+  // one or three token rows of argmax keys with no logits (the decode and verify steps'
+  // lm_head): the LDS ring
+  const bool ring = mfma && (B == 1 || B == 3) && pair == kRA && !y && I <= kRingI && O % kQR == 0;
   if (ring) {
-    const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS>);
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, 0, kLMaxGrid)));
-    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS>), dim3(g), dim3(kLT), 0, st, a);
+#define HSD_RING(NB)                                                                          \
+  {                                                                                           \
+    const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS, NB>);                \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, 0, kLMaxGrid)));    \
+    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB>), dim3(g), dim3(kLT), 0, st, a);             \
+  }
+    if (B == 1)
+      HSD_RING(1)
+    else
+      HSD_RING(3)
+#undef HSD_RING
   } else if (mfma) {
     switch (B) {
       case 1: HSD_Q4_P(1); break;

@@ -130,10 +130,11 @@ def test_many_blocks_matrix_core_path(dev, I):
 
 @pytest.mark.parametrize("I,O_", [(2688, 131072), (2688, 33024), (1024, 40960)])
 def test_one_row_argmax_ring(dev, I, O_):
-    """One token row of argmax keys with no logits (the decode step's lm_head) takes the
-    LDS-ring kernel: its token equals the first argmax of the same row's bf16 logits from
-    the register kernel (and of the oracle's), alone and among three rows; equal logits
-    give the smallest index; a NaN logit wins; xn_out equals the three-row call's."""
+    """One or three token rows of argmax keys with no logits (the decode and verify steps'
+    lm_head) take the LDS-ring kernel: each row's token equals the first argmax of the same
+    row's bf16 logits from the register kernel (and of the oracle's), alone and among three
+    rows; equal logits give the smallest index; a NaN logit wins; every key slot is
+    written; xn_out equals the three-row call's."""
     (w, s, b), W = q4_weight(71 + O_, O_, I, dev)
     rng = np.random.default_rng(72)
     nwd = S.to_device(O.f32_to_bf16(rng.uniform(0.5, 1.5, I).astype(np.float32)), dev)
@@ -141,8 +142,9 @@ def test_one_row_argmax_ring(dev, I, O_):
     slots = nn.argmax_slots(O_)
     xn3 = torch.empty((3, I), dtype=torch.bfloat16, device=dev)
     y3 = nn.linear(xd, W, norm=nwd, xn_out=xn3)                      # bf16 logits, 3 rows
-    keys3 = torch.empty((3, slots), dtype=torch.int64, device=dev)
+    keys3 = torch.full((3, slots), -1, dtype=torch.int64, device=dev)
     nn.linear(xd, W, norm=nwd, argmax_keys=keys3)
+    assert int((keys3 == -1).sum().item()) == 0
     tok3 = nn.argmax(keys3).cpu().numpy().tolist()
     want = O.argmax_bf16(y3.float().cpu().numpy()).tolist()
     assert tok3 == want
@@ -162,10 +164,14 @@ def test_one_row_argmax_ring(dev, I, O_):
     keys = torch.empty((1, slots), dtype=torch.int64, device=dev)
     nn.linear(xd[:1], Wt, norm=nwd, argmax_keys=keys)
     assert int(nn.argmax(keys).item()) == 0
+    nn.linear(xd, Wt, norm=nwd, argmax_keys=keys3)
+    assert nn.argmax(keys3).cpu().numpy().tolist() == [0, 0, 0]
     st[O_ - 3, 1] = 0x7FC0
     Wt = nn.QWeight(S.to_device(wt, dev), S.to_device(st, dev), S.to_device(bt, dev))
     nn.linear(xd[:1], Wt, norm=nwd, argmax_keys=keys)
     assert int(nn.argmax(keys).item()) == O_ - 3
+    nn.linear(xd, Wt, norm=nwd, argmax_keys=keys3)
+    assert nn.argmax(keys3).cpu().numpy().tolist() == [O_ - 3] * 3
 
 
 def test_residual_epilogue(dev):
