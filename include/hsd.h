@@ -298,6 +298,28 @@ int hsd_draft_ids(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots
                   int32_t* seq, const int32_t* script, int64_t script_len, const int32_t* accepts,
                   int64_t n_accepts, int64_t V, int32_t* ids, void* stream);
 
+/* The MTP head's input in one launch (hsd_embed_q4 then hsd_pair_norm, the same bits):
+ * out[b] = concat(rms_norm(embed(t_b), we), rms_norm(h[b], wh)), [B, 2D] bf16, t_b = tok[b]
+ * (mtp.py:81-83 with the head's token embedding, model.py:223-224). With tok NULL (the
+ * chained call of hsd/model.py:408-414, B = 1): t = the argmax of argmax_keys (slots keys,
+ * hsd_linear's HSD_Y_ARGMAX for the selected row), d1[0] = t and seq[HSD_SEQ_HEAD_POS2] =
+ * HEAD_POS + R as hsd_mtp_chain does, h being that row's normed hidden row. A token outside
+ * [0, V) embeds as zeros and sets HSD_STATUS_BAD_TOKEN. D % 64 == 0. */
+int hsd_head_input(const int32_t* tok, const uint64_t* argmax_keys, int64_t slots, const uint32_t* w,
+                   const uint16_t* scales, const uint16_t* biases, int64_t V, const uint16_t* h,
+                   int64_t h_ld, const uint16_t* we, const uint16_t* wh, float eps, int64_t B, int64_t D,
+                   int32_t* seq, int32_t* d1, uint16_t* out, int64_t out_ld, int32_t* dev_status,
+                   void* stream);
+
+/* hsd_draft_ids and the embedding of the k + 1 verify rows in one launch (model.py:416 and
+ * 223-224): ids as hsd_draft_ids, out[r] = hsd_embed_q4 of ids[r] (out 16-byte aligned,
+ * out_ld % 8 == 0, D % 64 == 0). */
+int hsd_verify_input(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots, int64_t k,
+                     int32_t* seq, const int32_t* script, int64_t script_len, const int32_t* accepts,
+                     int64_t n_accepts, int64_t V, const uint32_t* w, const uint16_t* scales,
+                     const uint16_t* biases, int64_t D, int32_t* ids, uint16_t* out, int64_t out_ld,
+                     int32_t* dev_status, void* stream);
+
 /* dst[i] = src[clamp(POS + offset + i, 0, n-1)] for i < count: the next rows of a prompt
  * held on the device, so a prefill step (model.py:259-279, here in steps of a few rows)
  * replays as one graph. */

@@ -4,6 +4,10 @@
 //   k_embed_q4       the quantised token embedding (mlx QuantizedEmbedding, model.py:223)
 //   k_pair_norm      concat(rms_norm(e, enorm), rms_norm(h, hnorm)): the MTP head's input
 //                    (mtp.py:81-83)
+//   k_head_in        the two above in one launch (the head's token rows embedded and
+//                    normed in place), or for the head's chained call with the chaining
+//                    of k_mtp_chain in front
+//   k_verify_in      k_draft and the verify rows' embedding in one launch
 //   k_decode_advance argmax of the last row + the sequence state after a plain step
 //   k_spec_accept    greedy acceptance of a verify step + the rollback of every cache
 //   k_mtp_chain      the inputs of the MTP head's chained call (mtp.py, model.py:408-414)
@@ -21,12 +25,9 @@ namespace {
 // out[b, i] = bf16(s[t, i/64] * q[t, i] + b[t, i/64]), t = tok[b] (one workgroup per row;
 // thread = 8 outputs = one word). A token outside [0, V) gives a zero row and the status
 // bit HSD_STATUS_BAD_TOKEN.
-__global__ __launch_bounds__(256) void k_embed_q4(const int32_t* __restrict__ tok, const uint32_t* __restrict__ w,
-                                                  const uint16_t* __restrict__ s, const uint16_t* __restrict__ bq,
-                                                  int V, int D, uint16_t* __restrict__ out, int64_t out_ld,
-                                                  int32_t* __restrict__ status) {
-  const int b = blockIdx.x;
-  const int t = tok[b];
+__device__ __forceinline__ void embed_row(int t, const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                          const uint16_t* __restrict__ bq, int V, int D, uint16_t* __restrict__ orow,
+                                          int32_t* __restrict__ status) {
   const bool ok = (unsigned)t < (unsigned)V;
   const size_t row = ok ? (size_t)t : 0;
   // passes of 4 words per thread, each pass's loads issued before they are used
@@ -55,36 +56,70 @@ __global__ __launch_bounds__(256) void k_embed_q4(const int32_t* __restrict__ to
         const uint32_t hi = ok ? f32_to_bf16_bits(fmaf(sc, (float)((q >> (8 * c + 4)) & 0xFu), bi)) : 0u;
         o[c] = lo | (hi << 16);
       }
-      if (wi < NW) reinterpret_cast<uint4*>(out + (size_t)b * out_ld)[wi] = make_uint4(o[0], o[1], o[2], o[3]);
+      if (wi < NW) reinterpret_cast<uint4*>(orow)[wi] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
   if (!ok && threadIdx.x == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_TOKEN);
 }
 
+__global__ __launch_bounds__(256) void k_embed_q4(const int32_t* __restrict__ tok, const uint32_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ s, const uint16_t* __restrict__ bq,
+                                                  int V, int D, uint16_t* __restrict__ out, int64_t out_ld,
+                                                  int32_t* __restrict__ status) {
+  const int b = blockIdx.x;
+  embed_row(tok[b], w, s, bq, V, D, out + (size_t)b * out_ld, status);
+}
+
 // ---------------------------------------------------------------- pair norm
-// out[b, :D] = rms_norm(e[b], w_e), out[b, D:] = rms_norm(h[b], w_h), each
-// bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w). One workgroup (256 threads) per row and half.
-__global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ e, int64_t e_ld,
-                                                   const uint16_t* __restrict__ h, int64_t h_ld,
-                                                   const uint16_t* __restrict__ we, const uint16_t* __restrict__ wh,
-                                                   float eps, int D, uint16_t* __restrict__ out, int64_t out_ld) {
-  __shared__ float wsum[4];
-  const int b = blockIdx.x >> 1, half = blockIdx.x & 1;
-  const uint16_t* x = half ? h + (size_t)b * h_ld : e + (size_t)b * e_ld;
-  const uint16_t* w = half ? wh : we;
-  // a pass of 16 elements per thread: every load issued before the first is used (a loop
-  // with one load per step waits for each in turn); the sum keeps the element order
+// One row's rms_norm by one 256-thread workgroup: o[i] = bf16(bf16(x_i * rsqrt(mean(x^2) +
+// eps)) * w_i), x_i the bf16 value src gives for element i. A pass of 16 elements per
+// thread: every load issued before the first is used (a loop with one load per step waits
+// for each in turn); the sum keeps the element order.
+struct RowBf16 {                                       // a bf16 row in memory
+  const uint16_t* p;
+  struct Raw {
+    uint16_t v;
+  };
+  __device__ __forceinline__ Raw load(int i) const { return {p[i]}; }
+  __device__ __forceinline__ uint16_t bits(const Raw& r, int) const { return r.v; }
+};
+struct RowEmbed {                                      // row `row` of the 4-bit embedding, as k_embed_q4 writes it
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  size_t row;
+  int D;
+  bool ok;
+  struct Raw {
+    uint32_t q;
+    uint16_t s, b;
+  };
+  __device__ __forceinline__ Raw load(int i) const {
+    return {w[row * (D / 8) + i / 8], s[row * (D / 64) + i / 64], b[row * (D / 64) + i / 64]};
+  }
+  __device__ __forceinline__ uint16_t bits(const Raw& r, int i) const {
+    // element i is nibble i % 8 of word i / 8 (k_embed_q4: bits 8c and 8c + 4 of a word
+    // are elements 2c and 2c + 1)
+    return ok ? f32_to_bf16_bits(fmaf(bf16_bits_to_f32(r.s), (float)((r.q >> (4 * (i & 7))) & 0xFu),
+                                      bf16_bits_to_f32(r.b)))
+              : (uint16_t)0;
+  }
+};
+template <class Src>
+__device__ __forceinline__ void rms_norm_row(const Src& x, const uint16_t* __restrict__ w, float eps, int D,
+                                             uint16_t* __restrict__ o, float* wsum) {
   constexpr int kIt = 16;
   float ss = 0.0f;
   for (int p0 = 0; p0 < D; p0 += 256 * kIt) {
-    uint16_t v[kIt];
+    typename Src::Raw v[kIt];
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) v[it] = x[min(p0 + (int)threadIdx.x + 256 * it, D - 1)];
+    for (int it = 0; it < kIt; ++it) v[it] = x.load(min(p0 + (int)threadIdx.x + 256 * it, D - 1));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const float f = p0 + (int)threadIdx.x + 256 * it < D ? bf16_bits_to_f32(v[it]) : 0.0f;
-      ss = p0 + (int)threadIdx.x + 256 * it < D ? fmaf(f, f, ss) : ss;
+      const int i = p0 + (int)threadIdx.x + 256 * it;
+      const float f = i < D ? bf16_bits_to_f32(x.bits(v[it], i)) : 0.0f;
+      ss = i < D ? fmaf(f, f, ss) : ss;
     }
   }
   ss = wave_sum_dpp(ss);
@@ -92,23 +127,35 @@ __global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ 
   __syncthreads();
   const float tot = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
   const float inv = __builtin_amdgcn_rsqf(tot / (float)D + eps);
-  uint16_t* o = out + (size_t)b * out_ld + half * D;
   for (int p0 = 0; p0 < D; p0 += 256 * kIt) {
-    uint16_t xv[kIt], wv[kIt];
+    typename Src::Raw xv[kIt];
+    uint16_t wv[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int i = min(p0 + (int)threadIdx.x + 256 * it, D - 1);
-      xv[it] = x[i];
+      xv[it] = x.load(i);
       wv[it] = w[i];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int i = p0 + (int)threadIdx.x + 256 * it;
-      const float t = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(xv[it]) * inv));
+      const float t = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(x.bits(xv[it], min(i, D - 1))) * inv));
       if (i < D) o[i] = f32_to_bf16_bits(t * bf16_bits_to_f32(wv[it]));
     }
   }
+}
+
+// out[b, :D] = rms_norm(e[b], w_e), out[b, D:] = rms_norm(h[b], w_h). One workgroup
+// (256 threads) per row and half.
+__global__ __launch_bounds__(256) void k_pair_norm(const uint16_t* __restrict__ e, int64_t e_ld,
+                                                   const uint16_t* __restrict__ h, int64_t h_ld,
+                                                   const uint16_t* __restrict__ we, const uint16_t* __restrict__ wh,
+                                                   float eps, int D, uint16_t* __restrict__ out, int64_t out_ld) {
+  __shared__ float wsum[4];
+  const int b = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const uint16_t* x = half ? h + (size_t)b * h_ld : e + (size_t)b * e_ld;
+  rms_norm_row(RowBf16{x}, half ? wh : we, eps, D, out + (size_t)b * out_ld + half * D, wsum);
 }
 
 // dst[i] = src[i] for i < n by one 256-thread workgroup, each pass's loads issued before
@@ -262,6 +309,90 @@ __global__ __launch_bounds__(64) void k_draft(const int32_t* __restrict__ d1, co
   }
 }
 
+// The MTP head's input rows in one launch: out[b, :D] = rms_norm(embed(t_b), w_e),
+// out[b, D:] = rms_norm(h[b], w_h) (k_embed_q4 then k_pair_norm, the same arithmetic; one
+// workgroup per row and half). t_b = tok[b]; without tok (the chained call, B = 1) t is the
+// argmax of `keys` and the chaining of k_mtp_chain happens here: d1[0] = t and HEAD_POS2 =
+// HEAD_POS + R (R = seq[HSD_SEQ_R] clamped to [1, 3]); h is then the normed hidden row.
+__global__ __launch_bounds__(256) void k_head_in(const int32_t* __restrict__ tok, const uint64_t* __restrict__ keys,
+                                                 int slots, const uint32_t* __restrict__ ew,
+                                                 const uint16_t* __restrict__ es, const uint16_t* __restrict__ eb,
+                                                 int V, const uint16_t* __restrict__ h, int64_t h_ld,
+                                                 const uint16_t* __restrict__ we, const uint16_t* __restrict__ wh,
+                                                 float eps, int D, int32_t* __restrict__ seq, int32_t* __restrict__ d1,
+                                                 uint16_t* __restrict__ out, int64_t out_ld,
+                                                 int32_t* __restrict__ status) {
+  __shared__ float wsum[4];
+  __shared__ int tsh;
+  const int b = blockIdx.x >> 1, half = blockIdx.x & 1;
+  uint16_t* o = out + (size_t)b * out_ld + half * D;
+  if (half) {
+    rms_norm_row(RowBf16{h + (size_t)b * h_ld}, wh, eps, D, o, wsum);
+    return;
+  }
+  int t;
+  if (tok) {
+    t = tok[b];
+  } else {
+    if (threadIdx.x < 64) {
+      const int a = wave_argmax_keys(keys, slots, threadIdx.x);
+      if (threadIdx.x == 0) {
+        tsh = a;
+        d1[0] = a;
+        const int r = min(max(seq[HSD_SEQ_R], 1), 3) - 1;
+        seq[HSD_SEQ_HEAD_POS2] = seq[HSD_SEQ_HEAD_POS] + r + 1;
+      }
+    }
+    __syncthreads();
+    t = tsh;
+  }
+  const bool ok = (unsigned)t < (unsigned)V;
+  rms_norm_row(RowEmbed{ew, es, eb, ok ? (size_t)t : 0, D, ok}, we, eps, D, o, wsum);
+  if (!ok && threadIdx.x == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_TOKEN);
+}
+
+// k_draft and the embedding of the verify rows in one launch: workgroup r takes row r of
+// [tok, d_0 .. d_{k-1}] (k_draft's rule, each workgroup for its own row: only the row of
+// the chained call's draft ranks keys2), writes ids[r] and embeds it (k_embed_q4's rows).
+__global__ __launch_bounds__(256) void k_verify_in(const int32_t* __restrict__ d1, const uint64_t* __restrict__ keys2,
+                                                   int slots, int k, int32_t* __restrict__ seq,
+                                                   const int32_t* __restrict__ script, int script_len,
+                                                   const int32_t* __restrict__ accepts, int n_accepts, int V,
+                                                   const uint32_t* __restrict__ ew, const uint16_t* __restrict__ es,
+                                                   const uint16_t* __restrict__ eb, int D, int32_t* __restrict__ ids,
+                                                   uint16_t* __restrict__ out, int64_t out_ld,
+                                                   int32_t* __restrict__ status) {
+  __shared__ int tsh;
+  const int r = blockIdx.x;                            // 0: TOK, i = r - 1 >= 0: draft i
+  if (threadIdx.x < 64) {
+    int t;
+    if (r == 0) {
+      t = seq[HSD_SEQ_TOK];
+    } else {
+      const int i = r - 1;
+      if (script) {
+        const int n = seq[HSD_SEQ_N];
+        const int st = seq[HSD_SEQ_STEPS];
+        const int at = accepts ? accepts[min(st, n_accepts - 1)] : k;
+        const int tt = script[min(n + i, script_len - 1)];
+        t = i < at ? tt : (i == at ? (tt + 1) % V : tt);
+      } else if (i == 0) {
+        t = d1 ? d1[0] : 0;
+      } else if (i == 1) {
+        t = wave_argmax_keys(keys2, slots, threadIdx.x);
+      } else {
+        t = 0;
+      }
+    }
+    if (threadIdx.x == 0) {
+      tsh = t;
+      ids[r] = t;
+    }
+  }
+  __syncthreads();
+  embed_row(tsh, ew, es, eb, V, D, out + (size_t)r * out_ld, status);
+}
+
 // dst[i] = src[clamp(POS + offset + i, 0, n - 1)]: the next rows' tokens of a prompt held
 // on the device (a prefill step replays as one graph).
 __global__ void k_gather_tokens(const int32_t* __restrict__ src, int n, const int32_t* __restrict__ seq,
@@ -384,6 +515,42 @@ extern "C" int hsd_draft_ids(const int32_t* d1, const uint64_t* argmax_keys2, in
     return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
   hipLaunchKernelGGL(k_draft, dim3(1), dim3(64), 0, as_stream(stream), d1, argmax_keys2, (int)slots, (int)k, seq,
                      script, (int)script_len, accepts, (int)n_accepts, (int)V, ids);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_head_input(const int32_t* tok, const uint64_t* argmax_keys, int64_t slots, const uint32_t* w,
+                              const uint16_t* scales, const uint16_t* biases, int64_t V, const uint16_t* h,
+                              int64_t h_ld, const uint16_t* we, const uint16_t* wh, float eps, int64_t B, int64_t D,
+                              int32_t* seq, int32_t* d1, uint16_t* out, int64_t out_ld, int32_t* dev_status,
+                              void* stream) {
+  const char* fn = "hsd_head_input";
+  if (!w || !scales || !biases || !h || !we || !wh || !out) return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (!tok && (!argmax_keys || !seq || !d1))
+    return set_error(HSD_ERR_ARG, "%s: without tok, argmax_keys, seq and d1 are needed", fn);
+  if (B < 0 || B > 65535 || (!tok && B != 1) || V <= 0 || V > 0x7FFFFFFF || D <= 0 || D % 64 || h_ld < D ||
+      out_ld < 2 * D || (!tok && (slots <= 0 || slots > (1 << 30))))
+    return set_error(HSD_ERR_SHAPE, "%s: need D %% 64 == 0, row strides h_ld >= D and out_ld >= 2 D, B == 1 without tok",
+                     fn);
+  if (B == 0) return HSD_OK;
+  hipLaunchKernelGGL(k_head_in, dim3((unsigned)(2 * B)), dim3(256), 0, as_stream(stream), tok, argmax_keys, (int)slots,
+                     w, scales, biases, (int)V, h, h_ld, we, wh, eps, (int)D, seq, d1, out, out_ld, dev_status);
+  return check_launch(fn);
+}
+
+extern "C" int hsd_verify_input(const int32_t* d1, const uint64_t* argmax_keys2, int64_t slots, int64_t k, int32_t* seq,
+                                const int32_t* script, int64_t script_len, const int32_t* accepts, int64_t n_accepts,
+                                int64_t V, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int64_t D,
+                                int32_t* ids, uint16_t* out, int64_t out_ld, int32_t* dev_status, void* stream) {
+  const char* fn = "hsd_verify_input";
+  if (!seq || !ids || !w || !scales || !biases || !out || (k >= 2 && !script && !argmax_keys2))
+    return set_error(HSD_ERR_ARG, "%s: null pointer", fn);
+  if (k < 1 || k > 7 || V <= 0 || V > 0x7FFFFFFF || (script && script_len <= 0) || (accepts && n_accepts <= 0) ||
+      (argmax_keys2 && slots <= 0) || D <= 0 || D % 64 || out_ld < D || out_ld % 8)
+    return set_error(HSD_ERR_SHAPE, "%s: bad sizes", fn);
+  if ((uintptr_t)out & 15u) return set_error(HSD_ERR_ALIGN, "%s: out must be 16-byte aligned", fn);
+  hipLaunchKernelGGL(k_verify_in, dim3((unsigned)(k + 1)), dim3(256), 0, as_stream(stream), d1, argmax_keys2,
+                     (int)slots, (int)k, seq, script, (int)script_len, accepts, (int)n_accepts, (int)V, w, scales,
+                     biases, (int)D, ids, out, out_ld, dev_status);
   return check_launch(fn);
 }
 

@@ -97,6 +97,10 @@ _SIGS = {
     "hsd_seq_select_row": (_c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _vp]),
     "hsd_mtp_chain": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "hsd_draft_ids": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp]),
+    "hsd_head_input": (_c_int, [_vp, _vp, _c_i64, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_float, _c_i64,
+                                _c_i64, _vp, _vp, _vp, _c_i64, _vp, _vp]),
+    "hsd_verify_input": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp,
+                                  _c_i64, _vp, _vp, _c_i64, _vp, _vp]),
     "hsd_seq_add": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "hsd_gather_tokens": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp]),
     "hsd_prefill_advance": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp]),

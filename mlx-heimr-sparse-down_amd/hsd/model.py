@@ -540,15 +540,17 @@ class NemotronModel:
         return out
 
     # ---- the MTP head forward (mtp.py:74-88)
-    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None, status=None):
+    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None, status=None, chain=None):
         """Head rows: h [B, D] (the target's pre-norm hidden), toks [B] int32 (the token
         after each row's position) at positions pos .. pos+B-1 of the head's KV cache kv.
         Leaves the normed hidden rows in buf["hn"] and (with keys) the argmax keys of the
-        head's logits."""
+        head's logits. chain = (keys, seq, d1): the chained call, its token the argmax of
+        those keys and h the selected row's normed hidden row (nn.head_input)."""
         B = h.shape[0]
         hd, c = self.mtp, self.cfg
-        e = self.embed(toks, out=buf["emb"][:B], status=status)
-        pair = nn.pair_norm(e, h, hd.enorm, hd.hnorm, eps=c.eps, out=buf["pair"][:B])
+        # the token embedding and the pair norm in one launch
+        pair = nn.head_input(toks, h, self.embedding, hd.enorm, hd.hnorm, eps=c.eps, out=buf["pair"][:B],
+                             status=status, chain=chain)
         x = nn.linear(pair, hd.eh_proj, out=buf["hx"][:B])
         hd.attn.rows(x, buf, kv, pos, status=status)
         hd.moe.rows(x, buf, dense=self.mode == "dense", status=status)
@@ -695,17 +697,19 @@ class NemotronModel:
         N.call("hsd_seq_select_row", N.ptr(x3), x3.stride(0), N.ptr(cache.seq), N.ptr(b1["x1"]), c.hidden, st)
         nn.linear(b1["x1"], self.lm_head, norm=self.mtp.final_norm, eps=c.eps, argmax_keys=b1["keys1"],
                   xn_out=b1["hn1"])
-        N.call("hsd_mtp_chain", N.ptr(b1["keys1"]), 0, self.slots, N.ptr(b1["hn1"]), 0, c.hidden, N.ptr(cache.seq),
-               N.ptr(b3["d1"]), N.ptr(b1["h2"]), st)
-        # the chained call on its own normed hidden row (mtp.py, model.py:411-413)
-        self.mtp_rows(b1["h2"], b3["d1"][:1], b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"],
-                      status=cache.status)
+        # the chained call on its own normed hidden row (mtp.py, model.py:411-413); its input
+        # launch also takes the first draft from keys1 (d1) and the cache row (HEAD_POS2)
+        self.mtp_rows(b1["hn1"], None, b1, cache.head_kv, cache.head_pos2, keys=b1["keys2"], status=cache.status,
+                      chain=(b1["keys1"], cache.seq, b3["d1"]))
+        # verify [tok, d1, d2] in one pass of 3 rows, then accept and roll back on the device;
+        # one launch writes the ids and their embedding rows
         ids = b3["ids"]
-        N.call("hsd_draft_ids", N.ptr(b3["d1"]), N.ptr(b1["keys2"]), self.slots, 2, N.ptr(cache.seq),
+        emb = self.embedding
+        N.call("hsd_verify_input", N.ptr(b3["d1"]), N.ptr(b1["keys2"]), self.slots, 2, N.ptr(cache.seq),
                N.ptr(script), 0 if script is None else script.numel(), N.ptr(accepts),
-               0 if accepts is None else accepts.numel(), c.vocab, N.ptr(ids), st)
-        # verify [tok, d1, d2] in one pass of 3 rows, then accept and roll back on the device
-        x = self.embed(ids[:3], out=b3["x"], status=cache.status)
+               0 if accepts is None else accepts.numel(), c.vocab, N.ptr(emb.w), N.ptr(emb.scales),
+               N.ptr(emb.biases), c.hidden, N.ptr(ids), N.ptr(b3["x"]), b3["x"].stride(0), N.ptr(cache.status), st)
+        x = b3["x"][:3]
         self.layers(x, b3, cache)
         self.head_keys(x, b3, b3["keys"])
         N.call("hsd_spec_accept", N.ptr(b3["keys"]), b3["keys"].stride(0), self.slots, 2, N.ptr(ids),

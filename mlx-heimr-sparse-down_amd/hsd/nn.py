@@ -132,6 +132,22 @@ def pair_norm(e, h, we, wh, eps=1e-5, out=None):
     return out
 
 
+def head_input(tok, h, W: QWeight, we, wh, eps=1e-5, out=None, status=None, chain=None):
+    """concat(rms_norm(embed(tok), we), rms_norm(h, wh)) -> [B, 2D] bf16 in one launch
+    (embed then pair_norm, the same bits; mtp.py:81-83 on the head's token rows). chain =
+    (keys [1, slots] int64, seq, d1 [>= 1] int32): the chained call (model.py:408-414), tok
+    unused: the token is the argmax of keys, written to d1[0], and seq's HEAD_POS2 advances as
+    hsd_mtp_chain does; h is then the selected row's normed hidden row [1, D]."""
+    B, D = h.shape
+    out = out if out is not None else torch.empty((B, 2 * D), dtype=torch.bfloat16, device=h.device)
+    keys, seq, d1 = chain if chain is not None else (None, None, None)
+    N.call("hsd_head_input", None if chain is not None else N.ptr(tok), N.ptr(keys),
+           0 if keys is None else keys.shape[-1], N.ptr(W.w), N.ptr(W.scales), N.ptr(W.biases), W.O, N.ptr(h),
+           h.stride(0), N.ptr(we), N.ptr(wh), float(eps), B, D, N.ptr(seq), N.ptr(d1), N.ptr(out), out.stride(0),
+           N.ptr(status), N.stream(h.device))
+    return out
+
+
 class KVCache:
     """One attention layer's cache: K and V [HKV, smax, HD] bf16. The length lives on the
     device (an int32 the step kernels advance), so trimming after a rejected draft

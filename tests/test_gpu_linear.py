@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from hsd import nn, synth as S
+from hsd import _native as N, nn, synth as S
 from oracle import hsd_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -260,3 +260,78 @@ def test_pair_norm(dev):
                           O.rms_norm_bf16(O.bf16_to_f32(h), O.bf16_to_f32(wh))], axis=1)
     ok, same = ulp_close(out, ref)
     assert ok and same >= 0.99
+
+
+def test_head_input_equals_embed_then_pair_norm(dev):
+    """hsd_head_input (the MTP head's embedding and pair norm in one launch) equals
+    hsd_embed_q4 then hsd_pair_norm bit for bit: on token rows (a token outside the table
+    embeds as zeros and sets the status bit), and for the chained call, whose token is the
+    argmax of a keys row (d1 and HEAD_POS2 as hsd_mtp_chain writes them)."""
+    rng = np.random.default_rng(81)
+    V, D = 1000, 2688
+    w, s, b = S.down_proj_np(rng, (), V, D)
+    W = nn.QWeight(S.to_device(w, dev), S.to_device(s, dev), S.to_device(b, dev))
+    h, hd = bf16_rows(rng, 3, D, dev, 5.0)
+    we = S.to_device(O.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32)), dev)
+    wh = S.to_device(O.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32)), dev)
+    tok = torch.tensor([5, 999, 1000], dtype=torch.int32, device=dev)
+    st1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    st2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    want = nn.pair_norm(nn.embed(tok, W, status=st1), hd, we, wh)
+    got = nn.head_input(tok, hd, W, we, wh, status=st2)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert int(st1.item()) == 4 and int(st2.item()) == 4
+    # the chained call: keys of one row (the per-workgroup keys of an argmax linear)
+    slots = 512
+    vals = rng.integers(0, 1 << 30, slots, dtype=np.int64)      # (order bits << 32) | ~index
+    keys = torch.from_numpy(((vals << 32) | (~np.arange(slots, dtype=np.int64) & 0xFFFFFFFF)).reshape(1, slots)).to(dev)
+    for R in (1, 2, 3):
+        seq = torch.zeros(N.SEQ_LEN, dtype=torch.int32, device=dev)
+        seq[N.SEQ_R] = R
+        seq[N.SEQ_HEAD_POS] = 40
+        seq2 = seq.clone()
+        d1a = torch.zeros(4, dtype=torch.int32, device=dev)
+        d1b = torch.zeros(4, dtype=torch.int32, device=dev)
+        h2 = torch.empty((1, D), dtype=torch.bfloat16, device=dev)
+        N.call("hsd_mtp_chain", N.ptr(keys), 0, slots, N.ptr(hd[1:2]), 0, D, N.ptr(seq), N.ptr(d1a), N.ptr(h2),
+               N.stream(dev))
+        want = nn.pair_norm(nn.embed(d1a[:1], W), h2, we, wh)
+        got = nn.head_input(None, hd[1:2], W, we, wh, chain=(keys, seq2, d1b))
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), R
+        assert torch.equal(d1a, d1b) and torch.equal(seq, seq2), R
+
+
+@pytest.mark.parametrize("scripted", [False, True])
+def test_verify_input_equals_draft_ids_then_embed(dev, scripted):
+    """hsd_verify_input (the verify ids and their embedding rows in one launch) equals
+    hsd_draft_ids then hsd_embed_q4 bit for bit, with the head's own drafts and with
+    scripted acceptance."""
+    rng = np.random.default_rng(82)
+    V, D = 1000, 2688
+    w, s, b = S.down_proj_np(rng, (), V, D)
+    W = nn.QWeight(S.to_device(w, dev), S.to_device(s, dev), S.to_device(b, dev))
+    slots = 512
+    vals = rng.integers(0, 1 << 30, slots, dtype=np.int64)      # (order bits << 32) | ~token
+    idx = (rng.permutation(slots) % V).astype(np.int64)
+    keys2 = torch.from_numpy(((vals << 32) | (~idx & 0xFFFFFFFF)).reshape(1, slots)).to(dev)
+    d1 = torch.tensor([321], dtype=torch.int32, device=dev)
+    script = torch.from_numpy(rng.integers(0, V, 64).astype(np.int32)).to(dev) if scripted else None
+    accepts = torch.tensor([0, 1, 2, 1], dtype=torch.int32, device=dev) if scripted else None
+    for step in range(4):
+        seq = torch.zeros(N.SEQ_LEN, dtype=torch.int32, device=dev)
+        seq[N.SEQ_TOK] = 777
+        seq[N.SEQ_N] = 5 + 2 * step
+        seq[N.SEQ_STEPS] = step
+        args = (N.ptr(d1), N.ptr(keys2), slots, 2, N.ptr(seq), N.ptr(script), 0 if script is None else script.numel(),
+                N.ptr(accepts), 0 if accepts is None else accepts.numel(), V)
+        ids_a = torch.full((4,), -1, dtype=torch.int32, device=dev)
+        N.call("hsd_draft_ids", *args, N.ptr(ids_a), N.stream(dev))
+        want = nn.embed(ids_a[:3], W)
+        ids_b = torch.full((4,), -1, dtype=torch.int32, device=dev)
+        got = torch.empty((3, D), dtype=torch.bfloat16, device=dev)
+        st = torch.zeros(1, dtype=torch.int32, device=dev)
+        N.call("hsd_verify_input", *args, N.ptr(W.w), N.ptr(W.scales), N.ptr(W.biases), D, N.ptr(ids_b), N.ptr(got),
+               got.stride(0), N.ptr(st), N.stream(dev))
+        assert torch.equal(ids_a, ids_b), step
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        assert int(st.item()) == 0
