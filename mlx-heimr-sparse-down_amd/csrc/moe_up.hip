@@ -39,19 +39,19 @@ constexpr int kUpSmallD = 3072;                 // the smaller instance (the ref
 static_assert((kUpBlk == 16 || kUpBlk == 8) && kUpBlk * (kUpMaxD / 64) / 4 <= kUpThreads,
               "a block is a quarter or an eighth of a mask group; 4 scales and biases per thread");
 // Two instances by the largest D: the register arrays (x words, the lane's weight pieces)
-// are sized for it, so D <= 3072 runs 7 wavefronts per SIMD (at most 72 VGPRs) and the
-// 4096 instance 6. A single instance for D <= 4096 (96 VGPRs, 5 per SIMD) had made the
+// are sized for it, so D <= 3072 runs 8 wavefronts per SIMD (64 VGPRs) and the 4096
+// instance 6. A single instance for D <= 4096 (96 VGPRs, 5 per SIMD) had made the
 // MTP-2 step 2.221 against 2.196 ms for 72 VGPRs and 7 per SIMD; the x rows in LDS sit at
 // a compile-time pitch (no per-piece address registers).
 template <int MAXD> struct UpShape {
   static constexpr int kMaxP = MAXD / 32;
   static constexpr int kXIt = (MAXD / 8 + kUpThreads - 1) / kUpThreads;  // x words per thread
-  // per SIMD: 7 for D <= 3072 (72 VGPRs). With the nibble mask in a register (one
-  // v_and_or_b32 per bf16 pair instead of a v_and_b32 and a v_or_b32) the routed instance
-  // needs 65-68 VGPRs; at 8 wavefronts (64 VGPRs) it spilled. 7 wavefronts with the shorter
-  // decode: MTP-2 step 1.854 / 1.846 against 1.860 / 1.863 ms for 8 with the literal decode,
-  // sparse decode step 1.037 / 1.028 against 1.044 / 1.041 ms (alternating runs).
-  static constexpr int kWaves = MAXD <= kUpSmallD ? 7 : 6;
+  // per SIMD: 8 for D <= 3072 (64 VGPRs, 2048 resident workgroups: 1.36 rounds at three
+  // token rows), once the wavefront index and the routed expert id are scalars; with the
+  // nibble mask in a register the routed instance had needed 65-68 VGPRs before that (7
+  // wavefronts: MTP-2 step 1.854 / 1.846 against 1.860 / 1.863 ms for 8 with the
+  // two-instruction decode).
+  static constexpr int kWaves = MAXD <= kUpSmallD ? 8 : 6;
 };
 // 16-row workgroups (4 rows per wavefront): at three token rows 19.0 against 19.8 us per
 // call for 8-row ones (fewer rounds of workgroups), at one row the same. Small workgroups
@@ -154,7 +154,9 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
   // per (row, group) of the block: (16 s, b - 16 s), the factors of the affine step
   __shared__ __attribute__((aligned(16))) float2 sbt[kUpBlk * (MAXD / 64)];  // [row][group]
   const int b = blockIdx.y, blk = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wavefront index as a scalar: the rows' addresses are then a scalar base plus the
+  // lane's offset (8 wavefronts per SIMD fit 64 VGPRs only so)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NR = topk * F + FS, NP = D / 32, NW = D / 8, NGD = D / 64;
   const int r0 = kUpBlk * blk;
   const bool routed = r0 < topk * F;
@@ -195,7 +197,7 @@ __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves)
         }
       }
       lds_barrier();
-      e = tsel[k];
+      e = __builtin_amdgcn_readfirstlane(tsel[k]);
     } else {
       e = 0;
     }
