@@ -61,8 +61,30 @@ struct AttnArgs {
   float scale;
 };
 
+// The fields each kernel's first loads need go ahead of the struct as scalar arguments,
+// which the dispatch preloads into SGPRs (a struct argument is read by scalar loads from
+// the argument segment, which the first global loads would wait for); the kernels rebuild
+// the whole struct from both.
+#define HSD_ATTN_PART_PARAMS                                                                    \
+  const int32_t *pos_, const uint16_t *qkv_, uint16_t *kc_, uint16_t *vc_, int64_t qkv_ld_,      \
+      int64_t smax_, int HQ_, int nch_, AttnArgs a_
+#define HSD_ATTN_PART_ARGS(a) a.pos, a.qkv, a.kc, a.vc, a.qkv_ld, a.smax, a.HQ, a.nch, a
+#define HSD_ATTN_COMB_PARAMS                                                                    \
+  const int32_t *pos_, float *part_, uint16_t *out_, int64_t out_ld_, int64_t smax_,       \
+      int HQ_, int nch_, int B_, AttnArgs a_
+#define HSD_ATTN_COMB_ARGS(a) a.pos, a.part, a.out, a.out_ld, a.smax, a.HQ, a.nch, a.B, a
+
 template <int kHPW>  // query heads per workgroup, one wavefront each
-__global__ __launch_bounds__(64 * kHPW) void k_attn_part(AttnArgs a) {
+__global__ __launch_bounds__(64 * kHPW) void k_attn_part(HSD_ATTN_PART_PARAMS) {
+  AttnArgs a = a_;
+  a.pos = pos_;
+  a.qkv = qkv_;
+  a.kc = kc_;
+  a.vc = vc_;
+  a.qkv_ld = qkv_ld_;
+  a.smax = smax_;
+  a.HQ = HQ_;
+  a.nch = nch_;
   constexpr int kAT = 64 * kHPW;
   constexpr int kAW = kAT / 64;     // wavefronts per workgroup
   constexpr int kTPH = kAT / kHPW;  // threads per head in the value sum
@@ -263,7 +285,16 @@ constexpr int kMaxCh = 512;      // chunks per row the combine stages in LDS (sm
 constexpr int kPre = 64;         // chunks whose values the combine loads up front (2048 keys;
                                  // 128 measured no faster, 158 VGPRs)
 
-__global__ __launch_bounds__(kHD) void k_attn_combine(AttnArgs a) {
+__global__ __launch_bounds__(kHD) void k_attn_combine(HSD_ATTN_COMB_PARAMS) {
+  AttnArgs a = a_;
+  a.pos = pos_;
+  a.part = part_;
+  a.out = out_;
+  a.out_ld = out_ld_;
+  a.smax = smax_;
+  a.HQ = HQ_;
+  a.nch = nch_;
+  a.B = B_;
   __shared__ float mw[kMaxCh];    // the chunks' maxima, then their weights e^(m - M)
   __shared__ float lw[kMaxCh];
   __shared__ float red[2];
@@ -370,13 +401,13 @@ extern "C" int hsd_attn_decode(const uint16_t* qkv, int64_t qkv_ld, int64_t B, u
   const int64_t nwg = HKV * nch * (ratio / hpw);
   if (nwg > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
   if (hpw == 16)
-    hipLaunchKernelGGL(k_attn_part<16>, dim3((unsigned)nwg), dim3(64 * 16), 0, st, a);
+    hipLaunchKernelGGL(k_attn_part<16>, dim3((unsigned)nwg), dim3(64 * 16), 0, st, HSD_ATTN_PART_ARGS(a));
   else if (hpw == 8)
-    hipLaunchKernelGGL(k_attn_part<8>, dim3((unsigned)nwg), dim3(64 * 8), 0, st, a);
+    hipLaunchKernelGGL(k_attn_part<8>, dim3((unsigned)nwg), dim3(64 * 8), 0, st, HSD_ATTN_PART_ARGS(a));
   else
-    hipLaunchKernelGGL(k_attn_part<4>, dim3((unsigned)nwg), dim3(64 * 4), 0, st, a);
+    hipLaunchKernelGGL(k_attn_part<4>, dim3((unsigned)nwg), dim3(64 * 4), 0, st, HSD_ATTN_PART_ARGS(a));
   int rc = check_launch(fn);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)(B * HQ)), dim3(kHD), 0, st, a);
+  hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)(B * HQ)), dim3(kHD), 0, st, HSD_ATTN_COMB_ARGS(a));
   return check_launch(fn);
 }

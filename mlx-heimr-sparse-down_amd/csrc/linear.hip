@@ -100,6 +100,26 @@ struct LinArgs {
   int O, I;
 };
 
+// The fields a workgroup's first loads need (x, the weights, scales and biases, the norm
+// weight, the shape) go ahead of the struct as scalar arguments: the dispatch preloads a
+// kernel's leading scalar arguments into SGPRs (56 bytes here), while a struct argument is
+// read from the argument segment by scalar loads, which the first global loads would wait
+// for. The kernels rebuild the whole struct from both.
+#define HSD_LIN_PARAMS                                                                                  \
+  const void *x_, const void *w_, const uint16_t *s_, const uint16_t *bq_, const uint16_t *nw_,          \
+      int64_t x_ld_, int O_, int I_, LinArgs a_
+#define HSD_LIN_UNPACK                                                                                  \
+  LinArgs a = a_;                                                                                       \
+  a.x = x_;                                                                                             \
+  a.w = w_;                                                                                             \
+  a.s = s_;                                                                                             \
+  a.bq = bq_;                                                                                           \
+  a.nw = nw_;                                                                                           \
+  a.x_ld = x_ld_;                                                                                       \
+  a.O = O_;                                                                                             \
+  a.I = I_
+#define HSD_LIN_ARGS(a) a.x, a.w, a.s, a.bq, a.nw, a.x_ld, a.O, a.I, a
+
 // Two floats to packed bf16 (round to nearest even; v_cvt_pk_bf16_f32 on gfx950). Used for
 // the normalised activations, which are finite.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -303,7 +323,8 @@ struct XIn {
 // it moved to the matrix cores) are faster with the registers of two.
 template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM>
 __global__ __launch_bounds__(kLT, WF == HSD_W_Q4 ? (IMAX == 3072 && NB < 4 ? 3 : 2) : (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2)
-void k_linear(LinArgs a) {
+void k_linear(HSD_LIN_PARAMS) {
+  HSD_LIN_UNPACK;
   using T = WTraits<WF>;
   constexpr bool Q4 = WF == HSD_W_Q4;
   static_assert(!Q4 || RW == 4 || RW == 2, "4-bit weights: 4 or 2 rows per wavefront, 2 or 1 per half-wavefront");
@@ -659,7 +680,8 @@ void k_linear(LinArgs a) {
 constexpr int kQR = 16;                  // output rows per block (the MFMA's N)
 
 template <int NB, int XK, int YK, int IMAX>
-__global__ __launch_bounds__(kLT, 2) void k_linear_q4(LinArgs a) {
+__global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
+  HSD_LIN_UNPACK;
   constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
@@ -852,7 +874,8 @@ static_assert(16 * (kRingI / 32 + 1) + 2 * (kRingI / 32) <= kRingChunks && kRing
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int XK, int NB>
-__global__ __launch_bounds__(kLT, 2) void k_lm_ring(LinArgs a) {
+__global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
+  HSD_LIN_UNPACK;
   constexpr int IMAX = kRingI, PX = IMAX / 32;
   constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
@@ -1145,7 +1168,8 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     const size_t ldsx = WF == HSD_W_Q4 ? (size_t)B * 17 * (IM / 32) * 4 : lds;                        \
     const int gr = RW == 2 ? std::min((int)((O + 7) / 8), kLMaxGrid) : grid;                          \
     const int g = std::max(1, std::min(gr, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));           \
-    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), ldsx, st, a);     \
+    hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), ldsx, st,        \
+                       HSD_LIN_ARGS(a));                                                          \
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                                   \
   {                                                                   \
@@ -1189,7 +1213,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     const void* kf = reinterpret_cast<const void*>(&k_linear_q4<NB, XK, YK, IM>);                 \
     const size_t ldsq = (size_t)NB * (16 * (IM / 32) + IM / 64) * 4 + (size_t)2 * kQR * (I / 64) * 4; \
     const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, ldsq, kLMaxGrid)));     \
-    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), ldsq, st, a);           \
+    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), ldsq, st, HSD_LIN_ARGS(a)); \
   }
 #define HSD_Q4_I(NB, XK, YK)                                    \
   if (I <= 3072) HSD_Q4_R(NB, XK, YK, 3072)                     \
@@ -1212,7 +1236,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   {                                                                                           \
     const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS, NB>);                \
     const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, 0, kLMaxGrid)));    \
-    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB>), dim3(g), dim3(kLT), 0, st, a);             \
+    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB>), dim3(g), dim3(kLT), 0, st, HSD_LIN_ARGS(a)); \
   }
     if (B == 1)
       HSD_RING(1)
