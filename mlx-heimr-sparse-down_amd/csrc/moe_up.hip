@@ -140,11 +140,16 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
 template <bool ROUTE, int MAXD>
 __global__ __launch_bounds__(kUpThreads)
 __attribute__((amdgpu_waves_per_eu(UpShape<MAXD>::kWaves, UpShape<MAXD>::kWaves))) void k_moe_up(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ sel, const uint32_t* __restrict__ w1,
+    int D, int F, int FS, int topk, int E, const uint16_t* __restrict__ x, const int32_t* __restrict__ sel,
+    const uint16_t* __restrict__ logits, const float* __restrict__ e_bias, const uint32_t* __restrict__ w1,
     const uint16_t* __restrict__ s1, const uint16_t* __restrict__ b1, const uint32_t* __restrict__ sw1,
     const uint16_t* __restrict__ ss1, const uint16_t* __restrict__ sb1, uint16_t* __restrict__ hcat,
-    uint64_t* __restrict__ live_out, int32_t* __restrict__ status, int D, int F, int FS, int topk,
-    int E, Router rt) {
+    uint64_t* __restrict__ live_out, int32_t* __restrict__ status, Router rt_) {
+  // the shape and the first round trip's pointers (x, the selection or the gate's logits
+  // and bias) are the leading scalar arguments, which the dispatch preloads into SGPRs
+  Router rt = rt_;
+  rt.logits = logits;
+  rt.bias = e_bias;
   // x pairs: piece j, word m, pair n at xp[4 (m kUpMaxP + j) + n] = (x[32 j + 8 m + n], x[.. + 4])
   // (a row of kUpMaxP pieces: the readers' addresses are a lane base plus constant offsets)
   constexpr int kUpMaxP = UpShape<MAXD>::kMaxP, kUpXIt = UpShape<MAXD>::kXIt;
@@ -377,9 +382,9 @@ extern "C" int hsd_moe_up_relu2(const void* x, int x_dtype, const int32_t* sel, 
   const dim3 grid((unsigned)((topk * F + FS) / kUpBlk), (unsigned)B);
 #define HSD_UP(MD)                                                                              \
   hipLaunchKernelGGL((k_moe_up<false, MD>), grid, dim3(kUpThreads), 0, as_stream(stream),      \
-                     reinterpret_cast<const uint16_t*>(x), sel, w1, s1, b1, sw1, ss1, sb1,    \
-                     reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, (int)D, (int)F, \
-                     (int)FS, (int)topk, (int)E, Router{})
+                     (int)D, (int)F, (int)FS, (int)topk, (int)E, reinterpret_cast<const uint16_t*>(x), \
+                     sel, nullptr, nullptr, w1, s1, b1, sw1, ss1, sb1,                          \
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, dev_status, Router{})
   if (D <= kUpSmallD)
     HSD_UP(kUpSmallD);
   else
@@ -413,9 +418,9 @@ extern "C" int hsd_moe_route_up_relu2(const void* x, int x_dtype, const uint16_t
   Router rt{logits, e_bias, sel, gains, routed_scale, norm_topk};
 #define HSD_UP(MD)                                                                                   \
   hipLaunchKernelGGL((k_moe_up<true, MD>), grid, dim3(kUpThreads), 0, as_stream(stream),            \
-                     reinterpret_cast<const uint16_t*>(x), nullptr, w1, s1, b1, sw1, ss1, sb1,     \
-                     reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, (int)D, (int)F, (int)FS, \
-                     (int)topk, (int)E, rt)
+                     (int)D, (int)F, (int)FS, (int)topk, (int)E, reinterpret_cast<const uint16_t*>(x), \
+                     nullptr, rt.logits, rt.bias, w1, s1, b1, sw1, ss1, sb1,                         \
+                     reinterpret_cast<uint16_t*>(hcat), live_masks, nullptr, rt)
   if (D <= kUpSmallD)
     HSD_UP(kUpSmallD);
   else
