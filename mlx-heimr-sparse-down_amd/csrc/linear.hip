@@ -686,7 +686,7 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
   extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];
   __shared__ float wsum[NB][4];
-  __shared__ float red[2][4][NB][kQR];                 // [block parity][wavefront][token row][row]
+  __shared__ float red[2][8][NB][kQR];                 // [block parity][chain][token row][row]
   const int I = a.I, O = a.O, G = I / 64;
   // LDS: x pairs [NB][I/2] words, the group sums [NB][G], then per block parity the
   // (scale | bias << 16) words of the block's rows [2][G][16]
@@ -748,14 +748,18 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
 
   uint64_t best = 0;                                   // wavefront 0, lanes of token row l / 16
   const int arow = min(n, NB - 1);                     // the token row of this lane's A operand
-  // one block: the wavefront's groups, its partial sums to LDS, then wavefront 0 adds the
-  // four partials and runs the epilogue. With next_sc, the next block's scales go to the
-  // other LDS parity before the barrier (their last readers were the previous block's).
+  // one block: the wavefront's groups (two chains), their partial sums to LDS, then
+  // wavefront 0 adds the eight partials and runs the epilogue. With next_sc, the next
+  // block's scales go to the other LDS parity before the barrier (their last readers were
+  // the previous block's).
   auto do_block = [&](int blk_, const Wq& wb, int par, bool next_sc, int nblk_, const uint4& nsv,
                       const uint4& nbv) {
-    float y[NB];
+    // two chains per wavefront: the even group slots (groups wave + 8 k) and the odd ones
+    // (wave + 4 + 8 k), so that the 8 partials and their order are those of the 8-wavefront
+    // LDS ring below (one chain per wavefront there)
+    float y[2][NB];
 #pragma unroll
-    for (int r = 0; r < NB; ++r) y[r] = 0.0f;
+    for (int r = 0; r < NB; ++r) y[0][r] = y[1][r] = 0.0f;
     const uint32_t* sb = sbl + par * kQR * G;
     // a group slot's x words (the lane's token row, 2 x 16 bytes), read for the next slot
     // before the current slot's arithmetic so the LDS latency is off the chain of groups
@@ -789,14 +793,17 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
       const float s16 = 16.0f * sv_, bo = fmaf(-16.0f, sv_, bv_);
 #pragma unroll
       for (int r = 0; r < NB; ++r) {
-        const float yn = y[r] + fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
-        y[r] = g0 < G ? yn : y[r];
+        const float yn = y[it & 1][r] + fmaf(s16, acc[r], bo * xg[r * (PX / 2) + g]);
+        y[it & 1][r] = g0 < G ? yn : y[it & 1][r];
       }
     }
     // lanes 0..15 hold token rows 0..3 of output row n (acc[r]: token row 4 (l / 16) + r)
     if (q == 0) {
 #pragma unroll
-      for (int r = 0; r < NB; ++r) red[par][wave][r][n] = y[r];
+      for (int r = 0; r < NB; ++r) {
+        red[par][wave][r][n] = y[0][r];
+        red[par][wave + 4][r][n] = y[1][r];
+      }
     }
     if (next_sc) store_sc(par ^ 1, nblk_, nsv, nbv);
     // LDS only: the next block's weights stay in flight across the barrier (53.9 against
@@ -807,7 +814,9 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
       const int o = blk_ * kQR + n;
       const bool live = m < NB && o < O;
       const int mm = min(m, NB - 1);
-      const float v = ((red[par][0][mm][n] + red[par][1][mm][n]) + red[par][2][mm][n]) + red[par][3][mm][n];
+      float v = red[par][0][mm][n];
+#pragma unroll
+      for (int c = 1; c < 8; ++c) v += red[par][c][mm][n];
       if constexpr (YK == HSD_Y_ARGMAX) {
         const uint16_t lb = f32_to_bf16_bits(v);
         uint64_t key = live ? argmax_key(lb, o) : 0;
@@ -858,34 +867,38 @@ __global__ __launch_bounds__(kLT, 2) void k_linear_q4(HSD_LIN_PARAMS) {
 }
 
 // lm_head at NB = 1 or 3 token rows (argmax keys, no logits written): k_linear_q4's
-// arithmetic with the weights streamed into LDS instead of registers. A workgroup keeps a
-// ring of blocks in flight (direct global-to-LDS loads, no registers held), where the
-// register form holds one: at one row 2 workgroups per CU x 3 slots (LDS: 3 x 24 KB + x), at
-// three rows (the verify) 2 x 2 slots, the x rows taking the third slot's LDS. Each ring
+// arithmetic with the weights streamed into LDS instead of registers. A workgroup of 8
+// wavefronts keeps a ring of 2 blocks in flight (direct global-to-LDS loads, no registers
+// held), where the register form holds one: 2 workgroups per CU (LDS: 2 x 24 KB + x), so 4
+// wavefronts per SIMD hide the latency of the group arithmetic (4 wavefronts and 3 slots
+// took 41.5 against 40.2 us per call at one row; 8 wavefronts and 3 slots 41.2). Each ring
 // slot holds a block's 16 weight rows (a 16-byte pad after each, so the 16 rows of a read
-// fall in different banks), then its scales and biases, 24 loads of 1 KB (6 per wavefront:
-// every wavefront waits on the same counts). A row's instruction sequence, group order and
-// cross-wavefront sum are k_linear_q4's, so its bf16 logits (and argmax) are bit-identical to
-// that kernel's for any number of token rows.
+// fall in different banks), then its scales and biases, 24 loads of 1 KB (3 per wavefront:
+// every wavefront waits on the same counts). Wavefront w adds the groups w, w + 8, ... of a
+// block; the 8 partials are summed in wavefront order. k_linear_q4 keeps the same 8 chains
+// (two per wavefront), so a row's bf16 logits (and argmax) are bit-identical to that
+// kernel's for any number of token rows.
 constexpr int kRingI = 2688;             // inputs per row the ring is sized for (the hidden size)
+constexpr int kRingW = 8;                // wavefronts per ring workgroup
+constexpr int kRingSlots1 = 2;           // ring slots at one token row (three at three rows do not fit)
 constexpr int kRingChunks = 1536;        // 16-byte chunks per slot: 16 (I/32 + 1) + 2 I/32 <= 1536
-constexpr int kRingPerWave = kRingChunks / 64 / 4;  // 1-KB loads per wavefront and block
 static_assert(16 * (kRingI / 32 + 1) + 2 * (kRingI / 32) <= kRingChunks && kRingChunks % 256 == 0, "ring slot");
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int XK, int NB>
-__global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
+template <int XK, int NB, int kRW>
+__global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   HSD_LIN_UNPACK;
   constexpr int IMAX = kRingI, PX = IMAX / 32;
-  constexpr int kGW = (IMAX / 64 + 3) / 4;             // groups per wavefront (max)
+  constexpr int kGW = (IMAX / 64 + kRW - 1) / kRW;     // groups per wavefront (max)
   constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
-  constexpr int kSlots = NB == 1 ? 3 : 2;              // ring slots
+  constexpr int kSlots = NB == 1 ? kRingSlots1 : 2;  // ring slots
+  constexpr int kPW = kRingChunks / 64 / kRW;          // 1-KB loads per wavefront and block
   static_assert(NB == 1 || NB == 3, "ring instances: one row (decode) and three (verify)");
   __shared__ __attribute__((aligned(16))) uint4 ring[kSlots][kRingChunks];
   __shared__ __attribute__((aligned(16))) uint32_t xp[NB * 16 * PX];
   __shared__ float xg[NB * (PX / 2)];
   __shared__ float wsum[NB][4];
-  __shared__ float red[2][4][NB][kQR];                 // [block parity][wavefront][token row][row]
+  __shared__ float red[2][kRW][NB][kQR];               // [block parity][wavefront][token row][row]
   const int I = a.I, O = a.O, G = I / 64, NPr = I / 32, rowc = NPr + 1;
   // the wavefront index as a scalar: the group loops below branch on it uniformly (a
   // vector index made each group an exec-masked branch, serialising the groups)
@@ -898,11 +911,11 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   // k + 1: chunk c = 64 i + lane of a slot takes weight row c / rowc, chunk c % rowc (the pad
   // chunk re-reads the row's last), then the block's scales, then its biases; chunks past
   // those re-read the last bias chunk (O % 16 == 0: no row past O)
-  const char* src[kRingPerWave];
-  uint32_t step[kRingPerWave];
+  const char* src[kPW];
+  uint32_t step[kPW];
 #pragma unroll
-  for (int j = 0; j < kRingPerWave; ++j) {
-    const int c = 64 * (wave + 4 * j) + lane;
+  for (int j = 0; j < kPW; ++j) {
+    const int c = 64 * (wave + kRW * j) + lane;
     if (c < 16 * rowc) {
       const int r = c / rowc, ch = min(c - r * rowc, NPr - 1);
       src[j] = reinterpret_cast<const char*>(a.w) + (size_t)((int)blockIdx.x * kQR + r) * (I / 2) + 16 * ch;
@@ -926,8 +939,8 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   auto issue = [&](int k, uint4* slot) {
     const uint32_t base = (uint32_t)(uintptr_t)(lds_void_t*)slot;
 #pragma unroll
-    for (int j = 0; j < kRingPerWave; ++j) {
-      const uint32_t m0 = base + 1024u * (wv + 4u * j);
+    for (int j = 0; j < kPW; ++j) {
+      const uint32_t m0 = base + 1024u * (wv + (uint32_t)kRW * j);
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src[j])
@@ -938,11 +951,16 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   };
 
   // ---- prologue: x, the first blocks (one per slot), x into LDS
+  // (the x prologue is written for 256 threads: with 8 wavefronts, wavefronts 4-7 only
+  // meet its barrier)
   XIn<HSD_W_Q4, NB, XK, XIT, PX> xin;
-  xin.load(a, tid);
+  if (kRW == 4 || wave < 4) xin.load(a, tid);
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) issue(k, ring[k]);
-  xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
+  if (kRW == 4 || wave < 4)
+    xin.template finish<64>(a, xp, xg, wsum, tid, lane, wave);
+  else
+    lds_barrier();
 
   uint64_t best = 0;                                   // lanes of token row l / 16
   const int arow = min(n, NB - 1);                     // the token row of this lane's A operand
@@ -958,7 +976,7 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
     // next slot's are read before the current slot's arithmetic, so the LDS latency is not
     // on the chain of one group after another
     auto ld = [&](int it, uint2& w2, uint4& xa0, uint4& xa1) {
-      const int g = min(wave + 4 * it, G - 1);
+      const int g = min(wave + kRW * it, G - 1);
       const int p = 2 * g + (q >> 1);
       w2 = *reinterpret_cast<const uint2*>(sl + 16 * (n * rowc + p) + 8 * (q & 1));
       xa0 = *reinterpret_cast<const uint4*>(&xp[arow * 16 * PX + 4 * ((2 * (q & 1) + 0) * PX + p)]);
@@ -971,7 +989,7 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
     // branch); the sum over the wavefront's groups keeps its order
 #pragma unroll
     for (int it = 0; it < kGW; ++it) {
-      const int g0 = wave + 4 * it, g = min(g0, G - 1);
+      const int g0 = wave + kRW * it, g = min(g0, G - 1);
       const uint2 w2 = w2n;
       const uint4 xa0 = xa0n, xa1 = xa1n;
       if (it + 1 < kGW) ld(it + 1, w2n, xa0n, xa1n);
@@ -998,15 +1016,17 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
       for (int r = 0; r < NB; ++r) red[k & 1][wave][r][n] = y[r];
     }
   };
-  // after block k's barrier: wavefront k % 4 adds the four partials of each row and keeps the
+  // after block k's barrier: wavefront k % 8 adds the 8 partials of each row and keeps the
   // best key, while the others go on to block k + 1 (which writes red[(k + 1) & 1]); taking
   // turns keeps one wavefront from running behind the others at every block's barrier
   auto epilogue = [&](int k) {
-    if (wave == (k & 3)) {                              // the wavefronts take turns
+    if (wave == k % kRW) {                              // the wavefronts take turns
       const int o = ((int)blockIdx.x + k * (int)gridDim.x) * kQR + n;
       const int m = min(q, NB - 1);                      // token row of this lane
       const bool live = q < NB && o < O;
-      const float v = ((red[k & 1][0][m][n] + red[k & 1][1][m][n]) + red[k & 1][2][m][n]) + red[k & 1][3][m][n];
+      float v = red[k & 1][0][m][n];
+#pragma unroll
+      for (int w = 1; w < kRW; ++w) v += red[k & 1][w][m][n];
       uint64_t key = live ? argmax_key(f32_to_bf16_bits(v), o) : 0;
       key = row16_max_u64(key);
       best = key > best ? key : best;
@@ -1017,14 +1037,15 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   // when it was issued), then one barrier: every wavefront's part of block k + 1 is in, the
   // slot of block k is free and red[k & 1] complete
   auto end_block = [&](int k) {
-    if (kSlots == 3 && (k + 2 <= 2 || k + 2 < nmine)) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    if (kSlots == 3 && (k + 2 <= 2 || k + 2 < nmine)) __builtin_amdgcn_s_waitcnt(0x0F70 | kPW);  // vmcnt(kPW)
     else __builtin_amdgcn_s_waitcnt(0x0F70);                                             // vmcnt(0)
     lds_barrier();
   };
+  static_assert(2 * kPW < 16, "vmcnt immediates below");
   if constexpr (kSlots == 3)
-    __builtin_amdgcn_s_waitcnt(0x0F7C);                // vmcnt(12): block 0 in
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kPW));    // vmcnt(2 kPW): block 0 in
   else
-    __builtin_amdgcn_s_waitcnt(0x0F76);                // vmcnt(6): block 0 in
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kPW);          // vmcnt(kPW): block 0 in
   lds_barrier();                                       // x and block 0 in LDS
   for (int k = 0; k < nmine; k += kSlots) {
 #pragma unroll
@@ -1038,13 +1059,13 @@ __global__ __launch_bounds__(kLT, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);                  // no ring load outlives the workgroup
   // each wavefront's best key per token row (lane 16 m holds row m's), then their maximum
-  __shared__ uint64_t wbest[4][NB];
+  __shared__ uint64_t wbest[kRW][NB];
   if (n == 0 && q < NB) wbest[wave][q] = best;
   lds_barrier();
   if (wave == 0 && lane < NB) {
     uint64_t m = wbest[0][lane];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) m = wbest[w][lane] > m ? wbest[w][lane] : m;
+    for (int w = 1; w < kRW; ++w) m = wbest[w][lane] > m ? wbest[w][lane] : m;
     a.keys[lane * a.key_ld + blockIdx.x] = m;
     for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[lane * a.key_ld + sl2] = 0;
   }
@@ -1234,9 +1255,10 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
   if (ring) {
 #define HSD_RING(NB)                                                                          \
   {                                                                                           \
-    const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS, NB>);                \
-    const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, 0, kLMaxGrid)));    \
-    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB>), dim3(g), dim3(kLT), 0, st, HSD_LIN_ARGS(a)); \
+    const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS, NB, kRingW>);        \
+    const int g = std::max(1, std::min(grid, resident_workgroups(kf, 64 * kRingW, 0, kLMaxGrid))); \
+    hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB, kRingW>), dim3(g), dim3(64 * kRingW), 0, st,  \
+                       HSD_LIN_ARGS(a));                                                      \
   }
     if (B == 1)
       HSD_RING(1)
