@@ -894,6 +894,9 @@ __global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   constexpr int kSlots = NB == 1 ? kRingSlots1 : 2;  // ring slots
   constexpr int kPW = kRingChunks / 64 / kRW;          // 1-KB loads per wavefront and block
   static_assert(NB == 1 || NB == 3, "ring instances: one row (decode) and three (verify)");
+  // wavefronts 4-7 meet the x prologue's one barrier with a barrier of their own: the RMS
+  // prologue has exactly one (the other prologues have none or more)
+  static_assert(XK == HSD_X_RMS && (kRW == 4 || kRW == 8), "ring instances: the RMS prologue, 4 or 8 wavefronts");
   __shared__ __attribute__((aligned(16))) uint4 ring[kSlots][kRingChunks];
   __shared__ __attribute__((aligned(16))) uint32_t xp[NB * 16 * PX];
   __shared__ float xg[NB * (PX / 2)];
