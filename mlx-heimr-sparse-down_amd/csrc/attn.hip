@@ -97,12 +97,15 @@ __global__ __launch_bounds__(64 * kHPW) void k_attn_part(HSD_ATTN_PART_PARAMS) {
   __shared__ __attribute__((aligned(16))) float vs[kCH][kHD];     // V in fp32 (converted once)
   __shared__ __attribute__((aligned(16))) uint32_t qs[kAMaxB][kHPW][kHD / 2];
   __shared__ float ps[kAMaxB][kHPW][kCH];
+  // the device length first: its load (preloaded pointer) leaves before the workgroup's
+  // coordinates, which wait for the rest of the arguments
+  const int P = *a.pos;
+  __builtin_amdgcn_sched_barrier(0);
   const int nhalf = a.HQ / a.HKV / kHPW;       // workgroups per (kv head, chunk)
   const int g = blockIdx.x / (a.nch * nhalf);
   const int rem = blockIdx.x - g * a.nch * nhalf;
   const int c = rem / nhalf, hh = rem - c * nhalf;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int P = *a.pos;
   const int B = a.B;
   if (P < 0 || P + B > a.smax) {
     if (blockIdx.x == 0 && tid == 0 && a.status) atomicOr(a.status, (int32_t)HSD_STATUS_BAD_STATE);

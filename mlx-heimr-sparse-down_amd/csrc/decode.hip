@@ -84,14 +84,15 @@ template <int HDT>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 ? 7 : 8))) void k_sparse_down_part(
     const typename Elem<HDT>::T* __restrict__ h, const int32_t* __restrict__ sel,
-    const float* __restrict__ gains, int nwg_, int nchunk_, int topk_, int ppr_, int gpr_, int gsh_, int NR_,
+    const float* __restrict__ gains, int nwg_, int nchunk_, int topk_, int ppr_, int gpr_, int gsh_, int nblk_,
     int F_, const uint32_t* __restrict__ pw, const uint16_t* __restrict__ ps, const uint16_t* __restrict__ pb,
     const uint32_t* __restrict__ spw, const uint16_t* __restrict__ sps,
     const uint16_t* __restrict__ spb, float* __restrict__ part, uint64_t* __restrict__ live_out,
     int32_t* __restrict__ status, Geom g_, int dense) {
   // the first round trip's pointers and geometry come as the leading scalar arguments,
   // which the dispatch preloads into SGPRs (the struct is read by scalar loads, which the
-  // first loads would wait for); the grid is B x nwg workgroups
+  // first loads would wait for); nblk_ is the grid (B x nwg workgroups: gridDim would be a
+  // scalar load of the dispatch's hidden arguments)
   Geom g = g_;
   g.nwg = nwg_;
   g.nchunk = nchunk_;
@@ -99,7 +100,7 @@ __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 
   g.ppr = ppr_;
   g.gpr = gpr_;
   g.gsh = gsh_;
-  g.NR = NR_;
+  g.NR = topk_ * F_ + 64 * gsh_;
   g.F = F_;
   using HT = typename Elem<HDT>::T;
   // Per-team rows padded by 64 bytes, so that the team strides are 16 banks mod 32 and
@@ -116,7 +117,7 @@ __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 
   __shared__ float red[kGPW * kRS][kRedP];          // per team: group terms [t][word]
   __shared__ float sum2[kDC][kL1 + 1];
 
-  const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int logical = xcd_remap((int)blockIdx.x, nblk_);
   const int b = logical / g.nwg;
   const int rem = logical - b * g.nwg;
   const int p = rem / g.nchunk, c = rem - p * g.nchunk;
@@ -616,7 +617,7 @@ int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t
 #define HSD_PART(DT)                                                                          \
   hipLaunchKernelGGL(k_sparse_down_part<DT>, dim3((unsigned)nblk), dim3(kThreads), 0, st,    \
                      reinterpret_cast<const typename Elem<DT>::T*>(h), sel, gains, g.nwg, g.nchunk,   \
-                     g.topk, g.ppr, g.gpr, g.gsh, g.NR, g.F, pw, ps, pb, spw, sps, spb, part,    \
+                     g.topk, g.ppr, g.gpr, g.gsh, (int)nblk, g.F, pw, ps, pb, spw, sps, spb, part,    \
                      live_masks, dev_status, g, dense)
   switch (h_dtype) {
     case HSD_DT_BF16: HSD_PART(HSD_DT_BF16); break;

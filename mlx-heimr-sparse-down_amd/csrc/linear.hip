@@ -101,13 +101,14 @@ struct LinArgs {
 };
 
 // The fields a workgroup's first loads need (x, the weights, scales and biases, the norm
-// weight, the shape) go ahead of the struct as scalar arguments: the dispatch preloads a
-// kernel's leading scalar arguments into SGPRs (56 bytes here), while a struct argument is
-// read from the argument segment by scalar loads, which the first global loads would wait
-// for. The kernels rebuild the whole struct from both.
+// weight, the shape, the grid) go ahead of the struct as scalar arguments: the dispatch
+// preloads a kernel's leading scalar arguments into SGPRs (56 bytes here), while a struct
+// argument (or gridDim, a hidden argument) is read from the argument segment by scalar
+// loads, which the first global loads would wait for. The kernels rebuild the whole struct
+// from both; grid_ is the launch's workgroup count.
 #define HSD_LIN_PARAMS                                                                                  \
   const void *x_, const void *w_, const uint16_t *s_, const uint16_t *bq_, const uint16_t *nw_,          \
-      int64_t x_ld_, int O_, int I_, LinArgs a_
+      int x_ld_, int grid_, int O_, int I_, LinArgs a_
 #define HSD_LIN_UNPACK                                                                                  \
   LinArgs a = a_;                                                                                       \
   a.x = x_;                                                                                             \
@@ -118,7 +119,7 @@ struct LinArgs {
   a.x_ld = x_ld_;                                                                                       \
   a.O = O_;                                                                                             \
   a.I = I_
-#define HSD_LIN_ARGS(a) a.x, a.w, a.s, a.bq, a.nw, a.x_ld, a.O, a.I, a
+#define HSD_LIN_ARGS(a, g) a.x, a.w, a.s, a.bq, a.nw, (int)a.x_ld, (int)(g), a.O, a.I, a
 
 // Two floats to packed bf16 (round to nearest even; v_cvt_pk_bf16_f32 on gfx950). Used for
 // the normalised activations, which are finite.
@@ -909,7 +910,7 @@ __global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   const uint32_t nibm = opaque_vgpr(kNibHi);         // (w & nibm) | one: one v_and_or_b32
   const int n = lane & 15, q = lane >> 4;
   const int nblk = (O + kQR - 1) / kQR;
-  const int nmine = nblk > (int)blockIdx.x ? (nblk - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int nmine = nblk > (int)blockIdx.x ? (nblk - 1 - (int)blockIdx.x) / grid_ + 1 : 0;
   // this lane's source of each of its ring loads for block k = 0, and the step to block
   // k + 1: chunk c = 64 i + lane of a slot takes weight row c / rowc, chunk c % rowc (the pad
   // chunk re-reads the row's last), then the block's scales, then its biases; chunks past
@@ -922,13 +923,13 @@ __global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
     if (c < 16 * rowc) {
       const int r = c / rowc, ch = min(c - r * rowc, NPr - 1);
       src[j] = reinterpret_cast<const char*>(a.w) + (size_t)((int)blockIdx.x * kQR + r) * (I / 2) + 16 * ch;
-      step[j] = gridDim.x * 8u * (uint32_t)I;
+      step[j] = (uint32_t)grid_ * 8u * (uint32_t)I;
     } else {
       const int k2 = c - 16 * rowc;
       const bool isb = k2 >= NPr;
       src[j] = reinterpret_cast<const char*>(isb ? a.bq : a.s) + (size_t)blockIdx.x * kQR * G * 2 +
                16 * min(isb ? k2 - NPr : k2, NPr - 1);
-      step[j] = gridDim.x * 32u * (uint32_t)G;
+      step[j] = (uint32_t)grid_ * 32u * (uint32_t)G;
     }
   }
   const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -1024,7 +1025,7 @@ __global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
   // turns keeps one wavefront from running behind the others at every block's barrier
   auto epilogue = [&](int k) {
     if (wave == k % kRW) {                              // the wavefronts take turns
-      const int o = ((int)blockIdx.x + k * (int)gridDim.x) * kQR + n;
+      const int o = ((int)blockIdx.x + k * grid_) * kQR + n;
       const int m = min(q, NB - 1);                      // token row of this lane
       const bool live = q < NB && o < O;
       float v = red[k & 1][0][m][n];
@@ -1070,7 +1071,7 @@ __global__ __launch_bounds__(64 * kRW, 2) void k_lm_ring(HSD_LIN_PARAMS) {
 #pragma unroll
     for (int w = 1; w < kRW; ++w) m = wbest[w][lane] > m ? wbest[w][lane] : m;
     a.keys[lane * a.key_ld + blockIdx.x] = m;
-    for (int sl2 = blockIdx.x + gridDim.x; sl2 < a.key_slots; sl2 += gridDim.x) a.keys[lane * a.key_ld + sl2] = 0;
+    for (int sl2 = (int)blockIdx.x + grid_; sl2 < a.key_slots; sl2 += grid_) a.keys[lane * a.key_ld + sl2] = 0;
   }
 }
 
@@ -1139,6 +1140,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     return set_error(HSD_ERR_SHAPE, "%s: HSD_X_GATED_Z rows hold I + I/16 values (x_ld >= %lld)", fn,
                      (long long)(I + I / 16));
   const int64_t xe = gated ? 4 : 2;                   // x element bytes
+  if (x_ld > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: x_ld must be below 2^31", fn);
   if (x_ld < I || (x_ld * xe) % 16 || ((uintptr_t)x & 15u) || (norm_w && ((uintptr_t)norm_w & 15u)) ||
       ((uintptr_t)w & 15u) || (gate && (((uintptr_t)gate & 15u) || gate_ld % 8 || gate_ld < I)) ||
       (xn_out && (((uintptr_t)xn_out & 15u) || xn_ld % 8 || xn_ld < I)))
@@ -1193,7 +1195,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     const int gr = RW == 2 ? std::min((int)((O + 7) / 8), kLMaxGrid) : grid;                          \
     const int g = std::max(1, std::min(gr, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));           \
     hipLaunchKernelGGL((k_linear<WF, NB, XK, YK, IM, RW, REM>), dim3(g), dim3(kLT), ldsx, st,        \
-                       HSD_LIN_ARGS(a));                                                          \
+                       HSD_LIN_ARGS(a, g));                                                       \
   }
 #define HSD_LIN(WF, NB, XK, YK, IM)                                   \
   {                                                                   \
@@ -1237,7 +1239,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     const void* kf = reinterpret_cast<const void*>(&k_linear_q4<NB, XK, YK, IM>);                 \
     const size_t ldsq = (size_t)NB * (16 * (IM / 32) + IM / 64) * 4 + (size_t)2 * kQR * (I / 64) * 4; \
     const int g = std::max(1, std::min(grid, resident_workgroups(kf, kLT, ldsq, kLMaxGrid)));     \
-    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), ldsq, st, HSD_LIN_ARGS(a)); \
+    hipLaunchKernelGGL((k_linear_q4<NB, XK, YK, IM>), dim3(g), dim3(kLT), ldsq, st, HSD_LIN_ARGS(a, g)); \
   }
 #define HSD_Q4_I(NB, XK, YK)                                    \
   if (I <= 3072) HSD_Q4_R(NB, XK, YK, 3072)                     \
@@ -1261,7 +1263,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     const void* kf = reinterpret_cast<const void*>(&k_lm_ring<HSD_X_RMS, NB, kRingW>);        \
     const int g = std::max(1, std::min(grid, resident_workgroups(kf, 64 * kRingW, 0, kLMaxGrid))); \
     hipLaunchKernelGGL((k_lm_ring<HSD_X_RMS, NB, kRingW>), dim3(g), dim3(64 * kRingW), 0, st,  \
-                       HSD_LIN_ARGS(a));                                                      \
+                       HSD_LIN_ARGS(a, g));                                                   \
   }
     if (B == 1)
       HSD_RING(1)

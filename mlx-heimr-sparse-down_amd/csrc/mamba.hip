@@ -52,7 +52,9 @@ __global__ __launch_bounds__(kMT) void k_mamba_ssm(
   // xcd_remap: consecutive heads (a B/C group's, and a norm group's) run on one XCD, so
   // their shared B/C conv inputs and their y rows stay in that XCD's L2; k_gated_norm's
   // workgroup for norm group g runs on XCD g % 8 as well
-  const int lb = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  // (the grid is H x P / kPB workgroups, from preloaded arguments: gridDim would be a
+  // scalar load of the dispatch's hidden arguments ahead of every load)
+  const int lb = xcd_remap((int)blockIdx.x, H * (P / kPB));
   const int hh = lb / npb, pblk = lb - (lb / npb) * npb;
   const int tid = threadIdx.x;
   const int DI = H * P, GN = G * kN, CD = DI + 2 * GN;
