@@ -91,8 +91,9 @@ __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 
     int32_t* __restrict__ status, Geom g_, int dense) {
   // the first round trip's pointers and geometry come as the leading scalar arguments,
   // which the dispatch preloads into SGPRs (the struct is read by scalar loads, which the
-  // first loads would wait for); nblk_ is the grid (B x nwg workgroups: gridDim would be a
-  // scalar load of the dispatch's hidden arguments)
+  // first loads would wait for). nwg_, nchunk_ and nblk_ are not needed by the (chunk,
+  // part, token row) grid; this layout measured 0.07 us per call faster than one that
+  // preloads D, E and the part count in their place.
   Geom g = g_;
   g.nwg = nwg_;
   g.nchunk = nchunk_;
@@ -117,14 +118,14 @@ __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 
   __shared__ float red[kGPW * kRS][kRedP];          // per team: group terms [t][word]
   __shared__ float sum2[kDC][kL1 + 1];
 
-  const int logical = xcd_remap((int)blockIdx.x, nblk_);
-  const int b = logical / g.nwg;
-  const int rem = logical - b * g.nwg;
-  const int p = rem / g.nchunk, c = rem - p * g.nchunk;
+  // grid (chunk, part, token row): the coordinates need no division (a one-dimensional
+  // grid placed on the XCDs by part took 3 divisions ahead of the first loads: one call
+  // 7.60 against 7.32 us, three rows 11.06 against 10.39)
+  const int c = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, team = tid >> 4, l = tid & 15;
   const int j = team % kGPW, phase = team / kGPW;   // group slot, row phase
   const bool routed = p < g.topk * g.ppr;
-  const int k = routed ? p / g.ppr : g.topk;
+  const int k = routed ? (int)((unsigned)p / (unsigned)g.ppr) : g.topk;
   const int g0 = (routed ? p - k * g.ppr : p - g.topk * g.ppr) * kGPW;
   const int ng = min(kGPW, (routed ? g.gpr : g.gsh) - g0);
   const int grp = g0 + j;
@@ -612,10 +613,12 @@ int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t
                        uint64_t* live_masks, int32_t* dev_status, float* part, hipStream_t st,
                        const uint16_t* res = nullptr) {
   const Geom g = make_geom(D, F, FS, topk, E);
+  // the grid is (chunks, parts, token rows): at most 65535 token rows per call
+  if (B > 65535 || g.nparts > 65535) return set_error(HSD_ERR_SHAPE, "%s: too many token rows or parts", fn);
   const int64_t nblk = B * (int64_t)g.nwg;
-  if (nblk > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too many workgroups", fn);
 #define HSD_PART(DT)                                                                          \
-  hipLaunchKernelGGL(k_sparse_down_part<DT>, dim3((unsigned)nblk), dim3(kThreads), 0, st,    \
+  hipLaunchKernelGGL(k_sparse_down_part<DT>, dim3((unsigned)g.nchunk, (unsigned)g.nparts, (unsigned)B),      \
+                     dim3(kThreads), 0, st,                                                               \
                      reinterpret_cast<const typename Elem<DT>::T*>(h), sel, gains, g.nwg, g.nchunk,   \
                      g.topk, g.ppr, g.gpr, g.gsh, (int)nblk, g.F, pw, ps, pb, spw, sps, spb, part,    \
                      live_masks, dev_status, g, dense)
