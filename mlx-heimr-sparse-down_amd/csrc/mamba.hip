@@ -33,16 +33,16 @@ constexpr int kN = 128;      // state size (16 lanes per state row, 8 elements e
 constexpr int kK = 4;        // conv kernel
 constexpr int kLMax = 7;     // rows per verify (nslab <= 8)
 
-// The shape, the ring index and the conv inputs and weights lead the arguments: the
-// dispatch preloads leading scalar arguments into SGPRs, so the first round trip's loads
-// need no scalar load of the argument segment before they issue.
+// The shape (L | G << 16, H | P << 16), the ring index, the conv inputs and weights and dt
+// lead the arguments: the dispatch preloads leading scalar arguments into SGPRs, so the
+// first round trip's loads need no scalar load of the argument segment before they issue.
 __global__ __launch_bounds__(kMT) void k_mamba_ssm(
-    int L, int H, int P, int G, const int32_t* __restrict__ cur_ptr, const uint16_t* __restrict__ conv_in,
-    int64_t cin_ld, const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ conv_b,
-    const uint16_t* __restrict__ dt_raw, int64_t dt_ld, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, const float* __restrict__ Dp, float* __restrict__ ssm,
-    uint16_t* __restrict__ convs, int nslab, float* __restrict__ y_pre, int64_t y_ld,
+    int LG, int HP, int cin_ld, const int32_t* __restrict__ cur_ptr, const uint16_t* __restrict__ conv_in,
+    const uint16_t* __restrict__ conv_w, const uint16_t* __restrict__ conv_b, const uint16_t* __restrict__ dt_raw,
+    int64_t dt_ld, const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* __restrict__ Dp,
+    float* __restrict__ ssm, uint16_t* __restrict__ convs, int nslab, float* __restrict__ y_pre, int64_t y_ld,
     const uint16_t* __restrict__ gate, int64_t gate_ld, float dt_lo, float dt_hi, int32_t* __restrict__ status) {
+  const int L = LG & 0xFFFF, G = LG >> 16, H = HP & 0xFFFF, P = HP >> 16;
   __shared__ float xs[kLMax][kPB];
   __shared__ float zsq[kLMax][kPB];
   __shared__ __attribute__((aligned(16))) float Bs[kLMax][kN];
@@ -392,10 +392,12 @@ extern "C" int hsd_mamba_verify(const uint16_t* conv_in, int64_t conv_in_ld,
     return set_error(HSD_ERR_WORKSPACE, "%s: workspace needs %zu bytes", fn, need);
   hipStream_t st = as_stream(stream);
   float* y_pre = reinterpret_cast<float*>(workspace);
-  hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, st, (int)L, (int)H, (int)P,
-                     (int)G, cur, conv_in, conv_in_ld, conv_w, conv_b, dt_raw, dt_ld, A_log, dt_bias, Dp,
-                     ssm_slabs, conv_slabs, (int)nslab, y_pre, (int64_t)DI, nullptr, (int64_t)0, dt_lo, dt_hi,
-                     dev_status);
+  if (conv_in_ld > 0x7FFFFFFF || H > 0xFFFF || P > 0xFFFF || G > 0xFFFF)
+    return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, st, (int)(L | (G << 16)),
+                     (int)(H | (P << 16)), (int)conv_in_ld, cur, conv_in, conv_w, conv_b, dt_raw, dt_ld, A_log,
+                     dt_bias, Dp, ssm_slabs, conv_slabs, (int)nslab, y_pre, (int64_t)DI, nullptr, (int64_t)0, dt_lo,
+                     dt_hi, dev_status);
   int rc = check_launch(fn);
   if (rc) return rc;
   const unsigned ngrid = (unsigned)(L * (DI / norm_group));
@@ -454,10 +456,12 @@ int launch_ssm(const char* fn, const uint16_t* conv_in, int64_t conv_in_ld, cons
   if (y_ld < (gate ? DI + DI / kPB : DI) || (gate && gate_ld < DI))
     return set_error(HSD_ERR_SHAPE, "%s: row strides smaller than the rows", fn);
   if ((uintptr_t)ssm_slabs & 15u) return set_error(HSD_ERR_ALIGN, "%s: ssm_slabs must be 16-byte aligned", fn);
-  if (H * (P / kPB) > 0x7FFFFFFF) return set_error(HSD_ERR_SHAPE, "%s: too large", fn);
-  hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, as_stream(stream), (int)L,
-                     (int)H, (int)P, (int)G, cur, conv_in, conv_in_ld, conv_w, conv_b, dt_raw, dt_ld, A_log, dt_bias,
-                     Dp, ssm_slabs, conv_slabs, (int)nslab, y, y_ld, gate, gate_ld, dt_lo, dt_hi, dev_status);
+  if (conv_in_ld > 0x7FFFFFFF || H > 0xFFFF || P > 0xFFFF || G > 0xFFFF)
+    return set_error(HSD_ERR_SHAPE, "%s: sizes too large", fn);
+  hipLaunchKernelGGL(k_mamba_ssm, dim3((unsigned)(H * (P / kPB))), dim3(kMT), 0, as_stream(stream),
+                     (int)(L | (G << 16)), (int)(H | (P << 16)), (int)conv_in_ld, cur, conv_in, conv_w, conv_b,
+                     dt_raw, dt_ld, A_log, dt_bias, Dp, ssm_slabs, conv_slabs, (int)nslab, y, y_ld, gate, gate_ld,
+                     dt_lo, dt_hi, dev_status);
   return check_launch(fn);
 }
 }  // namespace
