@@ -445,8 +445,11 @@ class NemotronModel:
                     # MTP head
                     pair=e(B, 2 * c.hidden), emb=e(B, c.hidden), hx=e(B, c.hidden), hn=e(B, c.hidden),
                     pend=e(4, dt=torch.int32), d1=e(4, dt=torch.int32), keys2=e(1, self.slots, dt=torch.int64),
-                    h2=e(1, c.hidden), x1=e(1, c.hidden), hn1=e(1, c.hidden),
-                    keys1=e(1, self.slots, dt=torch.int64))
+                    h2=e(1, c.hidden), hn1=e(1, c.hidden),
+                    keys1=e(1, self.slots, dt=torch.int64),
+                    # the head's residual rows and attention output side by side, so one
+                    # row selection takes both
+                    hcomb=e(B, c.hidden + c.attn_heads * c.head_dim))
 
     def moe_blocks(self):
         out = [b for t, b in zip(self.cfg.pattern, self.blocks) if t == "E"]
@@ -540,17 +543,36 @@ class NemotronModel:
         return out
 
     # ---- the MTP head forward (mtp.py:74-88)
-    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None, status=None, chain=None):
+    def mtp_rows(self, h, toks, buf, kv: nn.KVCache, pos, keys=None, status=None, chain=None, select=None):
         """Head rows: h [B, D] (the target's pre-norm hidden), toks [B] int32 (the token
         after each row's position) at positions pos .. pos+B-1 of the head's KV cache kv.
         Leaves the normed hidden rows in buf["hn"] and (with keys) the argmax keys of the
         head's logits. chain = (keys, seq, d1): the chained call, its token the argmax of
-        those keys and h the selected row's normed hidden row (nn.head_input)."""
+        those keys and h the selected row's normed hidden row (nn.head_input).
+        select = (seq, buf1): only row R - 1 (R from seq) goes on past the attention: every
+        row enters the head's KV cache, but only that row's prediction is a draft
+        (model.py:408-411), so o_proj and the MoE block run on it alone (buf1's one-row
+        buffers) and the row [1, D] is returned."""
         B = h.shape[0]
         hd, c = self.mtp, self.cfg
         # the token embedding and the pair norm in one launch
         pair = nn.head_input(toks, h, self.embedding, hd.enorm, hd.hnorm, eps=c.eps, out=buf["pair"][:B],
                              status=status, chain=chain)
+        if select is not None:
+            seq, b1 = select
+            D, a = c.hidden, hd.attn
+            comb = buf["hcomb"][:B]
+            x = nn.linear(pair, hd.eh_proj, out=comb[:, :D])
+            qkv = nn.linear(x, a.qkv, norm=a.norm_w, eps=c.eps, out=buf["qkv"][:B])
+            nn.attention(qkv, kv, pos, n_heads=c.attn_heads, n_kv_heads=c.kv_heads, head_dim=c.head_dim,
+                         out=comb[:, D:], workspace=buf["ws_attn"], status=status)
+            one = b1["hcomb"]
+            N.call("hsd_seq_select_row", N.ptr(comb), comb.stride(0), N.ptr(seq), N.ptr(one), comb.shape[1],
+                   N.stream(self.device))
+            x1 = one[:, :D]
+            nn.linear(one[:, D:], a.o_proj, residual=x1, out=x1)
+            hd.moe.rows(x1, b1, dense=self.mode == "dense", status=status)
+            return x1
         x = nn.linear(pair, hd.eh_proj, out=buf["hx"][:B])
         hd.attn.rows(x, buf, kv, pos, status=status)
         hd.moe.rows(x, buf, dense=self.mode == "dense", status=status)
@@ -693,9 +715,9 @@ class NemotronModel:
         st = N.stream(self.device)
         # the head over the rows the last verify confirmed (R of them valid); only row R-1's
         # prediction is a draft (model.py:408-411), so lm_head runs on that row alone
-        x3 = self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos, status=cache.status)
-        N.call("hsd_seq_select_row", N.ptr(x3), x3.stride(0), N.ptr(cache.seq), N.ptr(b1["x1"]), c.hidden, st)
-        nn.linear(b1["x1"], self.lm_head, norm=self.mtp.final_norm, eps=c.eps, argmax_keys=b1["keys1"],
+        x1 = self.mtp_rows(b3["x"], b3["pend"][:3], b3, cache.head_kv, cache.head_pos, status=cache.status,
+                           select=(cache.seq, b1))
+        nn.linear(x1, self.lm_head, norm=self.mtp.final_norm, eps=c.eps, argmax_keys=b1["keys1"],
                   xn_out=b1["hn1"])
         # the chained call on its own normed hidden row (mtp.py, model.py:411-413); its input
         # launch also takes the first draft from keys1 (d1) and the cache row (HEAD_POS2)
