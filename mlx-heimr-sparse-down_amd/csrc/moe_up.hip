@@ -99,13 +99,31 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
                                                 int (&e_out)[kMaxTopk], float (&g_out)[kMaxTopk]) {
   uint64_t key[4];
   float sg[4];
+  // every logit and bias load first, in one round trip: none under a branch (without a
+  // bias the loads read the logits' first word and the value is dropped), and the values
+  // pinned to registers after the last load is issued, so the compiler cannot sink a load
+  // into the branch that uses it (a load under a branch ends in a wait for every load
+  // where the paths merge: one round trip per key)
+  uint32_t lg[4], bv[4];
+  const bool has_bias = rt.bias != nullptr;
+  const float* bp = has_bias ? rt.bias : reinterpret_cast<const float*>(rt.logits);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ec = min(lane + 64 * i, E - 1);
+    lg[i] = rt.logits[(size_t)b * E + ec];
+    bv[i] = __float_as_uint(bp[has_bias ? ec : 0]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lg[i] = opaque_vgpr(lg[i]);
+    bv[i] = opaque_vgpr(bv[i]);
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    const int ec = min(e, E - 1);
-    const float x = bf16_bits_to_f32(rt.logits[(size_t)b * E + ec]);
+    const float x = bf16_bits_to_f32(lg[i]);
     const float s = 1.0f / (1.0f + expf(-x));
-    float c = s + (rt.bias ? rt.bias[ec] : 0.0f);
+    float c = s + (has_bias ? __uint_as_float(bv[i]) : 0.0f);
     c = c != c ? -INFINITY : c;
     key[i] = e < E ? ((uint64_t)ordered_bits(c) << 32) | (uint32_t)~(uint32_t)e : 0;
     sg[i] = s;
