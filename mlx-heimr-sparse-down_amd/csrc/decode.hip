@@ -298,25 +298,34 @@ constexpr int kSumThreads = 64;          // one wavefront per workgroup: 42 at D
 template <int YDT, int NP>
 __global__ __launch_bounds__(kSumThreads) void k_sum_parts(const float* __restrict__ part,
                                                    typename Elem<YDT>::T* __restrict__ y, int D,
-                                                   int nparts, int n, const uint16_t* __restrict__ res) {
-  const int idx = blockIdx.x * kSumThreads + threadIdx.x;
-  if (idx >= n) return;
-  const int b = idx / D, o = idx - b * D;
+                                                   int nparts, const uint16_t* __restrict__ res) {
+  // grid (output columns / 64, token rows): no division for the coordinates
+  const int b = blockIdx.y, o = blockIdx.x * kSumThreads + threadIdx.x;
+  if (o >= D) return;
+  const int idx = b * D + o;
   const float* pp = part + (size_t)b * nparts * D + o;
+  // the residual (bf16 output) is loaded with the parts, not after their sum (a load used
+  // only under a branch is issued there, one more round trip): without a residual the load
+  // reads the parts' first word and the value is dropped
+  constexpr bool kRes = YDT == HSD_DT_BF16;
+  const bool has_res = kRes && res != nullptr;
+  const uint16_t* rp = has_res ? res : reinterpret_cast<const uint16_t*>(part);
+  uint32_t rv = kRes ? rp[has_res ? idx : 0] : 0u;
   float s;
   if (NP > 0) {
     float v[NP > 0 ? NP : 1];
 #pragma unroll
     for (int q = 0; q < NP; ++q) v[q] = pp[(size_t)q * D];
+    if constexpr (kRes) rv = opaque_vgpr(rv);
     s = v[0];
 #pragma unroll
     for (int q = 1; q < NP; ++q) s += v[q];
   } else {
     s = pp[0];
+    if constexpr (kRes) rv = opaque_vgpr(rv);
     for (int q = 1; q < nparts; ++q) s += pp[(size_t)q * D];
   }
-  if (YDT == HSD_DT_BF16 && res)
-    s = bf16_bits_to_f32(res[idx]) + bf16_bits_to_f32(f32_to_bf16_bits(s));
+  if (has_res) s = bf16_bits_to_f32(rv) + bf16_bits_to_f32(f32_to_bf16_bits(s));
   Elem<YDT>::store(y, idx, s);
 }
 
@@ -631,15 +640,14 @@ int launch_sparse_down(const char* fn, const void* h, int h_dtype, const int32_t
 #undef HSD_PART
   int rc = check_launch(fn);
   if (rc) return rc;
-  const int n = (int)(B * D);
-  const dim3 rgrid((unsigned)((n + kSumThreads - 1) / kSumThreads));
+  const dim3 rgrid((unsigned)((D + kSumThreads - 1) / kSumThreads), (unsigned)B);
 #define HSD_SUM(DT)                                                                                  \
   if (g.nparts == 32)                                                                                \
     hipLaunchKernelGGL((k_sum_parts<DT, 32>), rgrid, dim3(kSumThreads), 0, st, part,                         \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n, res);       \
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, res);          \
   else                                                                                               \
     hipLaunchKernelGGL((k_sum_parts<DT, 0>), rgrid, dim3(kSumThreads), 0, st, part,                          \
-                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, n, res);
+                       reinterpret_cast<typename Elem<DT>::T*>(y), (int)D, g.nparts, res);
   switch (y_dtype) {
     case HSD_DT_BF16: HSD_SUM(HSD_DT_BF16); break;
     case HSD_DT_F16: HSD_SUM(HSD_DT_F16); break;

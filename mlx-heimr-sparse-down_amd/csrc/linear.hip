@@ -415,16 +415,51 @@ void k_linear(HSD_LIN_PARAMS) {
     }
   };
 
+  // ---- the output slot of this lane in a block's epilogue: token row ob, row orr of the
+  // wavefront's rows (lane_out: the lane writes one)
+  auto out_slot = [&](int& ob, int& orr, bool& lane_out) {
+    if constexpr (Q4) {
+      ob = jl / kRH;
+      orr = kRH * hw + jl % kRH;
+      lane_out = jl < kRH * NB;
+    } else {
+      ob = lane / kRW;
+      orr = lane - ob * kRW;
+      lane_out = lane < NB * kRW;
+    }
+  };
+  // the residual of the lane's output in block blk_ (HSD_Y_RESID), loaded ahead of the
+  // block's weights rather than in the epilogue, where it was one more round trip at the
+  // end of every block (slots the lane does not write re-read a valid element)
+  auto load_res = [&](int blk_) -> uint32_t {
+    if constexpr (YK == HSD_Y_RESID) {
+      int ob, orr;
+      bool lane_out;
+      out_slot(ob, orr, lane_out);
+      const int o = min(blk_ * kRows + kRW * wave + orr, O - 1);
+      return a.res[min(ob, NB - 1) * a.res_ld + o];
+    } else {
+      return 0u;
+    }
+  };
+
   // ---- prologue: this workgroup's copy of the NB input rows, normalised if asked
   XIn<WF, NB, XK, XIT, PX> xin;
   xin.load(a, tid);
-  // the first block's weight pieces, issued after x: the prologue waits for x only (loads
-  // complete in issue order), while the weights are still on their way
+  // the residual and the first block's weight pieces, issued after x: the prologue waits
+  // for x only (loads complete in issue order), while the weights are still on their way
   Blk cur;
   int blk = blockIdx.x;
+  uint32_t resv = load_res(blk);
   load_block(blk, cur);
+  // every load above is issued before the prologue's arithmetic: the scheduler had moved
+  // the gated norm's partial sums (which wait for their loads) ahead of the weight loads
+  __builtin_amdgcn_sched_barrier(0);
   xin.template finish<32>(a, xp, xh, wsum, tid, lane, wave);
   lds_barrier();                                       // x in LDS; the weights may still be in flight
+  // the residual in a register here (its load was issued before the weights', so this
+  // waits for it alone): the compiler cannot move the load into the epilogue's branch
+  if constexpr (YK == HSD_Y_RESID) resv = opaque_vgpr(resv);
 
   // bf16: one 16-byte piece j of a row against the token rows: the partial of each token row
   auto piece_terms = [&](int j, const uint4& qv, float (&t)[NB]) {
@@ -444,7 +479,7 @@ void k_linear(HSD_LIN_PARAMS) {
   uint64_t best[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
-  auto do_block = [&](int blk_, const Blk& bk) {
+  auto do_block = [&](int blk_, const Blk& bk, uint32_t resv_) {
     float outv = 0.0f;
     int ob, orr;
     bool lane_out;
@@ -516,9 +551,6 @@ void k_linear(HSD_LIN_PARAMS) {
           outv = jl == kRH * b + i ? u : outv;
         }
       }
-      ob = jl / kRH;
-      orr = kRH * hw + jl % kRH;
-      lane_out = jl < kRH * NB;
     } else {
       float pr[NB][kRW];
 #pragma unroll
@@ -577,10 +609,8 @@ void k_linear(HSD_LIN_PARAMS) {
           outv = lane == b * kRW + r ? u : outv;
         }
       }
-      ob = lane / kRW;
-      orr = lane - ob * kRW;
-      lane_out = lane < NB * kRW;
     }
+    out_slot(ob, orr, lane_out);
     const int o = blk_ * kRows + kRW * wave + orr;
     const bool live = lane_out && o < O;
     if constexpr (YK == HSD_Y_ARGMAX) {
@@ -604,7 +634,7 @@ void k_linear(HSD_LIN_PARAMS) {
       if constexpr (YK == HSD_Y_F32) {
         reinterpret_cast<float*>(a.y)[yi] = outv;
       } else if constexpr (YK == HSD_Y_RESID) {
-        const float rv = bf16_bits_to_f32(a.res[ob * a.res_ld + o]);
+        const float rv = bf16_bits_to_f32(resv_);
         reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(rv + rne_bf16(outv));
       } else {
         reinterpret_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_bits(outv);
@@ -613,17 +643,19 @@ void k_linear(HSD_LIN_PARAMS) {
   };
 
   if ((int)gridDim.x >= nblk) {
-    do_block(blk, cur);                                // one block per workgroup
+    do_block(blk, cur, resv);                          // one block per workgroup
   } else if constexpr (Q4) {
     // several blocks, one after the other: a second block's registers in flight would
     // cost the occupancy that makes every projection of the model one block per workgroup
     // (in_proj: 644 blocks, 768 resident workgroups)
     for (;;) {
-      do_block(blk, cur);
+      do_block(blk, cur, resv);
       blk += (int)gridDim.x;
       if (blk >= nblk) break;
       __builtin_amdgcn_sched_barrier(0);
+      resv = load_res(blk);
       load_block(blk, cur);
+      if constexpr (YK == HSD_Y_RESID) resv = opaque_vgpr(resv);
     }
   } else {
     // several blocks: the next block's pieces are in flight while one is computed; the
@@ -632,11 +664,14 @@ void k_linear(HSD_LIN_PARAMS) {
     for (;;) {
       const int nxt = blk + (int)gridDim.x;
       Blk nx;
+      uint32_t resn = load_res(nxt < nblk ? nxt : blk);
       load_block(nxt < nblk ? nxt : blk, nx);
-      do_block(blk, cur);
+      if constexpr (YK == HSD_Y_RESID) resn = opaque_vgpr(resn);
+      do_block(blk, cur, resv);
       if (nxt >= nblk) break;
       blk = nxt;
       cur = nx;
+      resv = resn;
     }
   }
   if constexpr (YK == HSD_Y_ARGMAX) {
