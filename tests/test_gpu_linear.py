@@ -194,6 +194,27 @@ def test_residual_epilogue(dev):
         assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
 
 
+def test_residual_epilogue_many_blocks(dev):
+    """More 16-row blocks than resident workgroups (a workgroup runs several blocks in
+    turn), so each block's residual is loaded with that block's weights: equal to the bf16
+    output plus the residual, and every row of the three-row call to that row alone. (The
+    residual epilogue takes 4-bit weights only.)"""
+    I, O_ = 2688, 20480
+    rng = np.random.default_rng(43)
+    _, W = q4_weight(44, O_, I, dev)
+    x, xd = bf16_rows(rng, 3, I, dev)
+    res = S.to_device(O.f32_to_bf16(rng.standard_normal((3, O_)).astype(np.float32) * 4), dev)
+    y = nn.linear(xd, W)
+    out = res.clone()
+    nn.linear(xd, W, residual=out, out=out)
+    want = (res.float() + y.float()).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    for r in range(3):
+        o1 = res[r:r + 1].clone()
+        nn.linear(xd[r:r + 1], W, residual=o1, out=o1)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
+
+
 def test_gated_norm_prologue(dev):
     I, O_ = 4096, 2688
     (w, s, b), W = q4_weight(51, O_, I, dev)
