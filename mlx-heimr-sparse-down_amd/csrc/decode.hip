@@ -23,7 +23,7 @@
 //   * k_sum_parts: y[b, o] = sum over the 32 parts in part order.
 // Eight groups per workgroup measured fastest: 16 (512 threads) and 32 (1024) were 4 % and
 // 6 % slower per call, 4 (128 threads, 63 parts) 6 % slower.
-// k_sum_parts runs one wavefront per workgroup (42 at D = 2688): 2.5 % faster per call than
+// k_sum_parts runs one wavefront per workgroup (42 per token row at D = 2688): 2.5 % faster per call than
 // 256-thread workgroups (11).
 // Two row phases per group: one phase (128-thread workgroups) was 0.9 % faster at 90 % zeros
 // but needs a second batch of row loads once a group has more than 16 live rows (denser
@@ -291,7 +291,7 @@ __attribute__((amdgpu_waves_per_eu(HDT == HSD_DT_F32 ? 7 : 8, HDT == HSD_DT_F32 
   if (!ok && tid == 0 && c == 0 && status) atomicOr(status, (int32_t)HSD_STATUS_BAD_EXPERT);
 }
 
-constexpr int kSumThreads = 64;          // one wavefront per workgroup: 42 at D = 2688
+constexpr int kSumThreads = 64;          // one wavefront per workgroup: 42 per token row at D = 2688
 
 // y = the parts summed in part order; with res (bf16 y only): y = bf16(res + bf16(sum)),
 // the MoE block's residual add (model.py:139).
