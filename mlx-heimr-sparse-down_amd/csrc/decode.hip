@@ -23,8 +23,8 @@
 //   * k_sum_parts: y[b, o] = sum over the 32 parts in part order.
 // Eight groups per workgroup measured fastest: 16 (512 threads) and 32 (1024) were 4 % and
 // 6 % slower per call, 4 (128 threads, 63 parts) 6 % slower.
-// k_sum_parts runs one wavefront per workgroup (42 per token row at D = 2688): 2.5 % faster per call than
-// 256-thread workgroups (11).
+// k_sum_parts runs one wavefront per workgroup (42 per token row at D = 2688): 2.5 %
+// faster per call than 256-thread workgroups (11).
 // Two row phases per group: one phase (128-thread workgroups) was 0.9 % faster at 90 % zeros
 // but needs a second batch of row loads once a group has more than 16 live rows (denser
 // activations, the dense-h control); four phases were 17 % slower.
