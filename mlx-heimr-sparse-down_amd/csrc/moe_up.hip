@@ -100,13 +100,14 @@ __device__ __forceinline__ void route_topk_wave(const Router& rt, int b, int E, 
   uint64_t key[4];
   float sg[4];
   // every logit and bias load first, in one round trip: none under a branch (without a
-  // bias the loads read the logits' first word and the value is dropped), and the values
-  // pinned to registers after the last load is issued, so the compiler cannot sink a load
-  // into the branch that uses it (a load under a branch ends in a wait for every load
-  // where the paths merge: one round trip per key)
+  // bias the loads read the 4-byte word holding the logits' first element, and the value
+  // is dropped), and the values pinned to registers after the last load is issued, so the
+  // compiler cannot sink a load into the branch that uses it (a load under a branch ends
+  // in a wait for every load where the paths merge: one round trip per key)
   uint32_t lg[4], bv[4];
   const bool has_bias = rt.bias != nullptr;
-  const float* bp = has_bias ? rt.bias : reinterpret_cast<const float*>(rt.logits);
+  const float* bp = has_bias ? rt.bias
+                             : reinterpret_cast<const float*>(reinterpret_cast<uintptr_t>(rt.logits) & ~uintptr_t(3));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ec = min(lane + 64 * i, E - 1);

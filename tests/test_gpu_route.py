@@ -62,6 +62,34 @@ def test_router_topk_and_front_end(dev, up, B):
         assert torch.equal(s1, sel[1:2]) and torch.equal(g1.view(torch.int32), gains[1:2].view(torch.int32))
 
 
+def test_router_without_bias_at_an_odd_offset(dev, up):
+    """No selection bias (e_bias None: the kernels then load a word of the logits in its
+    place and drop it) and logits starting at an odd element (a 2-byte aligned view)."""
+    u, ud = up
+    B = 3
+    rng = np.random.default_rng(47)
+    x = O.f32_to_bf16(rng.standard_normal((B, D)).astype(np.float32))
+    logits = O.f32_to_bf16(rng.standard_normal((B, E)).astype(np.float32) * 2)
+    buf = torch.zeros(B * E + 1, dtype=torch.bfloat16, device=dev)
+    buf[1:] = S.to_device(logits, dev).reshape(-1)
+    lv = buf[1:].view(B, E)
+    assert lv.data_ptr() % 4 == 2
+    hcat, sel, gains = moe.route_up_relu2(S.to_device(x, dev), lv, None, ud["w1"], ud["s1"], ud["b1"], ud["sw1"],
+                                          ud["ss1"], ud["sb1"], topk=K, routed_scale=2.5, norm_topk=True)
+    rsel, rg = O.router_topk(O.bf16_to_f32(logits), np.zeros(E, np.float32), K, scale=2.5)
+    sel_h, g_h = sel.cpu().numpy(), gains.cpu().numpy()
+    ch = O.sigmoid_f32(O.bf16_to_f32(logits))
+    for r in range(B):
+        srt = np.sort(ch[r])[::-1]
+        if srt[K - 1] - srt[K] < 1e-6:
+            print(f"row {r}: near tie at the k-th choice, skipped")
+            continue
+        assert sel_h[r].tolist() == rsel[r].tolist()
+        assert np.allclose(g_h[r, :K], rg[r], rtol=1e-6, atol=0)
+    s2, g2 = moe.router_topk(lv, None, topk=K, routed_scale=2.5)
+    assert torch.equal(s2, sel) and torch.equal(g2.view(torch.int32), gains.view(torch.int32))
+
+
 def test_ssm_only_entry(dev):
     p = S.mamba_params_np(9)
     mk = lambda: M.Mamba2Mixer(conv_w=S.to_device(p["conv_w"], dev), conv_b=S.to_device(p["conv_b"], dev),
