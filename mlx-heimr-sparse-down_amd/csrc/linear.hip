@@ -51,6 +51,7 @@ constexpr int kLMaxB = 4;                // token rows per launch
 constexpr int kLMaxI = 6144;             // inputs per row
 constexpr int kLSmallQ4 = 4096;          // 4-bit rows up to this length: 2 pieces per lane
 constexpr int kLMaxGrid = 2048;
+constexpr int kRowsMaxO = 512;           // bf16 rows with the RMS prologue up to this: k_linear_rows
 constexpr uint32_t kBfOne2 = 0x3F803F80u;
 constexpr uint32_t kNibHi = 0x00780078u;
 
@@ -690,6 +691,67 @@ void k_linear(HSD_LIN_PARAMS) {
   }
 }
 
+// bf16 weights with few output rows (the MoE router gate: 128 rows of 2688 inputs) and the
+// RMS prologue: one workgroup per output row, the row's 16-byte pieces split over the four
+// wavefronts (wavefront w takes the w-th quarter, lane l its pieces l and l + 64), each
+// wavefront's 64-lane sum per token row to LDS, the four added in wavefront order. The
+// workgroup-per-four-rows form of k_linear left most CUs idle (32 workgroups) with a whole
+// row per wavefront; here the prologue is the same and the dot products a quarter as long.
+template <int NB, int IMAX>
+__global__ __launch_bounds__(kLT) void k_linear_rows(HSD_LIN_PARAMS) {
+  HSD_LIN_UNPACK;
+  constexpr int XIT = (IMAX / 8 + kLT - 1) / kLT;
+  constexpr int kP = (IMAX / 8 / 4 + 63) / 64;         // passes per wavefront (max)
+  extern __shared__ __attribute__((aligned(16))) uint32_t lsm[];  // x as bf16 pairs [NB][I/2]
+  __shared__ float wsum[NB][4];
+  __shared__ float red[4][NB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int I = a.I, NPr = I / 8;                      // 16-byte pieces per row
+  const int o = blockIdx.x;                            // the grid is the row count
+  XIn<HSD_W_BF16, NB, HSD_X_RMS, XIT, 1> xin;
+  xin.load(a, tid);
+  // the wavefront's quarter of the row: pieces q0 .. q1 - 1 (past q1: re-read, unused)
+  const int per = (NPr + 3) / 4, q0 = wave * per, q1 = min(q0 + per, NPr);
+  const uint4* wr = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.w) + (size_t)o * I);
+  uint4 qv[kP];
+#pragma unroll
+  for (int p = 0; p < kP; ++p) qv[p] = wr[min(q0 + lane + 64 * p, NPr - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  xin.template finish<32>(a, lsm, nullptr, wsum, tid, lane, wave);
+  lds_barrier();
+  float pr[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) pr[b] = 0.0f;
+  const int npass = (per + 63) / 64;
+#pragma unroll
+  for (int p = 0; p < kP; ++p) {
+    if (p < npass) {                                   // uniform
+      const int j = q0 + lane + 64 * p;
+      const bool use = j < q1;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint4 xq = *reinterpret_cast<const uint4*>(&lsm[b * (I / 2) + 4 * min(j, NPr - 1)]);
+        float acc = 0.0f;
+        acc = dot2_bf16(xq.x, qv[p].x, acc);
+        acc = dot2_bf16(xq.y, qv[p].y, acc);
+        acc = dot2_bf16(xq.z, qv[p].z, acc);
+        acc = dot2_bf16(xq.w, qv[p].w, acc);
+        pr[b] += use ? acc : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float v = wave_sum_dpp(pr[b]);
+    if (lane == 0) red[wave][b] = v;
+  }
+  lds_barrier();
+  if (tid < NB) {
+    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    reinterpret_cast<uint16_t*>(a.y)[tid * a.y_ld + o] = f32_to_bf16_bits(v);
+  }
+}
+
 // 4-bit weights on the matrix cores, for projections with more 16-row blocks than
 // resident workgroups (lm_head: 8192), where the per-token-row dot products of the kernel
 // above bound the time at several token rows. A workgroup (4 wavefronts) loops over blocks
@@ -1314,6 +1376,17 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
     }
   } else if (w_kind == HSD_W_Q4) {
     HSD_LIN_B(HSD_W_Q4);
+  } else if (pair == kRB && O <= kRowsMaxO && I <= 3072) {
+    // few bf16 rows with the RMS prologue (the router gate): a workgroup per row
+#define HSD_ROWS(NB)                                                                              \
+  hipLaunchKernelGGL((k_linear_rows<NB, 3072>), dim3((unsigned)O), dim3(kLT), lds, st, HSD_LIN_ARGS(a, O));
+    switch (B) {
+      case 1: HSD_ROWS(1); break;
+      case 2: HSD_ROWS(2); break;
+      case 3: HSD_ROWS(3); break;
+      default: HSD_ROWS(4); break;
+    }
+#undef HSD_ROWS
   } else {
     HSD_LIN_B(HSD_W_BF16);
   }
