@@ -323,7 +323,9 @@ struct XIn {
 // blocks) want three workgroups per CU (8.5 against 9.1 us); the argmax instances (many
 // blocks per workgroup, the next block in flight: lm_head took 49 against 59 us here before
 // it moved to the matrix cores) are faster with the registers of two.
-template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM>
+// ROWSY: a one-row residual instance launched over (blocks, token rows), blockIdx.y the
+// token row (its own instance, so the one-row launches keep their code).
+template <int WF, int NB, int XK, int YK, int IMAX, int RW, bool REM, bool ROWSY = false>
 __global__ __launch_bounds__(kLT, WF == HSD_W_Q4 ? (IMAX == 3072 && NB < 4 ? 3 : 2) : (NB == 1 && YK != HSD_Y_ARGMAX) ? 3 : 2)
 void k_linear(HSD_LIN_PARAMS) {
   HSD_LIN_UNPACK;
@@ -416,6 +418,20 @@ void k_linear(HSD_LIN_PARAMS) {
     }
   };
 
+  // a one-row residual instance launched over several token rows (blockIdx.y = the token
+  // row: a three-row call of a projection with few blocks, whose x needs no gate and writes
+  // no normed copy): each y-slice is that row's one-row call, so the row's bits are those
+  // of the one-row and the three-row kernels. x moves here (its stride is a preloaded
+  // argument); the residual and the output take the row where they are used, so no wait for
+  // the other arguments moves ahead of the first loads
+  constexpr bool kRowsY = ROWSY;
+  static_assert(!ROWSY || (NB == 1 && YK == HSD_Y_RESID), "token rows over blockIdx.y: one-row residual instances");
+  const size_t yrow = kRowsY ? (size_t)blockIdx.y : 0;
+  if constexpr (kRowsY) {
+    constexpr size_t kXE = XIn<WF, NB, XK, XIT, PX>::kF32 ? 4 : 2;
+    a.x = reinterpret_cast<const char*>(a.x) + yrow * (size_t)x_ld_ * kXE;
+  }
+
   // ---- the output slot of this lane in a block's epilogue: token row ob, row orr of the
   // wavefront's rows (lane_out: the lane writes one)
   auto out_slot = [&](int& ob, int& orr, bool& lane_out) {
@@ -438,7 +454,7 @@ void k_linear(HSD_LIN_PARAMS) {
       bool lane_out;
       out_slot(ob, orr, lane_out);
       const int o = min(blk_ * kRows + kRW * wave + orr, O - 1);
-      return a.res[min(ob, NB - 1) * a.res_ld + o];
+      return a.res[(yrow + min(ob, NB - 1)) * a.res_ld + o];
     } else {
       return 0u;
     }
@@ -631,7 +647,7 @@ void k_linear(HSD_LIN_PARAMS) {
         best[b] = kb > best[b] ? kb : best[b];
       }
     } else if (live) {
-      const int64_t yi = ob * a.y_ld + o;
+      const int64_t yi = ((int64_t)yrow + ob) * a.y_ld + o;
       if constexpr (YK == HSD_Y_F32) {
         reinterpret_cast<float*>(a.y)[yi] = outv;
       } else if constexpr (YK == HSD_Y_RESID) {
@@ -1305,6 +1321,21 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
       HSD_LIN_R(WF, NB, XK, YK, IM, 1)                                \
     }                                                                 \
   }
+  // several token rows of a residual projection with few blocks (out_proj, o_proj: 168
+  // 16-row blocks): the one-row instance over (2-row wavefront blocks, token rows), three
+  // times the workgroups of the three-row instance, each doing a third of the arithmetic
+  const bool rows1 = w_kind == HSD_W_Q4 && !mfma && B > 1 && y_kind == HSD_Y_RESID && (O + 15) / 16 < 256 &&
+                     !xn_out;
+#define HSD_LIN_Y(XK, IM)                                                                             \
+  {                                                                                                   \
+    constexpr bool REM = IM != kLSmallQ4;                                                            \
+    const void* kf = reinterpret_cast<const void*>(&k_linear<HSD_W_Q4, 1, XK, HSD_Y_RESID, IM, 2, REM, true>); \
+    const size_t ldsx = (size_t)17 * (IM / 32) * 4;                                                   \
+    const int gr = std::min((int)((O + 7) / 8), kLMaxGrid);                                           \
+    const int g = std::max(1, std::min(gr, resident_workgroups(kf, kLT, ldsx, kLMaxGrid)));          \
+    hipLaunchKernelGGL((k_linear<HSD_W_Q4, 1, XK, HSD_Y_RESID, IM, 2, REM, true>), dim3(g, (unsigned)B), \
+                       dim3(kLT), ldsx, st, HSD_LIN_ARGS(a, g));                                      \
+  }
 #define HSD_LIN_I(WF, NB, XK, YK)                                       \
   if (isz == 0) HSD_LIN(WF, NB, XK, YK, 3072)                           \
   else if constexpr (WF == HSD_W_Q4) HSD_LIN(WF, NB, XK, YK, kLSmallQ4) \
@@ -1374,6 +1405,12 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
       case 3: HSD_Q4_P(3); break;
       default: HSD_Q4_P(4); break;
     }
+  } else if (rows1 && (pair == kZR || pair == kBR)) {
+    if (pair == kZR) {
+      if (isz == 0) HSD_LIN_Y(HSD_X_GATED_Z, 3072) else HSD_LIN_Y(HSD_X_GATED_Z, kLSmallQ4)
+    } else {
+      if (isz == 0) HSD_LIN_Y(HSD_X_BF16, 3072) else HSD_LIN_Y(HSD_X_BF16, kLSmallQ4)
+    }
   } else if (w_kind == HSD_W_Q4) {
     HSD_LIN_B(HSD_W_Q4);
   } else if (pair == kRB && O <= kRowsMaxO && I <= 3072) {
@@ -1398,6 +1435,7 @@ int launch_linear(const char* fn, const void* x, int64_t x_ld, int x_kind, const
 #undef HSD_LIN_I
 #undef HSD_LIN
 #undef HSD_LIN_R
+#undef HSD_LIN_Y
   return check_launch(fn);
 }
 
