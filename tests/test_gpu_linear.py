@@ -194,6 +194,26 @@ def test_residual_epilogue(dev):
         assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
 
 
+@pytest.mark.parametrize("B", [2, 4])
+def test_residual_epilogue_token_rows(dev, B):
+    """Two and four token rows of a residual projection with few blocks (the one-row kernel
+    over the token rows): each row equals that row alone, and the bf16 output plus the
+    residual."""
+    I, O_ = 4096, 2688
+    _, W = q4_weight(45, O_, I, dev)
+    rng = np.random.default_rng(46 + B)
+    x, xd = bf16_rows(rng, B, I, dev)
+    res = S.to_device(O.f32_to_bf16(rng.standard_normal((B, O_)).astype(np.float32) * 4), dev)
+    y = nn.linear(xd, W)
+    out = res.clone()
+    nn.linear(xd, W, residual=out, out=out)
+    assert torch.equal(out.view(torch.int16), (res.float() + y.float()).to(torch.bfloat16).view(torch.int16))
+    for r in range(B):
+        o1 = res[r:r + 1].clone()
+        nn.linear(xd[r:r + 1], W, residual=o1, out=o1)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), f"row {r}"
+
+
 def test_residual_epilogue_many_blocks(dev):
     """More 16-row blocks than resident workgroups (a workgroup runs several blocks in
     turn), so each block's residual is loaded with that block's weights: equal to the bf16
